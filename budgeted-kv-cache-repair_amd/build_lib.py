@@ -1,0 +1,78 @@
+"""Build libkvrepair.so (gfx950 HIP kernels + C ABI) in-tree with hipcc.
+
+The library links the HIP runtime by SONAME (libamdhip64.so.7). It must be
+loaded after ``import torch`` so that the dynamic linker binds it to the
+runtime torch already loaded, and both share streams and device memory.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_ROOT = Path(__file__).resolve().parent
+REPO_ROOT = PACKAGE_ROOT.parent
+CSRC = PACKAGE_ROOT / "csrc"
+INCLUDE = REPO_ROOT / "include"
+OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / "libkvrepair.so"
+SOURCES = ("kvr_common.hip", "kvr_rotate.hip", "kvr_scatter.hip", "kvr_attention.hip")
+ARCH = "gfx950"
+
+# Packed-FP32 instructions are disabled: hipcc still vectorises ordinary
+# float code into them otherwise.
+HIP_FLAGS = (
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-result",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+)
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    path = Path(rocm) / "bin" / "hipcc"
+    return str(path) if path.exists() else "hipcc"
+
+
+def build(verbose: bool = False, jobs: int = 4) -> Path:
+    """Compile every HIP source and link the shared library; returns its path."""
+    build_dir = PACKAGE_ROOT / "_build"
+    build_dir.mkdir(exist_ok=True)
+    objects, procs = [], []
+    for name in SOURCES:
+        obj = build_dir / (Path(name).stem + ".o")
+        cmd = [hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objects.append(obj)
+        while len([p for _, p in procs if p.poll() is None]) >= jobs:
+            procs[0][1].wait()
+    failed = []
+    for name, proc in procs:
+        out, _ = proc.communicate()
+        out = "\n".join(line for line in (out or "").splitlines() if "packed-fp32-ops" not in line)
+        if proc.returncode != 0:
+            failed.append((name, out))
+        elif verbose and out.strip():
+            print(out)
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(f"--- {n}\n{o}" for n, o in failed))
+    tmp = OUTPUT.with_suffix(".so.tmp")
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
+    if verbose:
+        print(" ".join(link), flush=True)
+    result = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if result.returncode != 0:
+        raise RuntimeError("hipcc link failed:\n" + result.stdout)
+    os.replace(tmp, OUTPUT)
+    return OUTPUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

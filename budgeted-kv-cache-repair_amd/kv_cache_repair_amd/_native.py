@@ -1,0 +1,108 @@
+"""ctypes binding of libkvrepair.so (the gfx950 HIP kernels behind include/kvrepair.h).
+
+The library is loaded lazily and only after ``import torch``: it links the HIP
+runtime by SONAME, so the dynamic linker binds it to the runtime instance
+torch already mapped and the two share streams and device memory. There is no
+fallback: a missing or stale library raises immediately.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libkvrepair.so"
+ABI_VERSION = 1
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+_vpp = ctypes.POINTER(ctypes.c_void_p)
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeError(RuntimeError):
+    """A kvrepair C entry point returned a negative status."""
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.kvr_abi_version.argtypes = []
+    lib.kvr_abi_version.restype = ctypes.c_int
+    lib.kvr_status_string.argtypes = [ctypes.c_int]
+    lib.kvr_status_string.restype = ctypes.c_char_p
+    lib.kvr_rope_delta_rotate.argtypes = [_vpp, _vpp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                                          ctypes.c_int32, ctypes.c_int32, _i64p, _i64p, ctypes.c_int64, _vp,
+                                          ctypes.c_float, ctypes.c_int32, _vp]
+    lib.kvr_rope_delta_rotate.restype = ctypes.c_int
+    lib.kvr_shift_cache_build.argtypes = [_vpp, _vpp, _vpp, _vpp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                          ctypes.c_int32, _i64p, _i64p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_float,
+                                          ctypes.c_int32, _vp]
+    lib.kvr_shift_cache_build.restype = ctypes.c_int
+    lib.kvr_indexed_scatter_kv.argtypes = [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                           ctypes.c_int32, _i64p, ctypes.c_int32, _vp]
+    lib.kvr_indexed_scatter_kv.restype = ctypes.c_int
+    lib.kvr_attention_schedule.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                           ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _i32p, ctypes.c_int64]
+    lib.kvr_attention_schedule.restype = ctypes.c_int64
+    lib.kvr_attention_workspace_bytes.argtypes = [_i32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]
+    lib.kvr_attention_workspace_bytes.restype = ctypes.c_int64
+    lib.kvr_packed_causal_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32,
+                                                ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_float,
+                                                _i64p, _vp, ctypes.c_int64, _i32p, _vp, ctypes.c_int64,
+                                                ctypes.c_int32, _vp]
+    lib.kvr_packed_causal_attention.restype = ctypes.c_int
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it is missing or has another ABI version."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if torch.version.hip is None:
+                raise NativeError("libkvrepair requires a ROCm build of PyTorch")
+            if not LIB_PATH.exists():
+                raise NativeError(f"{LIB_PATH} is missing; build it with `python __graft_entry__.py` "
+                                  "(budgeted-kv-cache-repair_amd/build_lib.py)")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            _declare(handle)
+            version = handle.kvr_abi_version()
+            if version != ABI_VERSION:
+                raise NativeError(f"libkvrepair ABI {version} != expected {ABI_VERSION}; rebuild the library")
+            _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status < 0:
+        text = lib().kvr_status_string(int(status)).decode()
+        raise NativeError(f"{what} failed: {text} (status {status})")
+
+
+def stream_handle(device: torch.device) -> ctypes.c_void_p:
+    """hipStream_t of the caller's current stream on ``device``."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def i64_array(values) -> ctypes.Array:
+    values = list(values)
+    return (ctypes.c_int64 * len(values))(*values)
+
+
+def ptr_array(tensors) -> ctypes.Array:
+    tensors = list(tensors)
+    return (ctypes.c_void_p * len(tensors))(*(t.data_ptr() for t in tensors))
+
+
+def strides3(t: torch.Tensor) -> list[int]:
+    """{head, row, dim} element strides of a [1, heads, rows, dim] tensor."""
+    return [int(t.stride(1)), int(t.stride(2)), int(t.stride(3))]

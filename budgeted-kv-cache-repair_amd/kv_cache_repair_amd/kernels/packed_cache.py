@@ -1,0 +1,358 @@
+"""Packed selected-row refresh through isolated native decoder module shells.
+
+MI355X counterpart of the reference packed executor
+(src/kv_cache_repair/kernels/packed_cache.py:225-298), re-derived for
+transformers 5.15. The selected rows run through every layer in ONE
+layer-major HF forward; at each layer the fresh K/V are scattered into the
+owned output cache (libkvrepair kvr_indexed_scatter_kv) and then attend to
+their full absolute causal history (libkvrepair kvr_packed_causal_attention),
+with no materialised mask and no GQA head copies.
+
+transformers 5.15 plugin points used (the reference's three, re-derived):
+  1. an attention function registered in ALL_ATTENTION_FUNCTIONS under a name
+     with no mask interface, so create_causal_mask returns None;
+  2. a DynamicLayer subclass whose update() scatters and returns the full K/V
+     (5.15 passes no cache_position, so positions come from the context);
+  3. a per-call context passed as a forward kwarg — no global request state.
+"""
+
+from __future__ import annotations
+
+import copy
+import ctypes
+from dataclasses import dataclass, field
+from threading import Lock
+from typing import Any, Sequence
+
+import torch
+import transformers
+from transformers.cache_utils import Cache, DynamicLayer
+
+from .. import _native
+from .executor import _validate_cache, _validate_intervals, layer_kv
+from .indexed_attention import IndexedPlan, DeviceIndexedPlan, _require_gfx950
+
+_ATTENTION_NAME = "kvr_hip_packed_absolute_attention_v1"
+_REGISTRATION_LOCK = Lock()
+_SUPPORTED_TRANSFORMERS = ("5.15.0",)
+_BACKENDS = ("hip",)
+
+
+@dataclass
+class _PackedContext:
+    """Per-request state shared by the layer shells of one forward."""
+
+    positions: torch.Tensor
+    logical_length: int
+    backend: str
+    device_plan: Any = None
+    launcher: Any = None
+
+
+@dataclass
+class _Launcher:
+    """Precomputed ctypes arguments for the per-layer scatter and attention calls."""
+
+    device: torch.device
+    n_sel: int
+    n_keys: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    dtype_code: int
+    host_schedule: Any
+    device_schedule: torch.Tensor
+    workspace: torch.Tensor | None
+    workspace_bytes: int
+    positions_ptr: int
+    _strides: dict = field(default_factory=dict)
+
+    def _stride_array(self, tensors):
+        key = tuple(t.stride() for t in tensors)
+        arr = self._strides.get(key)
+        if arr is None:
+            arr = _native.i64_array([s for t in tensors for s in _native.strides3(t)])
+            self._strides[key] = arr
+        return arr
+
+    def scatter(self, keys, values, fresh_k, fresh_v) -> None:
+        status = _native.lib().kvr_indexed_scatter_kv(
+            keys.data_ptr(), values.data_ptr(), fresh_k.data_ptr(), fresh_v.data_ptr(), self.positions_ptr,
+            self.n_sel, self.kv_heads, self.n_keys, self.head_dim,
+            self._stride_array((keys, values, fresh_k, fresh_v)), self.dtype_code,
+            _native.stream_handle(self.device))
+        _native.check(status, "kvr_indexed_scatter_kv")
+
+    def attention(self, q, k, v, out_view, scale: float) -> None:
+        status = _native.lib().kvr_packed_causal_attention(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out_view.data_ptr(), self.positions_ptr, self.n_sel,
+            self.q_heads, self.kv_heads, self.n_keys, self.head_dim, float(scale),
+            self._stride_array((q, k, v, out_view)), self.device_schedule.data_ptr(), len(self.host_schedule),
+            self.host_schedule, self.workspace.data_ptr() if self.workspace is not None else None,
+            self.workspace_bytes, self.dtype_code, _native.stream_handle(self.device))
+        _native.check(status, "kvr_packed_causal_attention")
+
+
+def _packed_attention(module, query, key, value, attention_mask, *, scaling=None, dropout=0.0,
+                      sur_packed_context=None, **kwargs):
+    """Registered attention function: packed queries over the full mixed cache."""
+    context = sur_packed_context
+    if not isinstance(context, _PackedContext):
+        raise RuntimeError("packed attention requires explicit per-call request context")
+    if attention_mask is not None:
+        raise RuntimeError("native dense mask construction must be bypassed for packed attention")
+    if dropout:
+        raise ValueError("packed attention supports inference without dropout only")
+    if query.shape[-2] != context.positions.numel() or key.shape[-2] != context.logical_length:
+        raise RuntimeError("packed attention query/cache lengths drifted")
+    if context.backend != "hip":
+        raise RuntimeError("unknown packed attention backend")
+    launcher = context.launcher
+    if (query.shape[1], key.shape[1], query.shape[3]) != (launcher.q_heads, launcher.kv_heads, launcher.head_dim):
+        raise RuntimeError("packed attention head geometry drifted")
+    scale = query.shape[-1] ** -0.5 if scaling is None else float(scaling)
+    # Native modules consume [batch, query, query_head, head_dim]; the kernel
+    # writes that layout directly through a permuted view.
+    out = torch.empty((1, query.shape[2], query.shape[1], query.shape[3]), dtype=query.dtype, device=query.device)
+    launcher.attention(query, key, value, out.permute(0, 2, 1, 3), scale)
+    return out, None
+
+
+def _register_attention() -> None:
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    with _REGISTRATION_LOCK:
+        if _ATTENTION_NAME in ALL_MASK_ATTENTION_FUNCTIONS:
+            raise RuntimeError("packed backend name unexpectedly has a native mask interface")
+        if _ATTENTION_NAME in ALL_ATTENTION_FUNCTIONS:
+            if ALL_ATTENTION_FUNCTIONS[_ATTENTION_NAME] is not _packed_attention:
+                raise RuntimeError("packed backend registry name is already owned by another implementation")
+        else:
+            ALL_ATTENTION_FUNCTIONS.register(_ATTENTION_NAME, _packed_attention)
+
+
+def _make_native_view(base):
+    """Shallow module shells sharing parameters, with a private config naming the
+    packed attention; the caller's modules and config are never modified."""
+    _register_attention()
+    config = copy.deepcopy(base.config)
+    config._attn_implementation = _ATTENTION_NAME
+    view = copy.copy(base)
+    view._modules = base._modules.copy()
+    view.config = config
+    layers = []
+    for original in base.layers:
+        layer = copy.copy(original)
+        layer._modules = original._modules.copy()
+        if hasattr(layer, "config"):
+            layer.config = config
+        attention = copy.copy(original.self_attn)
+        attention._modules = original.self_attn._modules.copy()
+        attention.config = config
+        layer._modules["self_attn"] = attention
+        layers.append(layer)
+    view._modules["layers"] = torch.nn.ModuleList(layers)
+    view.layers.training = False
+    return view
+
+
+def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend):
+    """Fail closed outside the inspected contract, before any device work."""
+    if transformers.__version__ not in _SUPPORTED_TRANSFORMERS:
+        raise ValueError(f"packed HIP executor requires transformers in {_SUPPORTED_TRANSFORMERS}")
+    from transformers.models.llama.modeling_llama import LlamaForCausalLM, LlamaModel
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3ForCausalLM, Qwen3Model
+
+    model = shim.generator
+    base = shim._base_transformer(model)
+    if (type(model), type(base)) not in {(LlamaForCausalLM, LlamaModel), (Qwen3ForCausalLM, Qwen3Model)}:
+        raise ValueError("packed executor requires exact native dense Llama or Qwen3 classes")
+    if model.training or base.training or any(module.training for module in base.modules()):
+        raise ValueError("packed executor requires eval mode on all decoder modules")
+    config = model.config
+    if config.num_hidden_layers != len(base_cache.layers) or len(base.layers) != len(base_cache.layers):
+        raise ValueError("model and cache layer counts must agree")
+    rope = getattr(config, "rope_parameters", None) or {}
+    if rope.get("rope_type", "default") != "default" or getattr(base.rotary_emb, "rope_type", None) != "default":
+        raise ValueError("packed executor supports default fixed RoPE only")
+    if getattr(config, "use_sliding_window", False) or getattr(base, "has_sliding_layers", False):
+        raise ValueError("packed executor requires full attention")
+    if any(kind != "full_attention" for kind in getattr(config, "layer_types", []) or []):
+        raise ValueError("packed executor rejects sliding/hybrid attention")
+    device = edited_ids.device
+    if device.type != "cuda" or torch.version.hip is None:
+        raise ValueError("packed HIP executor requires one ROCm GPU device")
+    if any(parameter.device != device for parameter in model.parameters()):
+        raise ValueError("packed executor requires all model parameters on the request device")
+    if any(layer_kv(base_cache, i)[0].device != device or layer_kv(base_cache, i)[1].device != device
+           for i in range(len(base_cache.layers))):
+        raise ValueError("packed executor requires all cache layers on the request device")
+    if any(getattr(module, "_hf_hook", None) is not None for module in model.modules()):
+        raise ValueError("packed executor does not support dispatch/offload hooks")
+    if any("forward" in module.__dict__ for module in base.modules()):
+        raise ValueError("packed executor does not support per-instance decoder forward overrides")
+    key = layer_kv(base_cache, 0)[0]
+    if key.dtype not in _native.DTYPE_CODES:
+        raise ValueError("packed HIP executor supports float32, float16 and bfloat16 caches")
+    if key.shape[-1] % 2 or key.shape[-1] > 256:
+        raise ValueError("packed HIP executor requires an even head dimension <= 256")
+    if config.num_attention_heads % config.num_key_value_heads:
+        raise ValueError("query head count must be divisible by KV head count")
+    _require_gfx950(device)
+    return base
+
+
+class _PackedLayer(DynamicLayer):
+    """Cache layer that scatters the fresh rows, then exposes the full mixed K/V."""
+
+    def __init__(self, key, value, context, backend):
+        super().__init__()
+        self.keys, self.values = key, value
+        self.dtype, self.device = key.dtype, key.device
+        self.is_initialized = True
+        self._context = context
+        self._backend = backend
+        self.updated = False
+
+    def get_mask_sizes(self, query_length):
+        return self._context.logical_length, 0
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        if self.updated:
+            raise RuntimeError("packed native forward updated one layer more than once")
+        positions = self._context.positions
+        expected = (*self.keys.shape[:2], positions.numel(), self.keys.shape[-1])
+        for source, target in ((key_states, self.keys), (value_states, self.values)):
+            if source.shape != expected or source.dtype != target.dtype or source.device != target.device:
+                raise RuntimeError("packed native projection geometry/dtype/device drifted")
+        if self._backend != "hip":
+            raise RuntimeError("unknown packed writeback backend")
+        self._context.launcher.scatter(self.keys, self.values, key_states, value_states)
+        self.updated = True
+        return self.keys, self.values
+
+
+def _launcher(device_plan: DeviceIndexedPlan, config, key: torch.Tensor) -> _Launcher:
+    q_heads, kv_heads, dim = int(config.num_attention_heads), int(key.shape[1]), int(key.shape[3])
+    host, dev = device_plan.attention_schedule(q_heads, kv_heads, dim, key.dtype)
+    ws_bytes = int(_native.lib().kvr_attention_workspace_bytes(host, len(host), q_heads, dim))
+    _native.check(ws_bytes, "kvr_attention_workspace_bytes")
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=key.device) if ws_bytes else None
+    return _Launcher(device=key.device, n_sel=device_plan.selected_count, n_keys=device_plan.logical_length,
+                     q_heads=q_heads, kv_heads=kv_heads, head_dim=dim, dtype_code=_native.DTYPE_CODES[key.dtype],
+                     host_schedule=host, device_schedule=dev, workspace=workspace, workspace_bytes=ws_bytes,
+                     positions_ptr=device_plan.positions.data_ptr())
+
+
+def _check_backends(attention_backend, writeback_backend):
+    if attention_backend not in _BACKENDS:
+        raise ValueError("attention_backend must be 'hip'")
+    if writeback_backend not in _BACKENDS:
+        raise ValueError("writeback_backend must be 'hip'")
+
+
+def _check_ids(edited_ids_t):
+    if not isinstance(edited_ids_t, torch.Tensor) or edited_ids_t.ndim != 2 or edited_ids_t.shape[0] != 1:
+        raise ValueError("edited_ids_t must be a single-batch rank-two tensor")
+    if edited_ids_t.dtype not in (torch.int32, torch.int64):
+        raise ValueError("edited_ids_t must contain int32 or int64 IDs")
+
+
+def _receipt(intervals, selected, length, layer_count, attention_backend, writeback_backend):
+    return {
+        "executor": "packed_interval_repair",
+        "schedule": "packed_selected_rows_layer_major",
+        "attention_backend": attention_backend,
+        "writeback_backend": writeback_backend,
+        "interval_count": len(intervals),
+        "recomputed_tokens": len(selected),
+        "logical_length": length,
+        "layer_count": layer_count,
+        "base_cache_ownership": "borrowed_immutable",
+        "output_cache_ownership": "independent" if selected else "borrowed_base",
+        "selected_absolute_positions": list(selected),
+        "native_model_mutated": False,
+        "numerical_contract": "separate_schedule_qualification_required",
+    }
+
+
+@torch.no_grad()
+def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
+                  attention_backend: str, writeback_backend: str) -> None:
+    """Run the packed forward, scattering into the caller-owned ``output`` cache."""
+    base = shim._base_transformer(shim.generator)
+    device_plan = host_plan.to(edited_ids_t.device)
+    positions = device_plan.positions
+    key0 = layer_kv(output, 0)[0]
+    context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan,
+                             _launcher(device_plan, base.config, key0))
+    native_view = _make_native_view(base)
+    layers = [_PackedLayer(*layer_kv(output, i), context, writeback_backend) for i in range(layer_count)]
+    cache = Cache(layers=layers)
+    result = native_view(input_ids=edited_ids_t.index_select(1, positions), position_ids=positions.unsqueeze(0),
+                         past_key_values=cache, use_cache=True, return_dict=True, sur_packed_context=context)
+    if result.past_key_values is not cache or not all(layer.updated for layer in layers):
+        raise RuntimeError("native packed forward did not update each cache layer exactly once")
+
+
+@torch.no_grad()
+def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
+                           intervals: Sequence[tuple[int, int]], *, attention_backend: str = "hip",
+                           writeback_backend: str = "hip", plan: Any = None) -> tuple[Any, dict[str, Any]]:
+    """Recompute sorted selected rows in one native layer-major forward.
+
+    Same signature, validation order, receipt and ownership contract as the
+    reference executor (packed_cache.py:225-298); the backends are the gfx950
+    HIP kernels. ``plan`` optionally supplies a reusable host IndexedPlan for
+    exactly these intervals and length. The borrowed ``base_cache`` is never
+    mutated: a nonempty repair returns an independently owned cache (one
+    libkvrepair copy launch), an empty one returns ``base_cache`` itself.
+    """
+    _check_backends(attention_backend, writeback_backend)
+    _check_ids(edited_ids_t)
+    length = int(edited_ids_t.shape[1])
+    layer_count = _validate_cache(base_cache, length)
+    intervals = _validate_intervals(intervals, length)
+    selected = tuple(p for start, end in intervals for p in range(start, end))
+    if plan is not None:
+        if not isinstance(plan, IndexedPlan) or tuple(plan.positions) != selected or plan.logical_length != length:
+            raise ValueError("supplied IndexedPlan must match exact selected positions and cache length")
+    receipt = _receipt(intervals, selected, length, layer_count, attention_backend, writeback_backend)
+    if not selected:
+        return base_cache, receipt
+    _qualify(shim, edited_ids_t, base_cache, attention_backend, writeback_backend)
+    host_plan = plan if plan is not None else IndexedPlan(selected, length)
+    from ..cache import clone_cache
+
+    output = clone_cache(base_cache)
+    _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend)
+    return output, receipt
+
+
+@torch.no_grad()
+def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tensor,
+                          intervals: Sequence[tuple[int, int]], *, plan: Any = None) -> dict[str, Any]:
+    """Packed refresh that scatters IN PLACE into a cache the caller owns.
+
+    For a cache the caller has just built and nobody else references (the
+    shifted cache of build_halo_cache inside repair_after_deletion) the
+    ownership copy of packed_interval_repair is redundant; this entry skips it.
+    The result equals packed_interval_repair's output bit for bit.
+    """
+    _check_ids(edited_ids_t)
+    length = int(edited_ids_t.shape[1])
+    layer_count = _validate_cache(owned_cache, length)
+    intervals = _validate_intervals(intervals, length)
+    selected = tuple(p for start, end in intervals for p in range(start, end))
+    if plan is not None:
+        if not isinstance(plan, IndexedPlan) or tuple(plan.positions) != selected or plan.logical_length != length:
+            raise ValueError("supplied IndexedPlan must match exact selected positions and cache length")
+    receipt = _receipt(intervals, selected, length, layer_count, "hip", "hip")
+    receipt["base_cache_ownership"] = "owned_in_place"
+    if not selected:
+        return receipt
+    _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
+    host_plan = plan if plan is not None else IndexedPlan(selected, length)
+    _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip")
+    return receipt

@@ -1,0 +1,164 @@
+/*
+ * kvrepair.h — C ABI of the MI355X (gfx950) packed refresh executor.
+ *
+ * Three data-parallel steps of budgeted KV-cache repair run as hand-written
+ * HIP kernels behind this header:
+ *   1. RoPE delta re-rotation of retained-suffix K rows (and the fused
+ *      shift-cache build that also copies the prefix and the V tail),
+ *   2. the indexed scatter of refreshed K/V rows into a layer's cache,
+ *   3. packed selected-query causal attention with GQA grouping.
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are rank-4 [batch=1, heads, rows, head_dim] views described by a
+ *     base device pointer (the address of element (0,0,0,0)) and three signed
+ *     element strides {head, row, dim}. The batch dimension is always 1.
+ *   - `dtype` is one of KVR_DTYPE_*; every tensor of a call shares it.
+ *   - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream);
+ *     NULL means the legacy default stream. Calls only enqueue work on that
+ *     stream: no allocation, no free, no host<->device copy, no synchronisation.
+ *   - Return value 0 is success; a negative value is a KVR_E_* status whose
+ *     text kvr_status_string() gives. Arguments are checked before any launch:
+ *     a failed check enqueues nothing.
+ *   - Calls are thread-safe and re-entrant; the library keeps no per-request
+ *     state.
+ */
+#ifndef KVREPAIR_H
+#define KVREPAIR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVR_ABI_VERSION 1
+
+enum kvr_dtype {
+    KVR_DTYPE_F32 = 0,
+    KVR_DTYPE_F16 = 1,
+    KVR_DTYPE_BF16 = 2,
+};
+
+enum kvr_status {
+    KVR_OK = 0,
+    KVR_E_INVALID_ARGUMENT = -1,
+    KVR_E_UNSUPPORTED_DTYPE = -2,
+    KVR_E_UNSUPPORTED_SHAPE = -3,
+    KVR_E_BAD_STRIDE = -4,
+    KVR_E_NULL_POINTER = -5,
+    KVR_E_WORKSPACE_TOO_SMALL = -6,
+    KVR_E_BAD_SCHEDULE = -7,
+    KVR_E_LAUNCH_FAILED = -8,
+    KVR_E_CAPACITY = -9,
+};
+
+/* ABI version of the loaded library (KVR_ABI_VERSION at build time). */
+int kvr_abi_version(void);
+
+/* Static, NUL-terminated description of a status code. */
+const char* kvr_status_string(int status);
+
+/*
+ * RoPE delta re-rotation of retained-suffix keys for every layer in ONE launch.
+ *
+ * Replaces the per-layer eager chain of the reference
+ * `shifted_suffix_keys(model, key, shift)` (src/kv_cache_repair/cache.py:47-77):
+ *   cos, sin = rotary_emb(key, full((1, rows), shift))   fp32, cast to dtype
+ *   out = key * cos + rotate_half(key) * sin              split-half pairs
+ * with each multiply and the add rounded to `dtype` exactly as the eager ops
+ * round them. cos/sin are recomputed in fp32 in-kernel from `inv_freq`
+ * (the model's rotary_emb.inv_freq as fp32, rotary_dim/2 entries, device
+ * memory): freq_i = inv_freq[i] * (float)shift, c = cosf(freq) * scaling.
+ * Dims >= rotary_dim pass through unchanged (cache.py:74-77). shift == 0 is an
+ * exact bit copy (cache.py:53-54). rows == 0 enqueues nothing.
+ *
+ * src[l] / dst[l]: per-layer base pointers (host arrays of n_layers device
+ * pointers); all layers share the strides. dst must not overlap src.
+ */
+int kvr_rope_delta_rotate(const void* const* src, void* const* dst, int32_t n_layers, int32_t n_heads,
+                          int64_t rows, int32_t head_dim, int32_t rotary_dim, const int64_t src_stride[3],
+                          const int64_t dst_stride[3], int64_t shift, const float* inv_freq,
+                          float attention_scaling, int32_t dtype, void* stream);
+
+/*
+ * Fused shift-cache build: writes a whole shifted cache for every layer in ONE
+ * launch (K and V), replacing the per-layer clone/rotate/cat sequence of the
+ * reference `build_halo_cache(..., halo_tokens=0)` (cache.py:103-144) when no
+ * boundary token needs recomputation:
+ *   new_k[:, :, :prefix]           = old_k[:, :, :prefix]            (bit copy)
+ *   new_v[:, :, :prefix]           = old_v[:, :, :prefix]            (bit copy)
+ *   new_k[:, :, nts:nts+tail_rows] = rotate(old_k[:, :, ots:ots+tail_rows], shift)
+ *   new_v[:, :, nts:nts+tail_rows] = old_v[:, :, ots:ots+tail_rows]  (bit copy)
+ * with nts = new_tail_start, ots = old_tail_start. Rows of new_* outside those
+ * two ranges are not written. The rotation is bit-identical to
+ * kvr_rope_delta_rotate.
+ */
+int kvr_shift_cache_build(const void* const* old_k, const void* const* old_v, void* const* new_k,
+                          void* const* new_v, int32_t n_layers, int32_t n_heads, int32_t head_dim,
+                          int32_t rotary_dim, const int64_t old_stride[3], const int64_t new_stride[3],
+                          int64_t prefix_rows, int64_t old_tail_start, int64_t new_tail_start, int64_t tail_rows,
+                          int64_t shift, const float* inv_freq, float attention_scaling, int32_t dtype,
+                          void* stream);
+
+/*
+ * Indexed K/V scatter (bit copy, NaN payloads included):
+ *   out_k[0, h, positions[r], :] = fresh_k[0, h, r, :]   for r < n_sel, h < n_heads
+ *   out_v[0, h, positions[r], :] = fresh_v[0, h, r, :]
+ * Replaces `_PackedLayer.update`'s index_copy_ pair
+ * (src/kv_cache_repair/kernels/packed_cache.py:189-191) and
+ * `indexed_kv_scatter_` (src/kv_cache_repair/kernels/indexed_attention.py:179-204).
+ * `positions` is a device int64 array; entries outside [0, n_keys) are skipped
+ * like the reference Triton kernel's masked store (_indexed_triton.py:22-27).
+ * strides: 12 element strides {head,row,dim} for out_k, out_v, fresh_k, fresh_v.
+ * n_sel == 0 enqueues nothing.
+ */
+int kvr_indexed_scatter_kv(void* out_k, void* out_v, const void* fresh_k, const void* fresh_v,
+                           const int64_t* positions, int64_t n_sel, int32_t n_heads, int64_t n_keys,
+                           int32_t head_dim, const int64_t strides[12], int32_t dtype, void* stream);
+
+/*
+ * Host-side work schedule for kvr_packed_causal_attention (no device access).
+ * Splits the selected rows into row groups and each group's causal key range
+ * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`
+ * is the HOST copy of the strictly increasing selected positions (the
+ * reference IndexedPlan.positions, indexed_attention.py:56-83).
+ * chunk_keys <= 0 selects a size from the geometry. Writes at most `capacity`
+ * int32 entries to `schedule` and returns the entry count, or a negative
+ * status. With schedule == NULL it returns the required entry count.
+ */
+int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_sel, int64_t n_keys, int32_t n_q_heads,
+                               int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys,
+                               int32_t* schedule, int64_t capacity);
+
+/* Workspace bytes kvr_packed_causal_attention needs for a schedule (host-only). */
+int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_t schedule_len, int32_t n_q_heads,
+                                      int32_t head_dim);
+
+/*
+ * Packed selected-query causal attention, GQA grouped:
+ *   out[0, h, r, :] = softmax_{j <= positions[r]}( scale * q[0,h,r,:] . k[0,h/G,j,:] ) @ v[0,h/G,:,:]
+ * for h < n_q_heads, r < n_sel, G = n_q_heads / n_kv_heads. Replaces the
+ * reference `_packed_attention` SDPA branch (packed_cache.py:47-67, mask
+ * key <= position built at :205-207) and `indexed_causal_attention`
+ * (indexed_attention.py:207-241). Softmax statistics and accumulation are
+ * fp32; QK^T and PV run on bf16/fp16 MFMA (P carried as a hi+lo pair) when
+ * dtype is bf16/fp16 and head_dim is 64 or 128, otherwise on the vector ALU.
+ * K/V must already hold the fresh selected rows (scatter first, same stream).
+ * `positions` (device int64) and `schedule` (device int32, the bytes of
+ * kvr_attention_schedule for the same positions/heads) are read-only.
+ * strides: 12 element strides {head,row,dim} for q, k, v, out (k and v share
+ * n_keys rows). `workspace` holds kvr_attention_workspace_bytes() bytes of
+ * scratch (no initialisation needed). n_sel == 0 enqueues nothing.
+ */
+int kvr_packed_causal_attention(const void* q, const void* k, const void* v, void* out, const int64_t* positions,
+                                int64_t n_sel, int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys,
+                                int32_t head_dim, float scale, const int64_t strides[12], const int32_t* schedule,
+                                int64_t schedule_len, const int32_t* host_schedule, void* workspace,
+                                int64_t workspace_bytes, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVREPAIR_H */

@@ -1,0 +1,204 @@
+"""GPU parity of the RoPE delta rotation and the fused shift-cache build.
+
+Checked against the C oracle (bit-exact given the same fp32 cos/sin, <= 1
+bfloat16 ulp with the oracle's own correctly rounded cos/sin) and against the
+reference's eager chain (oracle/reference_path.py) run on the same GPU,
+including BASELINE.json's full c2/c3 sizes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+CODE = {torch.float32: orc.F32, torch.float16: orc.F16, torch.bfloat16: orc.BF16}
+
+
+def host_bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.numpy().copy()
+    return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def ulp_distance(a: np.ndarray, b: np.ndarray) -> int:
+    """Max distance in units in the last place between two uint16 bf16/fp16 bit arrays."""
+    def ordered(x):
+        x = x.astype(np.int32)
+        return np.where(x & 0x8000, 0x8000 - (x & 0x7FFF), 0x8000 + (x & 0x7FFF))
+    return int(np.abs(ordered(a) - ordered(b)).max()) if a.size else 0
+
+
+def inv_freq(dim, theta, device):
+    return (1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float) / dim))).to(device)
+
+
+def device_cos_sin(inv, shift):
+    """fp32 cos/sin exactly as the reference computes them on this device
+    (transformers 5.15.0 modeling_llama.py:113-127 at position = shift)."""
+    freqs = inv * torch.tensor(float(shift), device=inv.device)
+    return freqs.cos().cpu().numpy(), freqs.sin().cpu().numpy()
+
+
+def rotate_layers(keys, outs, shift, inv):
+    from kv_cache_repair_amd.cache import rope_delta_rotate_
+
+    rope_delta_rotate_(keys, outs, shift, inv)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("shift", [-1, -32, -512, 7])
+def test_rotate_matches_oracle_bitwise(gpu_device, dtype, dim, shift):
+    torch.manual_seed(100 + dim + shift)
+    layers, heads, rows = 3, 4, 130
+    inv = inv_freq(dim, 500000.0, gpu_device)
+    keys = [torch.randn(1, heads, rows, dim, device=gpu_device).to(dtype) for _ in range(layers)]
+    outs = [torch.empty_like(k) for k in keys]
+    rotate_layers(keys, outs, shift, inv)
+    table = device_cos_sin(inv, shift)
+    own = orc.rope_cos_sin(inv.cpu().numpy(), shift)
+    for k, o in zip(keys, outs):
+        got = host_bits(o[0])
+        expect = orc.rope_rotate(host_bits(k[0]), CODE[dtype], shift, inv.cpu().numpy(), cos_sin=table)
+        assert same_bits(got, expect)
+        if dtype != torch.float32:
+            mine = orc.rope_rotate(host_bits(k[0]), CODE[dtype], shift, inv.cpu().numpy(), cos_sin=own)
+            assert ulp_distance(got, mine) <= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rotate_strided_views_and_partial_rotary(gpu_device, dtype):
+    torch.manual_seed(7)
+    dim, shift = 64, -40
+    backing = torch.randn(1, 3, 2 * 50 + 3, 2 * dim + 5, device=gpu_device).to(dtype)
+    key = backing[:, :, 1:1 + 100:2, 2:2 + 2 * dim:2]  # non-unit dim stride -> scalar path
+    inv = inv_freq(32, 10000.0, gpu_device)         # rotary_dim 32 < head_dim 64
+    out = torch.empty(key.shape, dtype=dtype, device=gpu_device)
+    from kv_cache_repair_amd.cache import rope_delta_rotate_
+
+    rope_delta_rotate_([key], [out], shift, inv)
+    torch.cuda.synchronize()
+    expect = orc.rope_rotate(host_bits(key[0]), CODE[dtype], shift, inv.cpu().numpy(), rotary_dim=32,
+                             cos_sin=device_cos_sin(inv, shift))
+    assert same_bits(host_bits(out[0]), expect)
+
+
+def test_zero_shift_is_a_bit_copy_with_nan_payloads(gpu_device):
+    raw = torch.tensor([0, -32768, 32640, -128, 32705, 1], dtype=torch.int16).repeat(2 * 7 * 128 // 6 + 1)
+    key = raw[: 2 * 7 * 128].view(torch.bfloat16).reshape(1, 2, 7, 128).to(gpu_device)
+    out = torch.empty_like(key)
+    rotate_layers([key], [out], 0, inv_freq(128, 10000.0, gpu_device))
+    assert torch.equal(out.view(torch.int16), key.view(torch.int16))
+
+
+def _tiny_llama(device, dtype=torch.float32, theta=10000.0, heads=4, kv_heads=2, dim=16, layers=2, seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=heads * dim, intermediate_size=2 * heads * dim,
+                      num_hidden_layers=layers, num_attention_heads=heads, num_key_value_heads=kv_heads,
+                      head_dim=dim, max_position_embeddings=4096, rope_theta=theta)
+    return LlamaForCausalLM(cfg).to(device=device, dtype=dtype).eval()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_shifted_suffix_keys_equals_reference_eager_chain_on_device(gpu_device, dtype):
+    from kv_cache_repair_amd.cache import OperatorShim, shifted_suffix_keys
+
+    model = _tiny_llama(gpu_device, dtype)
+    torch.manual_seed(11)
+    key = torch.randn(1, 2, 160, 16, device=gpu_device).to(dtype)
+    ours = shifted_suffix_keys(OperatorShim(model), key, -32)
+    eager = ref.shifted_suffix_keys(model, key, -32)
+    torch.cuda.synchronize()
+    assert torch.equal(ours.view(torch.uint8), eager.contiguous().view(torch.uint8))
+
+
+def test_build_halo_cache_matches_reference_config1(gpu_device):
+    """tiny Llama, 256 ids, delete positions 64-95 (shift -32)."""
+    from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache
+
+    model = _tiny_llama(gpu_device, torch.float32, heads=4, kv_heads=2, dim=16, layers=2, seed=0)
+    gen = torch.Generator().manual_seed(0)
+    old_ids = torch.randint(0, 512, (1, 256), generator=gen).to(gpu_device)
+    new_ids = torch.cat((old_ids[:, :64], old_ids[:, 96:]), dim=1)
+    with torch.no_grad():
+        old = model(input_ids=old_ids, use_cache=True).past_key_values
+    snapshot = [(k.clone(), v.clone()) for k, v in ((l.keys, l.values) for l in old.layers)]
+    ours, meta = build_halo_cache(OperatorShim(model), old, old_ids, new_ids, 0)
+    expect, emeta = ref.build_halo_cache(model, old, old_ids, new_ids, 0)
+    torch.cuda.synchronize()
+    assert meta == emeta
+    for i in range(2):
+        for a, b in zip(ref.layer_kv(ours, i), ref.layer_kv(expect, i)):
+            assert torch.equal(a.view(torch.uint8), b.contiguous().view(torch.uint8))
+        assert torch.equal(old.layers[i].keys, snapshot[i][0]) and torch.equal(old.layers[i].values, snapshot[i][1])
+
+
+def test_build_halo_cache_with_changed_boundary_token(gpu_device):
+    """A deletion that changes one boundary token: rows [prefix, new_suffix_start)
+    come from a native forward, the tail is rotated (cache.py:116-139)."""
+    from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache
+
+    model = _tiny_llama(gpu_device, torch.float32, seed=1)
+    old_ids = torch.tensor([[5, 6, 7, 8, 9, 10, 11, 12, 13, 14]], device=gpu_device)
+    new_ids = torch.tensor([[5, 6, 99, 11, 12, 13, 14]], device=gpu_device)
+    with torch.no_grad():
+        old = model(input_ids=old_ids, use_cache=True).past_key_values
+    ours, meta = build_halo_cache(OperatorShim(model), old, old_ids, new_ids, 0)
+    expect, emeta = ref.build_halo_cache(model, old, old_ids, new_ids, 0)
+    assert meta == emeta and meta["mandatory_changed_tokens"] == 1
+    for i in range(2):
+        for a, b in zip(ref.layer_kv(ours, i), ref.layer_kv(expect, i)):
+            assert torch.equal(a.view(torch.uint8), b.contiguous().view(torch.uint8))
+
+
+@pytest.mark.parametrize("config", ["c2", "c3"])
+def test_full_size_shift_cache_build_matches_reference(gpu_device, config):
+    """BASELINE configs 2/3 at full size: 32 layers x 8 KV heads x 128 dims bf16,
+    theta 5e5, K/V ~ N(0,1), delete 128 @512 of 2048 / 512 @2048 of 8192."""
+    from kv_cache_repair_amd.cache import OperatorShim, _shift_rows
+
+    total, at, span = (2048, 512, 128) if config == "c2" else (8192, 2048, 512)
+    gen = torch.Generator(device=gpu_device).manual_seed(1)
+    old = [(torch.randn(1, 8, total, 128, device=gpu_device, generator=gen).to(torch.bfloat16),
+            torch.randn(1, 8, total, 128, device=gpu_device, generator=gen).to(torch.bfloat16)) for _ in range(32)]
+    n = total - span
+    inv = inv_freq(128, 500000.0, gpu_device)
+    new = [(torch.empty(1, 8, n, 128, dtype=torch.bfloat16, device=gpu_device),
+            torch.empty(1, 8, n, 128, dtype=torch.bfloat16, device=gpu_device)) for _ in range(32)]
+    _shift_rows([k for k, _ in old], [v for _, v in old], [k for k, _ in new], [v for _, v in new],
+                prefix_rows=at, old_tail_start=at + span, new_tail_start=at, tail_rows=n - at, shift=-span,
+                inv_freq=inv, scaling=1.0, rotary_dim=128)
+    torch.cuda.synchronize()
+
+    class _Rot(torch.nn.Module):  # the reference's rotary_emb call on this device
+        def forward(self, x, position_ids):
+            freqs = inv[None, :, None].float() @ position_ids[:, None, :].float()
+            emb = torch.cat((freqs.transpose(1, 2),) * 2, dim=-1)
+            return emb.cos().to(x.dtype), emb.sin().to(x.dtype)
+
+    class _M:
+        base_model = type("B", (), {"rotary_emb": _Rot()})()
+
+    for layer in (0, 13, 31):
+        ok, ov = old[layer]
+        nk, nv = new[layer]
+        assert torch.equal(nk[:, :, :at].view(torch.int16), ok[:, :, :at].view(torch.int16))
+        assert torch.equal(nv[:, :, :at].view(torch.int16), ov[:, :, :at].view(torch.int16))
+        assert torch.equal(nv[:, :, at:].view(torch.int16), ov[:, :, at + span:].view(torch.int16))
+        eager = ref.shifted_suffix_keys(_M(), ok[:, :, at + span:], -span)
+        assert torch.equal(nk[:, :, at:].view(torch.int16), eager.view(torch.int16))

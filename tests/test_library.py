@@ -1,0 +1,113 @@
+"""The C-ABI library loads, exports every symbol include/kvrepair.h declares,
+and rejects invalid arguments with a status before launching anything (host
+only: no call below reaches a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kvrepair.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_symbols() == sorted([
+        "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
+        "kvr_indexed_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
+        "kvr_packed_causal_attention"])
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.kvr_abi_version() == _native.ABI_VERSION
+    assert lib.kvr_status_string(0) == b"ok"
+    assert lib.kvr_status_string(-3) == b"unsupported shape"
+
+
+def test_entry_points_validate_before_any_launch():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    strides = _native.i64_array([1] * 12)
+    # bad dtype, negative counts, non-positive strides: status, no launch
+    assert lib.kvr_indexed_scatter_kv(None, None, None, None, None, 4, 2, 8, 64, strides, 9, None) == -2
+    assert lib.kvr_indexed_scatter_kv(None, None, None, None, None, -1, 2, 8, 64, strides, 2, None) == -1
+    assert lib.kvr_indexed_scatter_kv(None, None, None, None, None, 4, 2, 8, 64, _native.i64_array([0] * 12), 2,
+                                      None) == -4
+    assert lib.kvr_indexed_scatter_kv(None, None, None, None, None, 4, 2, 8, 64, strides, 2, None) == -5
+    assert lib.kvr_indexed_scatter_kv(None, None, None, None, None, 0, 2, 8, 64, strides, 2, None) == 0
+    s3 = _native.i64_array([1, 1, 1])
+    assert lib.kvr_rope_delta_rotate(None, None, 1, 2, 4, 7, 7, s3, s3, 1, None, 1.0, 2, None) == -3  # odd dim
+    assert lib.kvr_rope_delta_rotate(None, None, 1, 2, 4, 8, 8, s3, s3, 1, None, 1.0, 2, None) == -5
+    assert lib.kvr_packed_causal_attention(None, None, None, None, None, 3, 4, 3, 9, 64, 1.0, strides, None, 0,
+                                           None, None, 0, 2, None) == -3  # heads not divisible
+    assert lib.kvr_packed_causal_attention(None, None, None, None, None, 3, 4, 2, 9, 64, float("nan"), strides,
+                                           None, 0, None, None, 0, 2, None) == -1
+
+
+def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    pos = _native.i64_array(positions)
+    need = lib.kvr_attention_schedule(pos, len(positions), n_keys, hq, hkv, dim, dtype, chunk, None, 0)
+    assert need > 0
+    buf = (ctypes.c_int32 * need)()
+    assert lib.kvr_attention_schedule(pos, len(positions), n_keys, hq, hkv, dim, dtype, chunk, buf, need) == need
+    return list(buf)
+
+
+@pytest.mark.parametrize("positions,n_keys,chunk", [
+    ([0, 1, 2], 3, 0), (list(range(928, 992)), 1920, 0), (list(range(0, 4000, 7)), 4000, 256),
+    ([5, 9, 4095], 4096, 0), (list(range(1024, 2048)), 2048, 512)])
+def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_keys, chunk):
+    s = schedule(positions, n_keys, 32, 8, 128, chunk=chunk)
+    header, n_tiles, kc, n_work = s[:16], s[3], s[4], s[5]
+    assert header[0] == 0x4B565253 and header[2] == len(positions)
+    tiles = [(s[16 + 2 * t], s[17 + 2 * t]) for t in range(n_tiles)]
+    work = [(s[16 + 2 * n_tiles + 2 * w], s[17 + 2 * n_tiles + 2 * w]) for w in range(n_work)]
+    assert kc % 256 == 0 and len(work) == n_work == sum(c for _, c in tiles)
+    # the work items of tile t are exactly chunks 0..c-1, contiguous from its base
+    for t, (base, count) in enumerate(tiles):
+        assert work[base:base + count] == [(t, c) for c in range(count)]
+        last = positions[min(16 * t + 15, len(positions) - 1)]
+        assert (count - 1) * kc <= last < count * kc  # chunks reach the tile's last causal key, no further
+    # every (row, key <= pos) pair lies in exactly one chunk of its tile
+    for r, p in enumerate(positions):
+        base, count = tiles[r // 16]
+        covering = [c for c in range(count) for key in (0, p) if c * kc <= key < (c + 1) * kc]
+        assert covering[0] == 0 and covering[-1] == p // kc
+
+
+def test_schedule_rejects_unsorted_or_out_of_range_positions():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    for positions, n in (([3, 2], 5), ([1, 1], 5), ([5], 5), ([-1], 5)):
+        pos = _native.i64_array(positions)
+        assert lib.kvr_attention_schedule(pos, len(positions), n, 4, 2, 64, 2, 0, None, 0) == -1
+
+
+def test_workspace_is_zero_when_every_tile_fits_one_chunk():
+    from kv_cache_repair_amd import _native
+
+    s = schedule([3, 4, 8, 9], 12, 4, 2, 64)
+    buf = (ctypes.c_int32 * len(s))(*s)
+    assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 0
+    s = schedule(list(range(0, 8000, 100)), 8000, 4, 2, 64, chunk=256)
+    buf = (ctypes.c_int32 * len(s))(*s)
+    assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 16 * 66 * 4
