@@ -1,0 +1,442 @@
+#!/usr/bin/env python3
+"""Refresh-stage benchmark of the MI355X packed refresh executor (one GPU).
+
+Workload (the headline metric's config): an
+8B-shaped Llama (32 layers, hidden 4096, MLP 14336, 32 query / 8 KV heads x
+128, RoPE theta 5e5, vocab 128256, random init, bf16); a synthetic 8192-token
+cache with K/V ~ N(0,1) (seed 1); a 512-token deletion at position 2048
+(shift -512, 5632-row suffix); a 64-token budget as 16 intervals of 4 rows at
+random suffix slots (seed 2).
+
+One step = one full refresh stage, inputs resident in HBM: shift-cache build
+(prefix copy + RoPE delta rotation of every suffix K row + V copy, all layers)
+-> plan upload -> packed forward through all 32 layers with the per-layer
+scatter and packed attention. Prefill, tokenisation and selection are outside
+the step, as in the reference benchmark (benchmark_refresh.py:3-9); unlike it,
+the rotation is inside.
+
+Printed (one JSON line): stage latency (ms per repair), the per-kernel HIP
+event timings of the timed steps, a roofline object for the dominant kernel,
+the rotate-only GB/s, the same stage run the reference way on the same GPU,
+and the reference path timed on the host CPU (cpu_baseline).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import random
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "budgeted-kv-cache-repair_amd"), str(ROOT)]
+
+import torch  # noqa: E402
+
+METRIC = "refresh-stage latency (ms) per repair at 8k ctx/64-tok budget; rotate GB/s"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+# BASELINE config 3 geometry
+LAYERS, HIDDEN, MLP, HQ, HKV, DIM, VOCAB, THETA = 32, 4096, 14336, 32, 8, 128, 128256, 500000.0
+TOTAL, DELETE_AT, DELETE_SPAN, BUDGET_INTERVALS, ROWS_PER_INTERVAL = 8192, 2048, 512, 16, 4
+
+
+def c3_intervals() -> list[tuple[int, int]]:
+    """16 intervals of 4 rows at random 8-token slots of the suffix (seed 2)."""
+    suffix = TOTAL - DELETE_AT - DELETE_SPAN
+    slots = sorted(random.Random(2).sample(range(suffix // 8), BUDGET_INTERVALS))
+    return [(DELETE_AT + 8 * s, DELETE_AT + 8 * s + ROWS_PER_INTERVAL) for s in slots]
+
+
+def make_model(device, layers=LAYERS, seed=1):
+    """Random-init 8B-shaped Llama in bf16 on ``device``.
+
+    Built on the meta device and materialised directly: linear and embedding
+    weights ~ N(0, 0.02) (drawn in fp32, cast to bf16), RMSNorm weights 1, RoPE
+    buffers recomputed -- the values HF's own init gives, without its slow
+    per-element bf16 sampling on the host.
+    """
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=HIDDEN, intermediate_size=MLP, num_hidden_layers=layers,
+                      num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=DIM, rope_theta=THETA,
+                      max_position_embeddings=TOTAL)
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("meta"):
+            model = LlamaForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(previous)
+    model = model.to_empty(device=device).eval()
+    gen = torch.Generator(device=device).manual_seed(seed)
+    with torch.no_grad():
+        for name, param in model.named_parameters():
+            if name.endswith("norm.weight"):
+                param.fill_(1.0)
+                continue
+            flat = param.view(-1)
+            for start in range(0, flat.numel(), 1 << 26):
+                chunk = flat[start:start + (1 << 26)]
+                chunk.copy_(torch.empty(chunk.numel(), device=device).normal_(0.0, 0.02, generator=gen))
+        rotary = model.model.rotary_emb
+        inv_freq, scaling = rotary.compute_default_rope_parameters(cfg, device)
+        rotary.inv_freq = inv_freq.to(device=device, dtype=torch.float32)
+        rotary.original_inv_freq = rotary.inv_freq.clone()
+        rotary.attention_scaling = scaling
+    model.set_attn_implementation("sdpa")
+    return model
+
+
+def make_request(device, layers=LAYERS):
+    """Synthetic stale cache (K/V ~ N(0,1), seed 1) and the c3 edit."""
+    from kv_cache_repair_amd.cache import cache_from_tensors
+
+    gen = torch.Generator(device=device).manual_seed(1)
+    pairs = [(torch.randn(1, HKV, TOTAL, DIM, device=device, generator=gen, dtype=torch.bfloat16),
+              torch.randn(1, HKV, TOTAL, DIM, device=device, generator=gen, dtype=torch.bfloat16))
+             for _ in range(layers)]
+    old_ids = torch.randint(0, VOCAB, (1, TOTAL), device=device, generator=gen)
+    # keep the shared prefix exactly DELETE_AT tokens long
+    old_ids[0, DELETE_AT] = (old_ids[0, DELETE_AT + DELETE_SPAN] + 1) % VOCAB
+    new_ids = torch.cat((old_ids[:, :DELETE_AT], old_ids[:, DELETE_AT + DELETE_SPAN:]), dim=1)
+    return cache_from_tensors(pairs), old_ids, new_ids
+
+
+# ----------------------------------------------------------------------------- our stage
+def hip_stage(shim, old, old_ids, new_ids, intervals):
+    from kv_cache_repair_amd.cache import build_halo_cache
+    from kv_cache_repair_amd.kernels.packed_cache import packed_refresh_owned_
+
+    cache, _ = build_halo_cache(shim, old, old_ids, new_ids, 0)
+    packed_refresh_owned_(shim, cache, new_ids, intervals)
+    return cache
+
+
+class KernelTimer:
+    """Brackets every libkvrepair launch with HIP events on the launching stream."""
+
+    NAMES = ("kvr_shift_cache_build", "kvr_indexed_scatter_kv", "kvr_packed_causal_attention",
+             "kvr_rope_delta_rotate")
+
+    def __init__(self):
+        from kv_cache_repair_amd import _native
+
+        self.lib = _native.lib()
+        self.original = {n: getattr(self.lib, n) for n in self.NAMES}
+        self.events: dict[str, list] = {n: [] for n in self.NAMES}
+        self.active = False
+
+    def install(self):
+        for name, fn in self.original.items():
+            setattr(self.lib, name, self._wrap(name, fn))
+
+    def uninstall(self):
+        for name, fn in self.original.items():
+            setattr(self.lib, name, fn)
+
+    def _wrap(self, name, fn):
+        def call(*args):
+            if not self.active:
+                return fn(*args)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            status = fn(*args)
+            end.record()
+            self.events[name].append((start, end))
+            return status
+        return call
+
+    def reset(self):
+        self.events = {n: [] for n in self.NAMES}
+
+    def summary(self, steps):
+        out = {}
+        for name, pairs in self.events.items():
+            if pairs:
+                times = [s.elapsed_time(e) * 1000.0 for s, e in pairs]  # us
+                out[name] = {"launches_per_step": len(times) / steps, "avg_us": sum(times) / len(times),
+                             "total_us_per_step": sum(times) / steps}
+        return out
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        out = fn()
+        torch.cuda.synchronize()
+        del out
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = fn()
+        del out
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1000.0 / steps
+
+
+# ----------------------------------------------------------------------------- reference stage (same GPU)
+def reference_stage(model, old, old_ids, new_ids, intervals):
+    """The reference's eager path on this GPU: build_halo_cache with the per-layer
+    rotate chain and cats (cache.py:103-144), clone_cache, boolean mask and
+    index_copy_ + HF sdpa_attention_forward per layer (packed_cache.py:179-298)."""
+    import copy
+
+    from transformers.cache_utils import Cache, DynamicLayer
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    from kv_cache_repair_amd.cache import cache_from_tensors
+
+    base = model.model
+    name = "bench_reference_packed_sdpa"
+    if name not in ALL_ATTENTION_FUNCTIONS:
+        def attend(module, q, k, v, mask, *, scaling=None, dropout=0.0, bench_mask=None, **kw):
+            return sdpa_attention_forward(module, q, k, v, bench_mask, dropout=0.0, scaling=scaling,
+                                          is_causal=False)
+        ALL_ATTENTION_FUNCTIONS.register(name, attend)
+
+    # build_halo_cache: host alignment, prefix clone, rotate chain, cats
+    old_l = [int(x) for x in old_ids[0].tolist()]
+    new_l = [int(x) for x in new_ids[0].tolist()]
+    prefix = 0
+    while prefix < min(len(old_l), len(new_l)) and old_l[prefix] == new_l[prefix]:
+        prefix += 1
+    suffix = 0
+    while suffix < min(len(old_l), len(new_l)) - prefix and old_l[-1 - suffix] == new_l[-1 - suffix]:
+        suffix += 1
+    shift = (len(new_l) - suffix) - (len(old_l) - suffix)
+    ots = len(old_l) - suffix
+    shifted = []
+    for layer in old.layers:
+        k, v = layer.keys, layer.values
+        pk, pv = k[:, :, :prefix].clone(), v[:, :, :prefix].clone()
+        tail = k[:, :, ots:]
+        pos = torch.full((1, tail.shape[2]), shift, dtype=torch.long, device=tail.device)
+        cos, sin = base.rotary_emb(tail, pos)
+        cos, sin = cos.unsqueeze(1).to(tail.dtype), sin.unsqueeze(1).to(tail.dtype)
+        half = tail.shape[-1] // 2
+        rot = torch.cat((-tail[..., half:], tail[..., :half]), dim=-1)
+        nk = torch.cat((pk, tail * cos + rot * sin), dim=2)
+        nv = torch.cat((pv, v[:, :, ots:].clone()), dim=2)
+        shifted.append((torch.cat((torch.empty_like(nk[:, :, :0]), nk), dim=2),
+                        torch.cat((torch.empty_like(nv[:, :, :0]), nv), dim=2)))  # DynamicLayer.update cat
+    # packed_interval_repair (sdpa + torch writeback)
+    selected = [p for s, e in intervals for p in range(s, e)]
+    positions = torch.tensor(selected, dtype=torch.long, device=new_ids.device)
+    length = new_ids.shape[1]
+    mask = (torch.arange(length, device=new_ids.device)[None, :] <= positions[:, None])[None, None]
+    output = cache_from_tensors([(k.clone(), v.clone()) for k, v in shifted])
+
+    class _Layer(DynamicLayer):
+        def __init__(self, k, v):
+            super().__init__()
+            self.keys, self.values, self.is_initialized = k, v, True
+            self.dtype, self.device = k.dtype, k.device
+
+        def update(self, ks, vs, *a, **kw):
+            self.keys.index_copy_(2, positions, ks)
+            self.values.index_copy_(2, positions, vs)
+            return self.keys, self.values
+
+        def get_mask_sizes(self, query_length):
+            return length, 0
+
+    config = copy.deepcopy(base.config)
+    config._attn_implementation = name
+    view = copy.copy(base)
+    view._modules = base._modules.copy()
+    view.config = config
+    layers = []
+    for original in base.layers:
+        layer = copy.copy(original)
+        layer._modules = original._modules.copy()
+        attn = copy.copy(original.self_attn)
+        attn._modules = original.self_attn._modules.copy()
+        attn.config = config
+        layer._modules["self_attn"] = attn
+        layers.append(layer)
+    view._modules["layers"] = torch.nn.ModuleList(layers)
+    cache = Cache(layers=[_Layer(l.keys, l.values) for l in output.layers])
+    view(input_ids=new_ids.index_select(1, positions), position_ids=positions[None], past_key_values=cache,
+         use_cache=True, bench_mask=mask)
+    return output
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+def cpu_baseline(layers_sample: int, repeats: int = 10) -> dict:
+    """The oracle's torch restatement of the reference stage (rotate chain +
+    packed SDPA forward), timed on this host's CPU cores over the first
+    ``layers_sample`` layers of the c3 workload (median of ``repeats`` runs)
+    and scaled to 32 layers."""
+    from oracle import reference_path as ref
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        model = make_model("cpu", layers=layers_sample, seed=1)
+        old, old_ids, new_ids = make_request("cpu", layers=layers_sample)
+        intervals = c3_intervals()
+        ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)  # warm-up (allocator, kernels)
+        samples = []
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)
+            samples.append((time.perf_counter() - t0) * 1000.0)
+        per_sample_ms = sorted(samples)[len(samples) // 2]
+    finally:
+        torch.set_num_threads(previous)
+    cpu_name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": per_sample_ms * LAYERS / layers_sample, "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"oracle torch restatement of the reference stage (eager rotate chain, clone, boolean mask, "
+                      f"index_copy_, HF sdpa) on the first {layers_sample} of 32 layers of the c3 workload, bf16, "
+                      f"median of {repeats} runs after one warm-up, scaled x{LAYERS / layers_sample:g} to "
+                      f"32 layers",
+            "cpu": cpu_name}
+
+
+# ----------------------------------------------------------------------------- main
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--cpu-layers", type=int, default=4, help="layers in the bounded CPU-baseline sample")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-reference", action="store_true", help="skip the same-GPU reference stage")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: this build runs on a single GPU (--gpus {args.gpus} requested). "
+              f"Multi-GPU sharding is a design note only.", file=sys.stderr)
+        return 2
+    if args.steps <= 0 or args.warmup < 0:
+        parser.error("steps must be positive and warmup nonnegative")
+    if not torch.cuda.is_available():
+        parser.error("bench.py needs a GPU")
+
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.cache import OperatorShim, rope_delta_rotate_
+
+    _native.lib()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    model = make_model(device)
+    shim = OperatorShim(model)
+    old, old_ids, new_ids = make_request(device)
+    intervals = c3_intervals()
+    positions = [p for s, e in intervals for p in range(s, e)]
+
+    # correctness gate (untimed): rotated/copied rows bit-exact, refreshed rows close
+    ours = hip_stage(shim, old, old_ids, new_ids, intervals)
+    checks = {}
+    if not args.no_reference:
+        theirs = reference_stage(model, old, old_ids, new_ids, intervals)
+        keep = torch.ones(new_ids.shape[1], dtype=torch.bool, device=device)
+        keep[positions] = False
+        bit_exact, max_abs, min_cos = True, 0.0, 1.0
+        for a_l, b_l in zip(ours.layers, theirs.layers):
+            for a, b in ((a_l.keys, b_l.keys), (a_l.values, b_l.values)):
+                bit_exact &= bool(torch.equal(a[:, :, keep].view(torch.int16), b[:, :, keep].view(torch.int16)))
+                sa, sb = a[:, :, positions].float(), b[:, :, positions].float()
+                max_abs = max(max_abs, (sa - sb).abs().max().item())
+                cos = torch.nn.functional.cosine_similarity(sa.reshape(-1, DIM), sb.reshape(-1, DIM), dim=-1)
+                min_cos = min(min_cos, cos.min().item())
+        checks = {"unselected_rows_bit_exact_vs_reference": bit_exact, "selected_rows_max_abs": max_abs,
+                  "selected_rows_min_cos": min_cos}
+        del theirs
+    del ours
+    torch.cuda.synchronize()
+
+    timer = KernelTimer()
+    timer.install()
+    step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals)  # noqa: E731
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.active = True
+    ms = time_steps(step, args.steps, 0)
+    timer.active = False
+    torch.cuda.synchronize()
+    kernels = timer.summary(args.steps)
+
+    # rotate-only launch over the same 32 suffix K views (BASELINE "rotate GB/s")
+    suffix = TOTAL - DELETE_AT - DELETE_SPAN
+    keys = [l.keys[:, :, DELETE_AT + DELETE_SPAN:] for l in old.layers]
+    outs = [torch.empty(1, HKV, suffix, DIM, dtype=torch.bfloat16, device=device) for _ in keys]
+    inv = model.model.rotary_emb.inv_freq.to(device=device, dtype=torch.float32).contiguous()
+    for _ in range(3):
+        rope_delta_rotate_(keys, outs, -DELETE_SPAN, inv)
+    torch.cuda.synchronize()
+    timer.reset()
+    timer.active = True
+    for _ in range(20):
+        rope_delta_rotate_(keys, outs, -DELETE_SPAN, inv)
+    timer.active = False
+    torch.cuda.synchronize()
+    rotate = timer.summary(20)["kvr_rope_delta_rotate"]
+    timer.uninstall()
+    del outs
+
+    reference = None
+    if not args.no_reference:
+        ref_ms = time_steps(lambda: reference_stage(model, old, old_ids, new_ids, intervals), args.steps,
+                            max(1, args.warmup))
+        reference = {"ms_per_step": ref_ms, "speedup": ref_ms / ms,
+                     "what": "reference eager path on the same GPU: per-layer rotate chain + cats, clone_cache, "
+                             "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv"}
+
+    # algorithmic bytes (one launch)
+    esz = 2
+    rotate_bytes = 2 * LAYERS * HKV * suffix * DIM * esz
+    build_bytes = 2 * 2 * LAYERS * HKV * (DELETE_AT + suffix) * DIM * esz
+    max_pos = max(positions)
+    attn_bytes = (2 * len(positions) * HQ * DIM + 2 * HKV * (max_pos + 1) * DIM) * esz
+    attn_flops = 4 * HQ * DIM * sum(p + 1 for p in positions)
+    scatter_bytes = 2 * 2 * HKV * len(positions) * DIM * esz
+    per_kernel = {
+        "kvr_shift_cache_build": build_bytes, "kvr_packed_causal_attention": attn_bytes,
+        "kvr_indexed_scatter_kv": scatter_bytes}
+    for name, b in per_kernel.items():
+        if name in kernels:
+            kernels[name]["algorithmic_bytes"] = b
+            kernels[name]["achieved_GBps"] = b / (kernels[name]["avg_us"] * 1e3)
+    kernels["kvr_packed_causal_attention"]["achieved_TFLOPs"] = \
+        attn_flops / (kernels["kvr_packed_causal_attention"]["avg_us"] * 1e6)
+    dominant = max(per_kernel, key=lambda n: kernels.get(n, {}).get("total_us_per_step", 0.0))
+    achieved = kernels[dominant]["achieved_GBps"]
+    roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                "avg_launch_us": kernels[dominant]["avg_us"], "algorithmic_bytes_per_launch": per_kernel[dominant]}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_layers)
+    line = {
+        "metric": METRIC, "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init 8B-shaped Llama, K/V ~ N(0,1), random ids)",
+        "config": {"workload": "c3: 8B-shaped Llama, 8192-token cache, delete 512 @2048, 64-token budget in 16x4",
+                   "layers": LAYERS, "kv_heads": HKV, "q_heads": HQ, "head_dim": DIM, "cache_tokens": TOTAL,
+                   "edited_tokens": TOTAL - DELETE_SPAN, "suffix_rows": suffix, "shift": -DELETE_SPAN,
+                   "budget_rows": len(positions), "intervals": intervals},
+        "rotate_GBps": rotate_bytes / (rotate["avg_us"] * 1e3),
+        "rotate": {"avg_us": rotate["avg_us"], "algorithmic_bytes": rotate_bytes,
+                   "frac_of_peak": rotate_bytes / (rotate["avg_us"] * 1e3) / HBM_PEAK_GBPS},
+        "kernels": kernels, "roofline": roofline, "reference_same_gpu": reference, "checks": checks,
+        "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

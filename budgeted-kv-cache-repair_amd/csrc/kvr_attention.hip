@@ -6,33 +6,41 @@
 // and indexed_causal_attention (indexed_attention.py:207-241).
 //
 // Work decomposition (host schedule, kvr_attention_schedule):
-//   selected rows are cut into row tiles of 16 rows; tile t needs keys
-//   [0, pos[last row of t] + 1), cut into chunks of KC keys. One work item is
-//   (tile, chunk). The grid is (work item, kv_head * head_groups); the
-//   work-item index runs over blockIdx.y so that all blocks of one KV head land
-//   on the same XCD (blocks are dealt to the 8 XCDs round-robin by linear id)
-//   and that head's K/V stays in one L2.
-// Tiles with one chunk write the final output; tiles with several chunks write
-// fp32 partials (running max m in the log2 domain, sum l, unnormalised O) and a
-// merge kernel combines them.
+//   selected rows are cut into groups of 64 (four tiles of 16 rows); group g
+//   needs keys [0, pos[last row of g] + 1), cut into chunks of KC keys. One
+//   block handles one (KV head, head group, row group, key chunk): it stages
+//   the chunk's K/V once in LDS, 64 keys at a time, double-buffered, and each
+//   of its four waves attends one row tile (QT query heads x 16 rows) to it.
+//   Grid x = KV head x head group, so every block of one KV head lands on the
+//   same XCD (blocks are dealt round-robin over the 8 XCDs by linear id) and
+//   that head's K/V and partials stay in one L2.
+// Groups with one chunk write the final output; groups with several chunks
+// write fp32 partials (running max m in the log2 domain, sum l, unnormalised
+// O) that a merge kernel combines.
 #include "kvr_internal.h"
 
 #include <math.h>
 #include <string.h>
 
+#include <utility>
+
 namespace kvr {
 namespace {
 
 constexpr int32_t kMagic = 0x4B565253;  // "KVRS"
-constexpr int32_t kVersion = 1;
+constexpr int32_t kVersion = 2;
 constexpr int kHeader = 16;
-constexpr int kRowTile = 16;  // selected rows per tile (MFMA N dimension)
+constexpr int kRowTile = 16;               // rows per MFMA tile
+constexpr int kTilesPerGroup = 4;          // one wave per tile
+constexpr int kGroupRows = kRowTile * kTilesPerGroup;
+constexpr int kSub = 64;                   // keys per LDS sub-tile
+constexpr int kMaxChunksPerGroup = 1024;   // merge weights fit in LDS
 
 enum Header {
     H_MAGIC = 0,
     H_VERSION,
     H_NSEL,
-    H_NTILES,
+    H_NGROUPS,
     H_KC,
     H_NWORK,
     H_QT,
@@ -44,12 +52,11 @@ enum Header {
     H_NMULTI,
     H_NKEYS,
     H_DTYPE,
-    H_RESERVED
+    H_MAXCHUNKS
 };
 enum Kind { KIND_GENERIC = 0, KIND_MFMA = 1 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct AttnArgs {
     const char* q;
@@ -59,15 +66,15 @@ struct AttnArgs {
     int64_t qs[3], ks[3], vs[3], os[3];  // {head,row,dim} element strides
     const int64_t* positions;
     const int32_t* sched;  // device schedule
-    float* ws_ml;          // [Hq][n_work][16] (m, l)
-    float* ws_o;           // [Hq][n_work][16][D]
+    float* ws_ml;          // [Hq][n_work][64] (m, l)
+    float* ws_o;           // [Hq][n_work][64][D]
     int64_t n_sel;
     int64_t n_keys;
     int32_t n_q_heads;
     int32_t group;  // G = Hq / Hkv
-    int32_t qt;     // query heads per block
+    int32_t qt;     // query heads per wave
     int32_t n_head_groups;
-    int32_t n_tiles;
+    int32_t n_groups;
     int32_t n_work;
     int32_t kc;
     int32_t head_dim;
@@ -75,8 +82,15 @@ struct AttnArgs {
 };
 
 // Schedule accessors (device or host pointer to the same int32 layout).
-__host__ __device__ inline const int32_t* tile_table(const int32_t* s) { return s + kHeader; }
-__host__ __device__ inline const int32_t* work_table(const int32_t* s) { return s + kHeader + 2 * s[H_NTILES]; }
+__host__ __device__ inline const int32_t* group_table(const int32_t* s) { return s + kHeader; }
+__host__ __device__ inline const int32_t* work_table(const int32_t* s) { return s + kHeader + 2 * s[H_NGROUPS]; }
+
+// Causal key limit (exclusive) of rows [first, first + count) clipped to n_sel.
+__device__ inline int64_t rows_kmax(const AttnArgs& a, int64_t first, int64_t count) {
+    if (first >= a.n_sel) return 0;
+    const int64_t last = (first + count - 1 < a.n_sel) ? first + count - 1 : a.n_sel - 1;
+    return a.positions[last] + 1;
+}
 
 // ===========================================================================
 // MFMA kernel
@@ -84,41 +98,74 @@ __host__ __device__ inline const int32_t* work_table(const int32_t* s) { return 
 template <typename T> struct mma_t;
 template <> struct mma_t<bf16_t> {
     typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    typedef __bf16 scalar;
     __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
-    __device__ static inline __bf16 cvt(float x) { return static_cast<__bf16>(x); }
-    __device__ static inline float back(__bf16 x) { return static_cast<float>(x); }
+    __device__ static inline scalar cvt(float x) { return static_cast<scalar>(x); }
+    __device__ static inline float back(scalar x) { return static_cast<float>(x); }
 };
 template <> struct mma_t<f16_t> {
     typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 scalar;
     __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
-    __device__ static inline _Float16 cvt(float x) { return static_cast<_Float16>(x); }
-    __device__ static inline float back(_Float16 x) { return static_cast<float>(x); }
+    __device__ static inline scalar cvt(float x) { return static_cast<scalar>(x); }
+    __device__ static inline float back(scalar x) { return static_cast<float>(x); }
 };
 
-constexpr int kMfmaThreads = 256;  // 4 waves
-constexpr int kWaves = 4;
-constexpr int kSub = 64;                  // keys per wave per iteration
-constexpr int kIterKeys = kWaves * kSub;  // keys staged per iteration
-constexpr int kPad = 8;                   // elements of row padding in LDS
+constexpr int kMfmaThreads = 256;  // 4 waves, one per row tile
+constexpr int kPad = 8;            // elements of LDS row padding (16 bytes)
 
 template <int D>
 struct MfmaSmem {
-    static constexpr int ks_stride = D + kPad;          // Ks[key][d]
-    static constexpr int vt_stride = kIterKeys + kPad;  // Vt[d][key]
-    static constexpr int ks_elems = kIterKeys * ks_stride;
-    static constexpr int vt_elems = D * vt_stride;
-    static constexpr int stage_bytes = (ks_elems + vt_elems) * 2;
-    static constexpr int red_bytes = kWaves * 4 * kRowTile * D * 4 + kWaves * 4 * kRowTile * 2 * 4;
-    static constexpr int bytes = stage_bytes > red_bytes ? stage_bytes : red_bytes;
+    static constexpr int stride = D + kPad;          // elements per staged key row
+    static constexpr int tile_elems = kSub * stride;  // one K or V sub-tile
+    static constexpr int bytes = 2 /*buffers*/ * 2 /*K,V*/ * tile_elems * 2;
+    static constexpr int chunks = kSub * D / 8;              // 16-byte pieces per sub-tile
+    static constexpr int per_thread = chunks / kMfmaThreads;  // per tensor
 };
 
-// QT query heads (query tiles of 16 rows) per wave; every wave of the block
-// owns a different 64-key slice of each 256-key iteration.
-template <typename T, int D, int QT, bool PRECISE_P>
+// Global -> register prefetch of one 64-key K/V sub-tile (zero beyond `end`).
+template <int D>
+__device__ inline void load_subtile(const AttnArgs& a, const char* kbase, const char* vbase, int64_t key0,
+                                    int64_t end, int tid, u32x4* kr, u32x4* vr) {
+    using S = MfmaSmem<D>;
+    constexpr int C8 = D / 8;
+#pragma unroll
+    for (int p = 0; p < S::per_thread; ++p) {
+        const int cid = tid + p * kMfmaThreads;
+        const int kk = cid / C8;
+        const int c8 = cid - kk * C8;
+        const int64_t key = key0 + kk;
+        kr[p] = u32x4{0u, 0u, 0u, 0u};
+        vr[p] = u32x4{0u, 0u, 0u, 0u};
+        if (key < end) {
+            kr[p] = *reinterpret_cast<const u32x4*>(kbase + (key * a.ks[1] + 8 * c8) * 2);
+            vr[p] = *reinterpret_cast<const u32x4*>(vbase + (key * a.vs[1] + 8 * c8) * 2);
+        }
+    }
+}
+
+template <int D>
+__device__ inline void store_subtile(uint16_t* Ks, uint16_t* Vs, int tid, const u32x4* kr, const u32x4* vr) {
+    using S = MfmaSmem<D>;
+    constexpr int C8 = D / 8;
+#pragma unroll
+    for (int p = 0; p < S::per_thread; ++p) {
+        const int cid = tid + p * kMfmaThreads;
+        const int kk = cid / C8;
+        const int c8 = cid - kk * C8;
+        *reinterpret_cast<u32x4*>(Ks + kk * S::stride + 8 * c8) = kr[p];
+        *reinterpret_cast<u32x4*>(Vs + kk * S::stride + 8 * c8) = vr[p];
+    }
+}
+
+// Each wave: QT query heads x the 16 rows of its tile. S^T = K Q^T (keys on the
+// MFMA M axis) so each lane holds 4 keys of one query, and the PV MFMA takes
+// P^T straight from those registers: O^T += V^T P^T.
+template <typename T, int D, int QT>
 __global__ void __launch_bounds__(kMfmaThreads)
 attn_mfma_kernel(AttnArgs a) {
     using M = mma_t<T>;
@@ -127,41 +174,38 @@ attn_mfma_kernel(AttnArgs a) {
     constexpr int DS = D / 32;  // k-steps of the QK^T MFMA
     constexpr int DT = D / 16;  // d tiles of the PV MFMA
     extern __shared__ __align__(16) char smem[];
-    uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
-    uint16_t* Vt = Ks + S::ks_elems;
+    uint16_t* lds = reinterpret_cast<uint16_t*>(smem);  // [buf][K|V][64][stride]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int lq = lane & 15;  // query column within the tile
+    const int lq = lane & 15;  // query row within the tile
     const int lj = lane >> 4;  // lane group 0..3
 
     const int32_t* wk = work_table(a.sched);
     const int work = blockIdx.y;
-    const int tile = wk[2 * work];
+    const int grp = wk[2 * work];
     const int chunk = wk[2 * work + 1];
+    const int n_chunks = group_table(a.sched)[2 * grp + 1];
     const int kv_head = blockIdx.x / a.n_head_groups;
     const int hg = blockIdx.x - kv_head * a.n_head_groups;
-    const int32_t* tt = tile_table(a.sched);
-    const int n_chunks = tt[2 * tile + 1];
-
-    const int64_t row0 = static_cast<int64_t>(tile) * kRowTile;
-    const int64_t last_row = (row0 + kRowTile - 1 < a.n_sel) ? row0 + kRowTile - 1 : a.n_sel - 1;
-    const int64_t kmax = a.positions[last_row] + 1;  // keys [0, kmax) needed by the tile
-    const int64_t key_begin = static_cast<int64_t>(chunk) * a.kc;
-    const int64_t key_end_raw = key_begin + a.kc;
-    const int64_t key_end = key_end_raw < kmax ? key_end_raw : kmax;
-    const int n_iter = static_cast<int>((key_end - key_begin + kIterKeys - 1) / kIterKeys);
-
-    // Per-lane query row and its causal limit.
-    const int64_t my_row = row0 + lq;
-    const int64_t my_pos = (my_row < a.n_sel) ? a.positions[my_row] : int64_t(-1);
     const int q_head0 = kv_head * a.group + hg * QT;
+
+    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
+    const int64_t key_begin = static_cast<int64_t>(chunk) * a.kc;
+    const int64_t group_kmax = rows_kmax(a, group_row0, kGroupRows);
+    const int64_t key_end = (key_begin + a.kc < group_kmax) ? key_begin + a.kc : group_kmax;
+    const int n_sub = static_cast<int>((key_end - key_begin + kSub - 1) / kSub);
+
+    const int64_t tile_row0 = group_row0 + wave * kRowTile;
+    const int64_t tile_kmax = rows_kmax(a, tile_row0, kRowTile);  // 0 for an empty tile
+    const int64_t my_row = tile_row0 + lq;
+    const int64_t my_pos = (my_row < a.n_sel) ? a.positions[my_row] : int64_t(-1);
 
     // Q fragments (B operand of S^T = K Q^T): lane holds q[row][32*ds + 8*lj .. +8].
     v8 qf[QT][DS];
 #pragma unroll
-    for (int h = 0; h < QT; ++h) {
+    for (int h = 0; h < QT; ++h)
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
             u32x4 raw = {0u, 0u, 0u, 0u};
@@ -171,7 +215,6 @@ attn_mfma_kernel(AttnArgs a) {
             }
             qf[h][ds] = __builtin_bit_cast(v8, raw);
         }
-    }
 
     f32x4 o[QT][DT];
     float m_run[QT], l_run[QT];
@@ -185,32 +228,21 @@ attn_mfma_kernel(AttnArgs a) {
 
     const char* kbase = a.k + static_cast<int64_t>(kv_head) * a.ks[0] * 2;
     const char* vbase = a.v + static_cast<int64_t>(kv_head) * a.vs[0] * 2;
-    constexpr int C8 = D / 8;  // 16-byte chunks per row
+    u32x4 kr[S::per_thread], vr[S::per_thread];
+    if (n_sub > 0) {
+        load_subtile<D>(a, kbase, vbase, key_begin, key_end, tid, kr, vr);
+        store_subtile<D>(lds, lds + S::tile_elems, tid, kr, vr);
+    }
 
-    for (int it = 0; it < n_iter; ++it) {
-        const int64_t it_key0 = key_begin + static_cast<int64_t>(it) * kIterKeys;
-        // ---- stage K (row-major) and V (transposed) for 256 keys ----
-#pragma unroll 4
-        for (int cid = tid; cid < kIterKeys * C8; cid += kMfmaThreads) {
-            const int kk = cid / C8;
-            const int c8 = cid - kk * C8;
-            const int64_t key = it_key0 + kk;
-            u32x4 kr = {0u, 0u, 0u, 0u}, vr = {0u, 0u, 0u, 0u};
-            if (key < key_end) {
-                kr = *reinterpret_cast<const u32x4*>(kbase + (key * a.ks[1] + 8 * c8) * 2);
-                vr = *reinterpret_cast<const u32x4*>(vbase + (key * a.vs[1] + 8 * c8) * 2);
-            }
-            *reinterpret_cast<u32x4*>(Ks + kk * S::ks_stride + 8 * c8) = kr;
-            uint16_t vv[8];
-            __builtin_memcpy(vv, &vr, 16);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) Vt[(8 * c8 + e) * S::vt_stride + kk] = vv[e];
-        }
-        __syncthreads();
+    for (int s = 0; s < n_sub; ++s) {
+        const int64_t sub_key0 = key_begin + static_cast<int64_t>(s) * kSub;
+        const bool more = s + 1 < n_sub;
+        if (more) load_subtile<D>(a, kbase, vbase, sub_key0 + kSub, key_end, tid, kr, vr);
+        __syncthreads();  // sub-tile s is staged; buffer (s+1)%2 is free
+        const uint16_t* Kb = lds + (s & 1) * 2 * S::tile_elems;
+        const uint16_t* Vb = Kb + S::tile_elems;
 
-        const int64_t sub_key0 = it_key0 + wave * kSub;
-        if (sub_key0 < key_end) {
-            const uint16_t* Kw = Ks + wave * kSub * S::ks_stride;
+        if (sub_key0 < tile_kmax) {
             // ---- S^T = K Q^T for 4 key tiles of 16 ----
             f32x4 st[QT][4];
 #pragma unroll
@@ -218,21 +250,20 @@ attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt) st[h][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
+            for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int ds = 0; ds < DS; ++ds) {
                     const u32x4 raw =
-                        *reinterpret_cast<const u32x4*>(Kw + (16 * kt + lq) * S::ks_stride + 32 * ds + 8 * lj);
+                        *reinterpret_cast<const u32x4*>(Kb + (16 * kt + lq) * S::stride + 32 * ds + 8 * lj);
                     const v8 kf = __builtin_bit_cast(v8, raw);
 #pragma unroll
                     for (int h = 0; h < QT; ++h) st[h][kt] = M::mma(kf, qf[h][ds], st[h][kt]);
                 }
-            }
             // ---- online softmax (log2 domain), mask key > pos ----
             v8 p_hi[QT][2], p_lo[QT][2];
 #pragma unroll
             for (int h = 0; h < QT; ++h) {
-                float s[4][4];
+                float sc[4][4];
                 float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt)
@@ -240,7 +271,7 @@ attn_mfma_kernel(AttnArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         const int64_t key = sub_key0 + 16 * kt + 4 * lj + i;
                         const float x = (key <= my_pos) ? st[h][kt][i] * a.scale_log2 : -INFINITY;
-                        s[kt][i] = x;
+                        sc[kt][i] = x;
                         mx = fmaxf(mx, x);
                     }
                 mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -254,54 +285,53 @@ attn_mfma_kernel(AttnArgs a) {
                 for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float p = exp2f(s[kt][i] - m_use);
-                        s[kt][i] = p;
+                        const float p = exp2f(sc[kt][i] - m_use);
+                        sc[kt][i] = p;
                         psum += p;
                     }
                 l_run[h] = l_run[h] * alpha + psum;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
+                for (int half = 0; half < 2; ++half)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float x0 = s[2 * half][i];
-                        const float x1 = s[2 * half + 1][i];
+                        const float x0 = sc[2 * half][i];
+                        const float x1 = sc[2 * half + 1][i];
                         const auto h0 = M::cvt(x0);
                         const auto h1 = M::cvt(x1);
                         p_hi[h][half][i] = h0;
                         p_hi[h][half][4 + i] = h1;
-                        if (PRECISE_P) {
-                            p_lo[h][half][i] = M::cvt(x0 - M::back(h0));
-                            p_lo[h][half][4 + i] = M::cvt(x1 - M::back(h1));
-                        }
+                        p_lo[h][half][i] = M::cvt(x0 - M::back(h0));
+                        p_lo[h][half][4 + i] = M::cvt(x1 - M::back(h1));
                     }
-                }
             }
-            // ---- O^T += V^T P^T ----
-            const uint16_t* Vw = Vt + wave * kSub;
+            // ---- O^T += V^T P^T: A = V^T gathered from the row-major tile ----
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
+            for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
-                    const uint16_t* vrow = Vw + (16 * dt + lq) * S::vt_stride + 32 * half + 4 * lj;
-                    const u32x2 r0 = *reinterpret_cast<const u32x2*>(vrow);
-                    const u32x2 r1 = *reinterpret_cast<const u32x2*>(vrow + 16);
-                    const u32x4 raw = {r0[0], r0[1], r1[0], r1[1]};
-                    const v8 vf = __builtin_bit_cast(v8, raw);
+                    const uint16_t* col = Vb + (32 * half + 4 * lj) * S::stride + 16 * dt + lq;
+                    uint16_t g[8];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        g[i] = col[i * S::stride];
+                        g[4 + i] = col[(16 + i) * S::stride];
+                    }
+                    v8 vf;
+                    __builtin_memcpy(&vf, g, 16);
 #pragma unroll
                     for (int h = 0; h < QT; ++h) {
                         o[h][dt] = M::mma(vf, p_hi[h][half], o[h][dt]);
-                        if (PRECISE_P) o[h][dt] = M::mma(vf, p_lo[h][half], o[h][dt]);
+                        o[h][dt] = M::mma(vf, p_lo[h][half], o[h][dt]);
                     }
                 }
-            }
         }
-        __syncthreads();
+        if (more) store_subtile<D>(lds + ((s + 1) & 1) * 2 * S::tile_elems,
+                                   lds + ((s + 1) & 1) * 2 * S::tile_elems + S::tile_elems, tid, kr, vr);
     }
 
-    // ---- combine the 4 waves of the block through LDS ----
-    // lane partial sums -> per-query sums
+    // ---- epilogue: per-query sums, then final output or fp32 partial ----
 #pragma unroll
     for (int h = 0; h < QT; ++h) {
         float l = l_run[h];
@@ -309,62 +339,27 @@ attn_mfma_kernel(AttnArgs a) {
         l += __shfl_xor(l, 32);
         l_run[h] = l;
     }
-    float* red_o = reinterpret_cast<float*>(smem);                 // [wave][QT][16][D]
-    float* red_ml = red_o + kWaves * QT * kRowTile * D;            // [wave][QT][16][2]
-    if (lj == 0) {
-#pragma unroll
-        for (int h = 0; h < QT; ++h) {
-            red_ml[((wave * QT + h) * kRowTile + lq) * 2 + 0] = m_run[h];
-            red_ml[((wave * QT + h) * kRowTile + lq) * 2 + 1] = l_run[h];
-        }
-    }
-    __syncthreads();
+    if (my_row >= a.n_sel) return;
+    const int r = static_cast<int>(my_row - group_row0);
 #pragma unroll
     for (int h = 0; h < QT; ++h) {
-        float mall = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) mall = fmaxf(mall, red_ml[((w * QT + h) * kRowTile + lq) * 2]);
-        const float m_use = (mall == -INFINITY) ? 0.f : mall;
-        const float sc = exp2f(m_run[h] - m_use);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const f32x4 val = o[h][dt] * sc;
-            *reinterpret_cast<f32x4*>(red_o + ((wave * QT + h) * kRowTile + lq) * D + 16 * dt + 4 * lj) = val;
-        }
-    }
-    __syncthreads();
-
-    // ---- final output (single chunk) or fp32 partial ----
-    for (int e = tid; e < QT * kRowTile * D; e += kMfmaThreads) {
-        const int h = e / (kRowTile * D);
-        const int rem = e - h * (kRowTile * D);
-        const int r = rem / D;
-        const int d = rem - r * D;
-        const int64_t row = row0 + r;
-        if (row >= a.n_sel) continue;
-        float mall = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) mall = fmaxf(mall, red_ml[((w * QT + h) * kRowTile + r) * 2]);
-        const float m_use = (mall == -INFINITY) ? 0.f : mall;
-        float osum = 0.f, lsum = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = red_ml[((w * QT + h) * kRowTile + r) * 2];
-            const float lw = red_ml[((w * QT + h) * kRowTile + r) * 2 + 1];
-            lsum += lw * exp2f(mw - m_use);
-            osum += red_o[((w * QT + h) * kRowTile + r) * D + d];
-        }
         const int q_head = q_head0 + h;
         if (n_chunks == 1) {
-            const float val = osum / lsum;
-            uint16_t* dst = reinterpret_cast<uint16_t*>(a.out);
-            dst[q_head * a.os[0] + row * a.os[1] + d * a.os[2]] = elem<T>::from_float(val);
+            const float inv = 1.f / l_run[h];
+            uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + q_head * a.os[0] + my_row * a.os[1];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    dst[(16 * dt + 4 * lj + i) * a.os[2]] = elem<T>::from_float(o[h][dt][i] * inv);
         } else {
-            const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kRowTile + r;
-            a.ws_o[slot * D + d] = osum;
-            if (d == 0) {
-                a.ws_ml[slot * 2 + 0] = mall;
-                a.ws_ml[slot * 2 + 1] = lsum;
+            const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kGroupRows + r;
+            float* po = a.ws_o + slot * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lj) = o[h][dt];
+            if (lj == 0) {
+                a.ws_ml[slot * 2 + 0] = m_run[h];
+                a.ws_ml[slot * 2 + 1] = l_run[h];
             }
         }
     }
@@ -372,10 +367,10 @@ attn_mfma_kernel(AttnArgs a) {
 
 // ===========================================================================
 // Generic kernel (vector ALU; fp32 / fp16 / bf16, any head_dim <= 256).
-// One 64-thread block per (work item, kv head, head group); thread = query
-// (head h = tid / 16, row r = tid % 16); K/V staged in LDS as fp32.
+// Same work items as the MFMA kernel. 256 threads: thread t owns query
+// (tile t/64, head (t%64)/16, row t%16); K/V staged in LDS as fp32.
 // ===========================================================================
-constexpr int kGenThreads = 64;
+constexpr int kGenThreads = 256;
 constexpr int kGenSub = 32;
 
 template <typename T, int DMAX>
@@ -391,22 +386,22 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
     const int tid = threadIdx.x;
     const int32_t* wk = work_table(a.sched);
     const int work = blockIdx.y;
-    const int tile = wk[2 * work];
+    const int grp = wk[2 * work];
     const int chunk = wk[2 * work + 1];
+    const int n_chunks = group_table(a.sched)[2 * grp + 1];
     const int kv_head = blockIdx.x / a.n_head_groups;
     const int hg = blockIdx.x - kv_head * a.n_head_groups;
-    const int n_chunks = tile_table(a.sched)[2 * tile + 1];
 
-    const int64_t row0 = static_cast<int64_t>(tile) * kRowTile;
-    const int64_t last_row = (row0 + kRowTile - 1 < a.n_sel) ? row0 + kRowTile - 1 : a.n_sel - 1;
-    const int64_t kmax = a.positions[last_row] + 1;
+    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
     const int64_t key_begin = static_cast<int64_t>(chunk) * a.kc;
-    const int64_t key_end = (key_begin + a.kc < kmax) ? key_begin + a.kc : kmax;
+    const int64_t group_kmax = rows_kmax(a, group_row0, kGroupRows);
+    const int64_t key_end = (key_begin + a.kc < group_kmax) ? key_begin + a.kc : group_kmax;
 
-    const int h = tid / kRowTile;
-    const int r = tid - h * kRowTile;
-    const bool live = h < a.qt && (row0 + r) < a.n_sel;
-    const int64_t row = row0 + r;
+    const int tile = tid / 64;
+    const int h = (tid % 64) / kRowTile;
+    const int r = tile * kRowTile + (tid % kRowTile);
+    const int64_t row = group_row0 + r;
+    const bool live = h < a.qt && row < a.n_sel;
     const int64_t pos = live ? a.positions[row] : int64_t(-1);
     const int q_head = kv_head * a.group + hg * a.qt + h;
 
@@ -469,7 +464,7 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
         for (int d = 0; d < DMAX; ++d)
             if (d < D) op[q_head * a.os[0] + row * a.os[1] + d * a.os[2]] = E::from_float(acc[d] / l_run);
     } else {
-        const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kRowTile + r;
+        const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kGroupRows + r;
 #pragma unroll
         for (int d = 0; d < DMAX; ++d)
             if (d < D) a.ws_o[slot * D + d] = acc[d];
@@ -479,40 +474,75 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
 }
 
 // ===========================================================================
-// Merge of multi-chunk tiles: grid (tile, q_head), 256 threads over 16 x D.
+// Merge of multi-chunk groups. Grid (q_head, group, row block of 8 rows).
+// Phase 1 stages per-(row, chunk) weights exp2(m_c - M) and the total l in
+// LDS; phase 2 gives each thread one (row, dim) element to accumulate.
 // ===========================================================================
+constexpr int kMergeThreads = 256;
+constexpr int kMergeRows = 8;
+
 template <typename T>
-__global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     using E = elem<T>;
     using bits = typename E::bits;
-    const int tile = blockIdx.x;
-    const int q_head = blockIdx.y;
-    const int32_t* tt = tile_table(a.sched);
-    const int base = tt[2 * tile];
-    const int n_chunks = tt[2 * tile + 1];
+    extern __shared__ __align__(16) char smem[];
+    const int q_head = blockIdx.x;
+    const int grp = blockIdx.y;
+    const int32_t* gt = group_table(a.sched);
+    const int base = gt[2 * grp];
+    const int n_chunks = gt[2 * grp + 1];
     if (n_chunks <= 1) return;
     const int D = a.head_dim;
-    const int64_t row0 = static_cast<int64_t>(tile) * kRowTile;
-    for (int e = threadIdx.x; e < kRowTile * D; e += 256) {
-        const int r = e / D;
-        const int d = e - r * D;
-        const int64_t row = row0 + r;
+    const int r0 = blockIdx.z * kMergeRows;  // first row (within the group) of this block
+    float* W = reinterpret_cast<float*>(smem);  // [kMergeRows][n_chunks]
+    float* Linv = W + kMergeRows * n_chunks;    // [kMergeRows]
+    const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * kGroupRows;
+
+    // phase 1: 32 lanes per row reduce over chunks
+    const int tr = threadIdx.x / 32;
+    const int tl = threadIdx.x % 32;
+    {
+        const int r = r0 + tr;
+        float mx = -INFINITY;
+        for (int c = tl; c < n_chunks; c += 32)
+            mx = fmaxf(mx, a.ws_ml[(slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2]);
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 32));
+        const float m_use = (mx == -INFINITY) ? 0.f : mx;
+        float l = 0.f;
+        for (int c = tl; c < n_chunks; c += 32) {
+            const int64_t s = (slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2;
+            const float w = exp2f(a.ws_ml[s] - m_use);
+            W[tr * n_chunks + c] = w;
+            l += w * a.ws_ml[s + 1];
+        }
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) l += __shfl_xor(l, off, 32);
+        if (tl == 0) Linv[tr] = 1.f / l;
+    }
+    __syncthreads();
+
+    // phase 2: one (row, d) element per thread-iteration
+    for (int e = threadIdx.x; e < kMergeRows * D; e += kMergeThreads) {
+        const int rr = e / D;
+        const int d = e - rr * D;
+        const int r = r0 + rr;
+        const int64_t row = static_cast<int64_t>(grp) * kGroupRows + r;
         if (row >= a.n_sel) continue;
-        float mall = -INFINITY;
-        for (int c = 0; c < n_chunks; ++c) {
-            const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + base + c) * kRowTile + r;
-            mall = fmaxf(mall, a.ws_ml[slot * 2]);
+        const float* po = a.ws_o + (slot0 + r) * D + d;
+        const float* w = W + rr * n_chunks;
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        int c = 0;
+        for (; c + 4 <= n_chunks; c += 4) {
+            acc0 += w[c] * po[static_cast<int64_t>(c) * kGroupRows * D];
+            acc1 += w[c + 1] * po[static_cast<int64_t>(c + 1) * kGroupRows * D];
+            acc2 += w[c + 2] * po[static_cast<int64_t>(c + 2) * kGroupRows * D];
+            acc3 += w[c + 3] * po[static_cast<int64_t>(c + 3) * kGroupRows * D];
         }
-        const float m_use = (mall == -INFINITY) ? 0.f : mall;
-        float osum = 0.f, lsum = 0.f;
-        for (int c = 0; c < n_chunks; ++c) {
-            const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + base + c) * kRowTile + r;
-            const float w = exp2f(a.ws_ml[slot * 2] - m_use);
-            lsum += a.ws_ml[slot * 2 + 1] * w;
-            osum += a.ws_o[slot * D + d] * w;
-        }
+        for (; c < n_chunks; ++c) acc0 += w[c] * po[static_cast<int64_t>(c) * kGroupRows * D];
         bits* op = reinterpret_cast<bits*>(a.out);
-        op[q_head * a.os[0] + row * a.os[1] + d * a.os[2]] = E::from_float(osum / lsum);
+        op[q_head * a.os[0] + row * a.os[1] + d * a.os[2]] =
+            E::from_float(((acc0 + acc1) + (acc2 + acc3)) * Linv[rr]);
     }
 }
 
@@ -545,26 +575,26 @@ bool allow_lds(F fn, size_t bytes) {
                                static_cast<int>(bytes)) == hipSuccess;
 }
 
-template <typename T, int D, int QT, bool P>
+template <typename T, int D, int QT>
 int launch_mfma_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
     const size_t smem = MfmaSmem<D>::bytes;
-    static const bool ok = allow_lds(attn_mfma_kernel<T, D, QT, P>, smem);
+    static const bool ok = allow_lds(attn_mfma_kernel<T, D, QT>, smem);
     if (!ok) return KVR_E_LAUNCH_FAILED;
-    attn_mfma_kernel<T, D, QT, P><<<grid, kMfmaThreads, smem, s>>>(a);
+    attn_mfma_kernel<T, D, QT><<<grid, kMfmaThreads, smem, s>>>(a);
     return launch_status();
 }
 
-// P always enters PV as a hi+lo pair (PRECISE_P = true).
 template <typename T, int D>
 int launch_mfma(const AttnArgs& a, int qt, dim3 grid, hipStream_t s) {
-    if (qt == 4) return launch_mfma_inst<T, D, 4, true>(a, grid, s);
-    if (qt == 2) return launch_mfma_inst<T, D, 2, true>(a, grid, s);
-    return launch_mfma_inst<T, D, 1, true>(a, grid, s);
+    if (qt == 4) return launch_mfma_inst<T, D, 4>(a, grid, s);
+    if (qt == 2) return launch_mfma_inst<T, D, 2>(a, grid, s);
+    return launch_mfma_inst<T, D, 1>(a, grid, s);
 }
 
 template <typename T, int DMAX>
 int launch_generic_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
-    const size_t smem = (static_cast<size_t>(2) * kGenSub * DMAX + static_cast<size_t>(kGenSub) * kGenThreads) * sizeof(float);
+    const size_t smem =
+        (static_cast<size_t>(2) * kGenSub * DMAX + static_cast<size_t>(kGenSub) * kGenThreads) * sizeof(float);
     static const bool ok = allow_lds(attn_generic_kernel<T, DMAX>, smem);
     if (!ok) return KVR_E_LAUNCH_FAILED;
     attn_generic_kernel<T, DMAX><<<grid, kGenThreads, smem, s>>>(a);
@@ -582,10 +612,19 @@ int launch_generic(const AttnArgs& a, int dmax, dim3 grid, hipStream_t s) {
 }
 
 template <typename T>
-int launch_merge(const AttnArgs& a, hipStream_t s) {
-    dim3 grid(a.n_tiles, a.n_q_heads);
-    attn_merge_kernel<T><<<grid, 256, 0, s>>>(a);
+int launch_merge(const AttnArgs& a, int max_chunks, hipStream_t s) {
+    const size_t smem = (static_cast<size_t>(kMergeRows) * max_chunks + kMergeRows) * sizeof(float);
+    static const bool ok = allow_lds(attn_merge_kernel<T>, static_cast<size_t>(kMergeRows) *
+                                                               (kMaxChunksPerGroup + 1) * sizeof(float));
+    if (!ok) return KVR_E_LAUNCH_FAILED;
+    dim3 grid(a.n_q_heads, a.n_groups, kGroupRows / kMergeRows);
+    attn_merge_kernel<T><<<grid, kMergeThreads, smem, s>>>(a);
     return launch_status();
+}
+
+int64_t group_kmax_host(const int64_t* positions, int64_t n_sel, int64_t g) {
+    const int64_t last = (g + 1) * kGroupRows - 1 < n_sel ? (g + 1) * kGroupRows - 1 : n_sel - 1;
+    return positions[last] + 1;
 }
 
 }  // namespace
@@ -596,11 +635,10 @@ using namespace kvr;
 extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_sel, int64_t n_keys, int32_t n_q_heads,
                                           int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys,
                                           int32_t* schedule, int64_t capacity) {
+    if (dtype_size(dtype) == 0) return KVR_E_UNSUPPORTED_DTYPE;
     if (n_sel < 0 || n_keys < 0 || n_sel > n_keys) return KVR_E_INVALID_ARGUMENT;
     if (n_keys >= (int64_t(1) << 31) || n_sel >= (int64_t(1) << 31)) return KVR_E_UNSUPPORTED_SHAPE;
-    if (n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads) return KVR_E_UNSUPPORTED_SHAPE;
-    if (head_dim <= 0 || dtype_size(dtype) == 0) return dtype_size(dtype) ? KVR_E_UNSUPPORTED_SHAPE
-                                                                          : KVR_E_UNSUPPORTED_DTYPE;
+    if (n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads || head_dim <= 0) return KVR_E_UNSUPPORTED_SHAPE;
     if (n_sel > 0 && !positions) return KVR_E_NULL_POINTER;
     for (int64_t i = 0; i < n_sel; ++i) {
         if (positions[i] < 0 || positions[i] >= n_keys) return KVR_E_INVALID_ARGUMENT;
@@ -608,46 +646,50 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     }
     const bool mfma = mfma_eligible(dtype, head_dim);
     if (!mfma && generic_dmax(head_dim) == 0) return KVR_E_UNSUPPORTED_SHAPE;
-    if (chunk_keys < 0 || (chunk_keys > 0 && chunk_keys % (mfma ? kIterKeys : kGenSub) != 0))
-        return KVR_E_INVALID_ARGUMENT;
+    if (chunk_keys < 0 || (chunk_keys > 0 && chunk_keys % kSub != 0)) return KVR_E_INVALID_ARGUMENT;
     const int group = n_q_heads / n_kv_heads;
     const int qt = pick_qt(group);
     const int n_head_groups = group / qt;
-    const int64_t n_tiles = (n_sel + kRowTile - 1) / kRowTile;
+    const int64_t n_groups = (n_sel + kGroupRows - 1) / kGroupRows;
+    const int64_t heads = static_cast<int64_t>(n_kv_heads) * n_head_groups;
 
-    // Chunk size: the largest multiple of the iteration size that still gives
-    // at least `target` blocks; tiles whose key range fits in one chunk need
-    // no merge.
-    const int unit = mfma ? kIterKeys : kGenSub;
+    int64_t maxk = kSub;
+    for (int64_t g = 0; g < n_groups; ++g) {
+        const int64_t k = group_kmax_host(positions, n_sel, g);
+        maxk = k > maxk ? k : maxk;
+    }
+    auto chunks_for = [&](int64_t kc) {
+        int64_t blocks = 0, worst = 0;
+        for (int64_t g = 0; g < n_groups; ++g) {
+            const int64_t c = (group_kmax_host(positions, n_sel, g) + kc - 1) / kc;
+            blocks += c;
+            worst = c > worst ? c : worst;
+        }
+        return std::pair<int64_t, int64_t>(blocks, worst);
+    };
+    // Chunk size: the smallest multiple of 64 keys that keeps the grid within
+    // one block per CU (256 CUs, one 4-wave block each); when even unsplit
+    // groups exceed that, groups are not split. A group whose keys fit one
+    // chunk needs no merge.
     int64_t kc = chunk_keys;
     if (kc == 0) {
-        const int64_t target = 512;
-        const int64_t heads = static_cast<int64_t>(n_kv_heads) * n_head_groups;
-        int64_t maxk = unit;
-        for (int64_t t = 0; t < n_tiles; ++t) {
-            const int64_t last = (t + 1) * kRowTile - 1 < n_sel ? (t + 1) * kRowTile - 1 : n_sel - 1;
-            maxk = positions[last] + 1 > maxk ? positions[last] + 1 : maxk;
-        }
-        kc = unit;
-        for (int64_t cand = unit; cand <= ((maxk + unit - 1) / unit) * unit; cand *= 2) {
-            int64_t blocks = 0;
-            for (int64_t t = 0; t < n_tiles; ++t) {
-                const int64_t last = (t + 1) * kRowTile - 1 < n_sel ? (t + 1) * kRowTile - 1 : n_sel - 1;
-                blocks += (positions[last] + 1 + cand - 1) / cand;
+        const int64_t target = 256;
+        const int64_t whole = ((maxk + kSub - 1) / kSub) * kSub;
+        kc = whole;
+        for (int64_t cand = kSub; cand < whole; cand += kSub) {
+            if (chunks_for(cand).first * heads <= target) {
+                kc = cand;
+                break;
             }
-            if (blocks * heads >= target) kc = cand;
         }
-        if (kc > (int64_t(1) << 30)) kc = int64_t(1) << 30;
     }
-    int64_t n_work = 0, n_multi = 0;
-    for (int64_t t = 0; t < n_tiles; ++t) {
-        const int64_t last = (t + 1) * kRowTile - 1 < n_sel ? (t + 1) * kRowTile - 1 : n_sel - 1;
-        const int64_t c = (positions[last] + 1 + kc - 1) / kc;
-        n_work += c;
-        n_multi += c > 1;
-    }
+    while (chunks_for(kc).second > kMaxChunksPerGroup) kc += kSub;
+    const auto counts = chunks_for(kc);
+    const int64_t n_work = counts.first;
     if (n_work > 65535) return KVR_E_UNSUPPORTED_SHAPE;  // grid.y limit
-    const int64_t need = kHeader + 2 * n_tiles + 2 * n_work;
+    int64_t n_multi = 0;
+    for (int64_t g = 0; g < n_groups; ++g) n_multi += (group_kmax_host(positions, n_sel, g) + kc - 1) / kc > 1;
+    const int64_t need = kHeader + 2 * n_groups + 2 * n_work;
     if (!schedule) return need;
     if (capacity < need) return KVR_E_CAPACITY;
     int32_t* h = schedule;
@@ -655,7 +697,7 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     h[H_MAGIC] = kMagic;
     h[H_VERSION] = kVersion;
     h[H_NSEL] = static_cast<int32_t>(n_sel);
-    h[H_NTILES] = static_cast<int32_t>(n_tiles);
+    h[H_NGROUPS] = static_cast<int32_t>(n_groups);
     h[H_KC] = static_cast<int32_t>(kc);
     h[H_NWORK] = static_cast<int32_t>(n_work);
     h[H_QT] = qt;
@@ -667,16 +709,16 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     h[H_NMULTI] = static_cast<int32_t>(n_multi);
     h[H_NKEYS] = static_cast<int32_t>(n_keys);
     h[H_DTYPE] = dtype;
-    int32_t* tiles = h + kHeader;
-    int32_t* works = tiles + 2 * n_tiles;
+    h[H_MAXCHUNKS] = static_cast<int32_t>(counts.second);
+    int32_t* groups = h + kHeader;
+    int32_t* works = groups + 2 * n_groups;
     int64_t w = 0;
-    for (int64_t t = 0; t < n_tiles; ++t) {
-        const int64_t last = (t + 1) * kRowTile - 1 < n_sel ? (t + 1) * kRowTile - 1 : n_sel - 1;
-        const int64_t c = (positions[last] + 1 + kc - 1) / kc;
-        tiles[2 * t] = static_cast<int32_t>(w);
-        tiles[2 * t + 1] = static_cast<int32_t>(c);
+    for (int64_t g = 0; g < n_groups; ++g) {
+        const int64_t c = (group_kmax_host(positions, n_sel, g) + kc - 1) / kc;
+        groups[2 * g] = static_cast<int32_t>(w);
+        groups[2 * g + 1] = static_cast<int32_t>(c);
         for (int64_t i = 0; i < c; ++i, ++w) {
-            works[2 * w] = static_cast<int32_t>(t);
+            works[2 * w] = static_cast<int32_t>(g);
             works[2 * w + 1] = static_cast<int32_t>(i);
         }
     }
@@ -689,7 +731,7 @@ extern "C" int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_
         return KVR_E_BAD_SCHEDULE;
     if (schedule[H_HQ] != n_q_heads || schedule[H_D] != head_dim) return KVR_E_BAD_SCHEDULE;
     if (schedule[H_NMULTI] == 0) return 0;
-    return static_cast<int64_t>(n_q_heads) * schedule[H_NWORK] * kRowTile * (head_dim + 2) * 4;
+    return static_cast<int64_t>(n_q_heads) * schedule[H_NWORK] * kGroupRows * (head_dim + 2) * 4;
 }
 
 extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const void* v, void* out,
@@ -713,8 +755,9 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     if (hs[H_NSEL] != n_sel || hs[H_HQ] != n_q_heads || hs[H_HKV] != n_kv_heads || hs[H_D] != head_dim ||
         hs[H_NKEYS] != n_keys || hs[H_DTYPE] != dtype)
         return KVR_E_BAD_SCHEDULE;
-    if (schedule_len != kHeader + 2 * static_cast<int64_t>(hs[H_NTILES]) + 2 * static_cast<int64_t>(hs[H_NWORK]))
+    if (schedule_len != kHeader + 2 * static_cast<int64_t>(hs[H_NGROUPS]) + 2 * static_cast<int64_t>(hs[H_NWORK]))
         return KVR_E_BAD_SCHEDULE;
+    if (hs[H_MAXCHUNKS] > kMaxChunksPerGroup || hs[H_KC] <= 0 || hs[H_KC] % kSub) return KVR_E_BAD_SCHEDULE;
     const int64_t ws_need = kvr_attention_workspace_bytes(hs, schedule_len, n_q_heads, head_dim);
     if (ws_need < 0) return KVR_E_BAD_SCHEDULE;
     if (workspace_bytes < ws_need || (ws_need > 0 && !workspace)) return KVR_E_WORKSPACE_TOO_SMALL;
@@ -739,23 +782,20 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     a.group = n_q_heads / n_kv_heads;
     a.qt = hs[H_QT];
     a.n_head_groups = hs[H_NHG];
-    a.n_tiles = hs[H_NTILES];
+    a.n_groups = hs[H_NGROUPS];
     a.n_work = hs[H_NWORK];
     a.kc = hs[H_KC];
     a.head_dim = head_dim;
     a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
     if (ws_need > 0) {
         a.ws_ml = static_cast<float*>(workspace);
-        a.ws_o = a.ws_ml + static_cast<int64_t>(n_q_heads) * a.n_work * kRowTile * 2;
+        a.ws_o = a.ws_ml + static_cast<int64_t>(n_q_heads) * a.n_work * kGroupRows * 2;
     }
     if (a.qt * a.n_head_groups != a.group) return KVR_E_BAD_SCHEDULE;
 
-    hipStream_t s = as_stream(stream);
-    const dim3 grid(static_cast<unsigned>(n_kv_heads * a.n_head_groups), static_cast<unsigned>(a.n_work));
     // The MFMA kernel reads 16-byte fragments of q/k/v: unit dim strides and
     // 16-byte aligned rows. Other layouts (strided slices, odd offsets) take
-    // the generic kernel, whose chunking (multiples of 32 keys) is compatible
-    // with every MFMA schedule (multiples of 256 keys).
+    // the generic kernel, which accepts every schedule.
     bool use_mfma = hs[H_KIND] == KIND_MFMA;
     if (use_mfma && !mfma_eligible(dtype, head_dim)) return KVR_E_BAD_SCHEDULE;
     for (int t = 0; t < 3 && use_mfma; ++t) {
@@ -764,14 +804,15 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     }
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u)
         use_mfma = false;
+
+    hipStream_t s = as_stream(stream);
+    const dim3 grid(static_cast<unsigned>(n_kv_heads * a.n_head_groups), static_cast<unsigned>(a.n_work));
     int st;
     if (use_mfma) {
         if (dtype == KVR_DTYPE_BF16)
-            st = head_dim == 128 ? launch_mfma<bf16_t, 128>(a, a.qt, grid, s)
-                                 : launch_mfma<bf16_t, 64>(a, a.qt, grid, s);
+            st = head_dim == 128 ? launch_mfma<bf16_t, 128>(a, a.qt, grid, s) : launch_mfma<bf16_t, 64>(a, a.qt, grid, s);
         else
-            st = head_dim == 128 ? launch_mfma<f16_t, 128>(a, a.qt, grid, s)
-                                 : launch_mfma<f16_t, 64>(a, a.qt, grid, s);
+            st = head_dim == 128 ? launch_mfma<f16_t, 128>(a, a.qt, grid, s) : launch_mfma<f16_t, 64>(a, a.qt, grid, s);
     } else {
         const int dmax = generic_dmax(head_dim);
         if (dmax == 0) return KVR_E_UNSUPPORTED_SHAPE;
@@ -783,8 +824,8 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     }
     if (st != KVR_OK || hs[H_NMULTI] == 0) return st;
     switch (dtype) {
-        case KVR_DTYPE_F32: return launch_merge<f32_t>(a, s);
-        case KVR_DTYPE_F16: return launch_merge<f16_t>(a, s);
-        default: return launch_merge<bf16_t>(a, s);
+        case KVR_DTYPE_F32: return launch_merge<f32_t>(a, hs[H_MAXCHUNKS], s);
+        case KVR_DTYPE_F16: return launch_merge<f16_t>(a, hs[H_MAXCHUNKS], s);
+        default: return launch_merge<bf16_t>(a, hs[H_MAXCHUNKS], s);
     }
 }

@@ -73,24 +73,41 @@ def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
 
 @pytest.mark.parametrize("positions,n_keys,chunk", [
     ([0, 1, 2], 3, 0), (list(range(928, 992)), 1920, 0), (list(range(0, 4000, 7)), 4000, 256),
-    ([5, 9, 4095], 4096, 0), (list(range(1024, 2048)), 2048, 512)])
+    ([5, 9, 4095], 4096, 0), (list(range(1024, 2048)), 2048, 512), (list(range(100, 200)), 300, 64)])
 def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_keys, chunk):
     s = schedule(positions, n_keys, 32, 8, 128, chunk=chunk)
-    header, n_tiles, kc, n_work = s[:16], s[3], s[4], s[5]
+    header, n_groups, kc, n_work = s[:16], s[3], s[4], s[5]
     assert header[0] == 0x4B565253 and header[2] == len(positions)
-    tiles = [(s[16 + 2 * t], s[17 + 2 * t]) for t in range(n_tiles)]
-    work = [(s[16 + 2 * n_tiles + 2 * w], s[17 + 2 * n_tiles + 2 * w]) for w in range(n_work)]
-    assert kc % 256 == 0 and len(work) == n_work == sum(c for _, c in tiles)
-    # the work items of tile t are exactly chunks 0..c-1, contiguous from its base
-    for t, (base, count) in enumerate(tiles):
-        assert work[base:base + count] == [(t, c) for c in range(count)]
-        last = positions[min(16 * t + 15, len(positions) - 1)]
-        assert (count - 1) * kc <= last < count * kc  # chunks reach the tile's last causal key, no further
-    # every (row, key <= pos) pair lies in exactly one chunk of its tile
+    assert n_groups == (len(positions) + 63) // 64
+    groups = [(s[16 + 2 * g], s[17 + 2 * g]) for g in range(n_groups)]
+    work = [(s[16 + 2 * n_groups + 2 * w], s[17 + 2 * n_groups + 2 * w]) for w in range(n_work)]
+    assert kc % 64 == 0 and (chunk == 0 or kc == chunk)
+    assert len(work) == n_work == sum(c for _, c in groups) and header[15] == max(c for _, c in groups)
+    # the work items of group g are exactly chunks 0..c-1, contiguous from its base, and
+    # the chunks reach the group's last causal key and no further
+    for g, (base, count) in enumerate(groups):
+        assert work[base:base + count] == [(g, c) for c in range(count)]
+        last = positions[min(64 * g + 63, len(positions) - 1)]
+        assert (count - 1) * kc <= last < count * kc
+    # every (row, key <= pos) pair lies in exactly one chunk of its group
     for r, p in enumerate(positions):
-        base, count = tiles[r // 16]
-        covering = [c for c in range(count) for key in (0, p) if c * kc <= key < (c + 1) * kc]
-        assert covering[0] == 0 and covering[-1] == p // kc
+        base, count = groups[r // 64]
+        for key in (0, p // 2, p):
+            assert sum(1 for c in range(count) if c * kc <= key < (c + 1) * kc) == 1
+    assert header[12] == sum(1 for _, c in groups if c > 1)  # groups needing a merge
+
+
+def test_default_chunking_keeps_one_block_per_cu_for_the_c3_support():
+    import random
+
+    slots = sorted(random.Random(2).sample(range(5632 // 8), 16))
+    positions = [2048 + 8 * k + i for k in slots for i in range(4)]
+    s = schedule(positions, 7680, 32, 8, 128)
+    n_work, kc = s[5], s[4]
+    assert n_work * 8 <= 256 < (-(-max(positions) // (kc - 64)) if kc > 64 else 10 ** 9) * 8
+    # a group that fits one chunk is never split
+    s = schedule(list(range(15104)), 16128, 32, 8, 128)
+    assert s[12] == 0 and s[5] == s[3]
 
 
 def test_schedule_rejects_unsorted_or_out_of_range_positions():
@@ -110,4 +127,4 @@ def test_workspace_is_zero_when_every_tile_fits_one_chunk():
     assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 0
     s = schedule(list(range(0, 8000, 100)), 8000, 4, 2, 64, chunk=256)
     buf = (ctypes.c_int32 * len(s))(*s)
-    assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 16 * 66 * 4
+    assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 64 * 66 * 4
