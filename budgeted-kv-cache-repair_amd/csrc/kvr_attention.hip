@@ -7,41 +7,48 @@
 //
 // Work decomposition (host schedule, kvr_attention_schedule):
 //   selected rows are cut into groups of 64 (four tiles of 16 rows); group g
-//   needs keys [0, pos[last row of g] + 1), cut into chunks of KC keys. One
-//   block handles one (KV head, head group, row group, key chunk): it stages
-//   the chunk's K/V once in LDS, 64 keys at a time, double-buffered, and each
-//   of its four waves attends one row tile (QT query heads x 16 rows) to it.
-//   Grid x = KV head x head group, so every block of one KV head lands on the
-//   same XCD (blocks are dealt round-robin over the 8 XCDs by linear id) and
-//   that head's K/V and partials stay in one L2.
+//   needs keys [0, pos[last row of g] + 1). That key range is cut into chunks
+//   whose boundaries are multiples of 64 keys, sized so every chunk carries
+//   about the same cost (64-key sub-tiles weighted by how many of the group's
+//   row tiles still attend to them) and the whole grid is about one block per
+//   CU. One block handles one (KV head, head group, row group, chunk): it
+//   stages the chunk's K (row-major) and V (transposed) in LDS, 64 keys at a
+//   time, double-buffered, and each wave attends the rows of two row tiles
+//   for one query head to it. Grid x = KV head x head group, so every block
+//   of one KV head lands on the same XCD (blocks are dealt round-robin over
+//   the 8 XCDs by linear id) and that head's K/V and partials share one L2.
 // Groups with one chunk write the final output; groups with several chunks
 // write fp32 partials (running max m in the log2 domain, sum l, unnormalised
-// O) that a merge kernel combines.
+// O) only for row tiles that attend into the chunk, and a merge kernel
+// combines them.
 #include "kvr_internal.h"
 
 #include <math.h>
 #include <string.h>
 
-#include <utility>
+#include <vector>
 
 namespace kvr {
 namespace {
 
 constexpr int32_t kMagic = 0x4B565253;  // "KVRS"
-constexpr int32_t kVersion = 2;
+constexpr int32_t kVersion = 3;
 constexpr int kHeader = 16;
+constexpr int kWorkInts = 4;               // (group, chunk, key_begin, key_end)
 constexpr int kRowTile = 16;               // rows per MFMA tile
-constexpr int kTilesPerGroup = 4;          // one wave per tile
+constexpr int kTilesPerGroup = 4;
 constexpr int kGroupRows = kRowTile * kTilesPerGroup;
 constexpr int kSub = 64;                   // keys per LDS sub-tile
 constexpr int kMaxChunksPerGroup = 1024;   // merge weights fit in LDS
+constexpr int kTargetBlocks = 256;         // one block per CU (MI355X: 256 CUs)
+constexpr float kLazyLog2 = 8.f;           // lazy-rescale headroom (log2 units): p <= 256
 
 enum Header {
     H_MAGIC = 0,
     H_VERSION,
     H_NSEL,
     H_NGROUPS,
-    H_KC,
+    H_KC,  // longest chunk in keys
     H_NWORK,
     H_QT,
     H_NHG,
@@ -57,6 +64,8 @@ enum Header {
 enum Kind { KIND_GENERIC = 0, KIND_MFMA = 1 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct AttnArgs {
     const char* q;
@@ -72,12 +81,12 @@ struct AttnArgs {
     int64_t n_keys;
     int32_t n_q_heads;
     int32_t group;  // G = Hq / Hkv
-    int32_t qt;     // query heads per wave
+    int32_t qt;     // query heads per block
     int32_t n_head_groups;
     int32_t n_groups;
     int32_t n_work;
-    int32_t kc;
     int32_t head_dim;
+    int32_t out_vec;  // output rows take 8-byte stores (unit dim stride, aligned)
     float scale_log2;  // scale * log2(e)
 };
 
@@ -85,281 +94,376 @@ struct AttnArgs {
 __host__ __device__ inline const int32_t* group_table(const int32_t* s) { return s + kHeader; }
 __host__ __device__ inline const int32_t* work_table(const int32_t* s) { return s + kHeader + 2 * s[H_NGROUPS]; }
 
-// Causal key limit (exclusive) of rows [first, first + count) clipped to n_sel.
-__device__ inline int64_t rows_kmax(const AttnArgs& a, int64_t first, int64_t count) {
+// Causal key limit (exclusive) of rows [first, first + count) clipped to n_sel; 0 when empty.
+__device__ inline int32_t rows_kmax(const AttnArgs& a, int64_t first, int64_t count) {
     if (first >= a.n_sel) return 0;
     const int64_t last = (first + count - 1 < a.n_sel) ? first + count - 1 : a.n_sel - 1;
-    return a.positions[last] + 1;
+    return static_cast<int32_t>(a.positions[last] + 1);
 }
 
 // ===========================================================================
-// MFMA kernel
+// MFMA kernel (bf16 / fp16, head_dim 64 or 128)
 // ===========================================================================
+// Probabilities enter the PV MFMA as a hi + lo pair of 16-bit values so they
+// are not rounded to 16 bits (the reference Triton kernel keeps P in fp32,
+// _indexed_triton.py:54-58). split() packs two probabilities: hi holds their
+// 16-bit heads, lo the rounded remainders p - head.
 template <typename T> struct mma_t;
 template <> struct mma_t<bf16_t> {
     typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-    typedef __bf16 scalar;
     __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
-    __device__ static inline scalar cvt(float x) { return static_cast<scalar>(x); }
-    __device__ static inline float back(scalar x) { return static_cast<float>(x); }
+    // bf16 head = the upper half of the fp32 bits (truncation); p - head is exact
+    // in fp32 and its RNE bf16 rounding leaves an error below 2^-16 |p|.
+    __device__ static inline void split(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+        const uint32_t b0 = __float_as_uint(p0), b1 = __float_as_uint(p1);
+        hi = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+        const f32x2 r = {p0 - __uint_as_float(b0 & 0xffff0000u), p1 - __uint_as_float(b1 & 0xffff0000u)};
+        lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));  // v_cvt_pk_bf16_f32 (RNE)
+    }
 };
 template <> struct mma_t<f16_t> {
     typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-    typedef _Float16 scalar;
     __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
-    __device__ static inline scalar cvt(float x) { return static_cast<scalar>(x); }
-    __device__ static inline float back(scalar x) { return static_cast<float>(x); }
+    __device__ static inline void split(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+        const _Float16 h0 = static_cast<_Float16>(p0), h1 = static_cast<_Float16>(p1);
+        const _Float16 l0 = static_cast<_Float16>(p0 - static_cast<float>(h0));
+        const _Float16 l1 = static_cast<_Float16>(p1 - static_cast<float>(h1));
+        hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+        lo = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+    }
 };
 
-constexpr int kMfmaThreads = 256;  // 4 waves, one per row tile
-constexpr int kPad = 8;            // elements of LDS row padding (16 bytes)
-
-template <int D>
-struct MfmaSmem {
-    static constexpr int stride = D + kPad;          // elements per staged key row
-    static constexpr int tile_elems = kSub * stride;  // one K or V sub-tile
-    static constexpr int bytes = 2 /*buffers*/ * 2 /*K,V*/ * tile_elems * 2;
-    static constexpr int chunks = kSub * D / 8;              // 16-byte pieces per sub-tile
-    static constexpr int per_thread = chunks / kMfmaThreads;  // per tensor
+// LDS layout of one staged 64-key sub-tile: K row-major [64][D + 8] then V
+// transposed [D][64 + 4] (16-bit elements). The paddings make the 16-byte
+// K-fragment reads, the 8-byte V^T-fragment reads and the 4-byte transposing
+// V writes conflict-free within each 16/32-lane phase.
+template <int D, int QT>
+struct MfmaCfg {
+    static constexpr int threads = 128 * QT;  // two waves per query head
+    static constexpr int kstr = D + 8;
+    static constexpr int vstr = kSub + 4;
+    static constexpr int k_elems = kSub * kstr;
+    static constexpr int v_elems = D * vstr;
+    static constexpr int buf_elems = k_elems + v_elems;
+    static constexpr int bytes = 2 * buf_elems * 2;  // double-buffered, 2 bytes per element
+    static constexpr int c8 = D / 8;                 // 16-byte pieces per row
+    static constexpr int k_pieces = kSub * c8;
+    static constexpr int v_pieces = (kSub / 2) * c8;  // (key pair, piece)
+    static constexpr int kp = (k_pieces + threads - 1) / threads;
+    static constexpr int vp = (v_pieces + threads - 1) / threads;
 };
 
-// Global -> register prefetch of one 64-key K/V sub-tile (zero beyond `end`).
-template <int D>
-__device__ inline void load_subtile(const AttnArgs& a, const char* kbase, const char* vbase, int64_t key0,
-                                    int64_t end, int tid, u32x4* kr, u32x4* vr) {
-    using S = MfmaSmem<D>;
-    constexpr int C8 = D / 8;
-#pragma unroll
-    for (int p = 0; p < S::per_thread; ++p) {
-        const int cid = tid + p * kMfmaThreads;
-        const int kk = cid / C8;
-        const int c8 = cid - kk * C8;
-        const int64_t key = key0 + kk;
-        kr[p] = u32x4{0u, 0u, 0u, 0u};
-        vr[p] = u32x4{0u, 0u, 0u, 0u};
-        if (key < end) {
-            kr[p] = *reinterpret_cast<const u32x4*>(kbase + (key * a.ks[1] + 8 * c8) * 2);
-            vr[p] = *reinterpret_cast<const u32x4*>(vbase + (key * a.vs[1] + 8 * c8) * 2);
-        }
-    }
-}
-
-template <int D>
-__device__ inline void store_subtile(uint16_t* Ks, uint16_t* Vs, int tid, const u32x4* kr, const u32x4* vr) {
-    using S = MfmaSmem<D>;
-    constexpr int C8 = D / 8;
-#pragma unroll
-    for (int p = 0; p < S::per_thread; ++p) {
-        const int cid = tid + p * kMfmaThreads;
-        const int kk = cid / C8;
-        const int c8 = cid - kk * C8;
-        *reinterpret_cast<u32x4*>(Ks + kk * S::stride + 8 * c8) = kr[p];
-        *reinterpret_cast<u32x4*>(Vs + kk * S::stride + 8 * c8) = vr[p];
-    }
-}
-
-// Each wave: QT query heads x the 16 rows of its tile. S^T = K Q^T (keys on the
-// MFMA M axis) so each lane holds 4 keys of one query, and the PV MFMA takes
-// P^T straight from those registers: O^T += V^T P^T.
 template <typename T, int D, int QT>
-__global__ void __launch_bounds__(kMfmaThreads)
-attn_mfma_kernel(AttnArgs a) {
+struct MfmaWave {
     using M = mma_t<T>;
     using v8 = typename M::v8;
-    using S = MfmaSmem<D>;
-    constexpr int DS = D / 32;  // k-steps of the QK^T MFMA
-    constexpr int DT = D / 16;  // d tiles of the PV MFMA
-    extern __shared__ __align__(16) char smem[];
-    uint16_t* lds = reinterpret_cast<uint16_t*>(smem);  // [buf][K|V][64][stride]
+    using C = MfmaCfg<D, QT>;
+    static constexpr int DS = D / 32;  // k-steps of the QK^T MFMA
+    static constexpr int DT = D / 16;  // d tiles of the PV MFMA
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int lq = lane & 15;  // query row within the tile
-    const int lj = lane >> 4;  // lane group 0..3
+    v8 qf[2][DS];
+    f32x4 o[2][DT];
+    float m_run[2], l_run[2];
+    int32_t kmax[2], nomask_end[2], pos[2];
 
-    const int32_t* wk = work_table(a.sched);
-    const int work = blockIdx.y;
-    const int grp = wk[2 * work];
-    const int chunk = wk[2 * work + 1];
-    const int n_chunks = group_table(a.sched)[2 * grp + 1];
-    const int kv_head = blockIdx.x / a.n_head_groups;
-    const int hg = blockIdx.x - kv_head * a.n_head_groups;
-    const int q_head0 = kv_head * a.group + hg * QT;
-
-    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
-    const int64_t key_begin = static_cast<int64_t>(chunk) * a.kc;
-    const int64_t group_kmax = rows_kmax(a, group_row0, kGroupRows);
-    const int64_t key_end = (key_begin + a.kc < group_kmax) ? key_begin + a.kc : group_kmax;
-    const int n_sub = static_cast<int>((key_end - key_begin + kSub - 1) / kSub);
-
-    const int64_t tile_row0 = group_row0 + wave * kRowTile;
-    const int64_t tile_kmax = rows_kmax(a, tile_row0, kRowTile);  // 0 for an empty tile
-    const int64_t my_row = tile_row0 + lq;
-    const int64_t my_pos = (my_row < a.n_sel) ? a.positions[my_row] : int64_t(-1);
-
-    // Q fragments (B operand of S^T = K Q^T): lane holds q[row][32*ds + 8*lj .. +8].
-    v8 qf[QT][DS];
+    // One 64-key sub-tile for the wave's active tiles A0 (tile half) / A1 (tile
+    // half + 2). MASK: some key of the sub-tile lies beyond some row's position.
+    template <bool A0, bool A1, bool MASK>
+    __device__ inline void step(const uint16_t* Ks, const uint16_t* Vt, int32_t key0, int lq, int lj,
+                                float scale_log2) {
+        f32x4 st[2][4];
 #pragma unroll
-    for (int h = 0; h < QT; ++h)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-            u32x4 raw = {0u, 0u, 0u, 0u};
-            if (my_row < a.n_sel) {
-                const int64_t off = (q_head0 + h) * a.qs[0] + my_row * a.qs[1] + (32 * ds + 8 * lj) * a.qs[2];
-                raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
+            for (int kt = 0; kt < 4; ++kt) st[t][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // S^T = K Q^T: keys on the M axis, each lane gets 4 keys of its row.
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+                const v8 kf = __builtin_bit_cast(
+                    v8, *reinterpret_cast<const u32x4*>(Ks + (16 * kt + lq) * C::kstr + 32 * ds + 8 * lj));
+                if (A0) st[0][kt] = M::mma(kf, qf[0][ds], st[0][kt]);
+                if (A1) st[1][kt] = M::mma(kf, qf[1][ds], st[1][kt]);
             }
-            qf[h][ds] = __builtin_bit_cast(v8, raw);
-        }
-
-    f32x4 o[QT][DT];
-    float m_run[QT], l_run[QT];
+        u32x4 phi[2][2], plo[2][2];
 #pragma unroll
-    for (int h = 0; h < QT; ++h) {
-        m_run[h] = -INFINITY;
-        l_run[h] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    const char* kbase = a.k + static_cast<int64_t>(kv_head) * a.ks[0] * 2;
-    const char* vbase = a.v + static_cast<int64_t>(kv_head) * a.vs[0] * 2;
-    u32x4 kr[S::per_thread], vr[S::per_thread];
-    if (n_sub > 0) {
-        load_subtile<D>(a, kbase, vbase, key_begin, key_end, tid, kr, vr);
-        store_subtile<D>(lds, lds + S::tile_elems, tid, kr, vr);
-    }
-
-    for (int s = 0; s < n_sub; ++s) {
-        const int64_t sub_key0 = key_begin + static_cast<int64_t>(s) * kSub;
-        const bool more = s + 1 < n_sub;
-        if (more) load_subtile<D>(a, kbase, vbase, sub_key0 + kSub, key_end, tid, kr, vr);
-        __syncthreads();  // sub-tile s is staged; buffer (s+1)%2 is free
-        const uint16_t* Kb = lds + (s & 1) * 2 * S::tile_elems;
-        const uint16_t* Vb = Kb + S::tile_elems;
-
-        if (sub_key0 < tile_kmax) {
-            // ---- S^T = K Q^T for 4 key tiles of 16 ----
-            f32x4 st[QT][4];
-#pragma unroll
-            for (int h = 0; h < QT; ++h)
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt) st[h][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 2; ++t) {
+            if (!(t == 0 ? A0 : A1)) continue;
+            // raw scores; scale_log2 > 0 (the host routes other scales to the
+            // generic kernel), so the scaled max is the raw max times the scale
+            float x[4][4];
+            float mx = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    const u32x4 raw =
-                        *reinterpret_cast<const u32x4*>(Kb + (16 * kt + lq) * S::stride + 32 * ds + 8 * lj);
-                    const v8 kf = __builtin_bit_cast(v8, raw);
-#pragma unroll
-                    for (int h = 0; h < QT; ++h) st[h][kt] = M::mma(kf, qf[h][ds], st[h][kt]);
+                for (int i = 0; i < 4; ++i) {
+                    float s = st[t][kt][i];
+                    if (MASK) s = (key0 + 16 * kt + 4 * lj + i <= pos[t]) ? s : -INFINITY;
+                    x[kt][i] = s;
+                    mx = fmaxf(mx, s);
                 }
-            // ---- online softmax (log2 domain), mask key > pos ----
-            v8 p_hi[QT][2], p_lo[QT][2];
-#pragma unroll
-            for (int h = 0; h < QT; ++h) {
-                float sc[4][4];
-                float mx = -INFINITY;
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t key = sub_key0 + 16 * kt + 4 * lj + i;
-                        const float x = (key <= my_pos) ? st[h][kt][i] * a.scale_log2 : -INFINITY;
-                        sc[kt][i] = x;
-                        mx = fmaxf(mx, x);
-                    }
+            mx *= scale_log2;
+            // Lazy rescaling: a row's reference max m moves only when its scores
+            // exceed m by more than kLazyLog2 (so p <= 2^kLazyLog2 and fp32 o, l
+            // cannot overflow). When no lane of the wave sees such a score, the
+            // row reduction and the o/l rescale are skipped; o / l is unchanged.
+            if (__any(mx > m_run[t] + kLazyLog2)) {
                 mx = fmaxf(mx, __shfl_xor(mx, 16));
                 mx = fmaxf(mx, __shfl_xor(mx, 32));
-                const float m_new = fmaxf(m_run[h], mx);
-                const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-                const float alpha = exp2f(m_run[h] - m_use);
-                m_run[h] = m_new;
-                float psum = 0.f;
+                const float m_new = (mx > m_run[t] + kLazyLog2) ? mx : m_run[t];
+                // 1 if unmoved, 0 from -inf; a row with no visible key yet keeps m = -inf
+                // and alpha = exp2(-inf - 0) = 0 (never exp2(-inf + inf))
+                const float alpha = __builtin_amdgcn_exp2f(m_run[t] - (m_new == -INFINITY ? 0.f : m_new));
+                m_run[t] = m_new;
+                l_run[t] *= alpha;
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float p = exp2f(sc[kt][i] - m_use);
-                        sc[kt][i] = p;
-                        psum += p;
-                    }
-                l_run[h] = l_run[h] * alpha + psum;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
-#pragma unroll
-                for (int half = 0; half < 2; ++half)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float x0 = sc[2 * half][i];
-                        const float x1 = sc[2 * half + 1][i];
-                        const auto h0 = M::cvt(x0);
-                        const auto h1 = M::cvt(x1);
-                        p_hi[h][half][i] = h0;
-                        p_hi[h][half][4 + i] = h1;
-                        p_lo[h][half][i] = M::cvt(x0 - M::back(h0));
-                        p_lo[h][half][4 + i] = M::cvt(x1 - M::back(h1));
-                    }
+                for (int dt = 0; dt < DT; ++dt) o[t][dt] *= alpha;
             }
-            // ---- O^T += V^T P^T: A = V^T gathered from the row-major tile ----
+            const float m_use = (m_run[t] == -INFINITY) ? 0.f : m_run[t];
+            float psum = 0.f;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
+            for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const uint16_t* col = Vb + (32 * half + 4 * lj) * S::stride + 16 * dt + lq;
-                    uint16_t g[8];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        g[i] = col[i * S::stride];
-                        g[4 + i] = col[(16 + i) * S::stride];
-                    }
-                    v8 vf;
-                    __builtin_memcpy(&vf, g, 16);
-#pragma unroll
-                    for (int h = 0; h < QT; ++h) {
-                        o[h][dt] = M::mma(vf, p_hi[h][half], o[h][dt]);
-                        o[h][dt] = M::mma(vf, p_lo[h][half], o[h][dt]);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], scale_log2, -m_use));
+                    x[kt][i] = p;
+                    psum += p;
                 }
+            l_run[t] += psum;
+            // P^T as the B operand: lane group lj holds keys {4lj+i} of key tiles
+            // 2h and 2h+1; V^T below is read in the same key order.
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t hv[4], lv[4];
+                M::split(x[2 * h][0], x[2 * h][1], hv[0], lv[0]);
+                M::split(x[2 * h][2], x[2 * h][3], hv[1], lv[1]);
+                M::split(x[2 * h + 1][0], x[2 * h + 1][1], hv[2], lv[2]);
+                M::split(x[2 * h + 1][2], x[2 * h + 1][3], hv[3], lv[3]);
+                phi[t][h] = u32x4{hv[0], hv[1], hv[2], hv[3]};
+                plo[t][h] = u32x4{lv[0], lv[1], lv[2], lv[3]};
+            }
         }
-        if (more) store_subtile<D>(lds + ((s + 1) & 1) * 2 * S::tile_elems,
-                                   lds + ((s + 1) & 1) * 2 * S::tile_elems + S::tile_elems, tid, kr, vr);
+        // O^T += V^T P^T
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint16_t* row = Vt + (16 * dt + lq) * C::vstr + 32 * h + 4 * lj;
+                const uint2 lo = *reinterpret_cast<const uint2*>(row);
+                const uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
+                const v8 vf = __builtin_bit_cast(v8, u32x4{lo.x, lo.y, hi.x, hi.y});
+                if (A0) {
+                    o[0][dt] = M::mma(vf, __builtin_bit_cast(v8, phi[0][h]), o[0][dt]);
+                    o[0][dt] = M::mma(vf, __builtin_bit_cast(v8, plo[0][h]), o[0][dt]);
+                }
+                if (A1) {
+                    o[1][dt] = M::mma(vf, __builtin_bit_cast(v8, phi[1][h]), o[1][dt]);
+                    o[1][dt] = M::mma(vf, __builtin_bit_cast(v8, plo[1][h]), o[1][dt]);
+                }
+            }
     }
 
-    // ---- epilogue: per-query sums, then final output or fp32 partial ----
+    template <bool MASK>
+    __device__ inline void dispatch(bool a0, bool a1, const uint16_t* Ks, const uint16_t* Vt, int32_t key0,
+                                    int lq, int lj, float scale_log2) {
+        // Tile half + 2 holds later rows than tile half, so it is active whenever
+        // tile half is, unless it has no rows at all (the last, partial group):
+        // then it runs fully masked (pos = -1 gives p = 0) and is never written.
+        if (a0)
+            step<true, true, MASK>(Ks, Vt, key0, lq, lj, scale_log2);
+        else if (a1)
+            step<false, true, MASK>(Ks, Vt, key0, lq, lj, scale_log2);
+    }
+};
+
+template <typename T, int D, int QT>
+__global__ void __launch_bounds__(128 * QT)
+attn_mfma_kernel(AttnArgs a) {
+    using C = MfmaCfg<D, QT>;
+    using W = MfmaWave<T, D, QT>;
+    using v8 = typename W::v8;
+    constexpr int NT = C::threads;
+    extern __shared__ __align__(16) char smem[];
+    uint16_t* lds = reinterpret_cast<uint16_t*>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches below
+    const int lq = lane & 15;
+    const int lj = lane >> 4;
+
+    const int work = blockIdx.y;
+    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int grp = wk[0];
+    const int32_t key_begin = wk[2];
+    const int32_t key_end = wk[3];
+    const int n_chunks = group_table(a.sched)[2 * grp + 1];
+    const int kv_head = blockIdx.x / a.n_head_groups;
+    const int hg = blockIdx.x - kv_head * a.n_head_groups;
+    const int hq = wave % QT;
+    const int half = wave / QT;
+    const int q_head = kv_head * a.group + hg * QT + hq;
+    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
+
+    W w;
 #pragma unroll
-    for (int h = 0; h < QT; ++h) {
-        float l = l_run[h];
+    for (int t = 0; t < 2; ++t) {
+        const int64_t row0 = group_row0 + kRowTile * (half + 2 * t);
+        const int64_t row = row0 + lq;
+        w.kmax[t] = rows_kmax(a, row0, kRowTile);
+        w.nomask_end[t] = (row0 + kRowTile <= a.n_sel) ? static_cast<int32_t>(a.positions[row0] + 1) : 0;
+        w.pos[t] = (row < a.n_sel) ? static_cast<int32_t>(a.positions[row]) : -1;
+        w.m_run[t] = -INFINITY;
+        w.l_run[t] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < W::DT; ++dt) w.o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < W::DS; ++ds) {
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (row < a.n_sel) {
+                const int64_t off = q_head * a.qs[0] + row * a.qs[1] + (32 * ds + 8 * lj);
+                raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
+            }
+            w.qf[t][ds] = __builtin_bit_cast(v8, raw);
+        }
+    }
+
+    const int32_t ks1 = static_cast<int32_t>(a.ks[1]);
+    const int32_t vs1 = static_cast<int32_t>(a.vs[1]);
+    const char* kbase = a.k + (static_cast<int64_t>(kv_head) * a.ks[0] + static_cast<int64_t>(key_begin) * a.ks[1]) * 2;
+    const char* vbase = a.v + (static_cast<int64_t>(kv_head) * a.vs[0] + static_cast<int64_t>(key_begin) * a.vs[1]) * 2;
+    const int32_t n_keys_chunk = key_end - key_begin;
+    const int n_sub = (n_keys_chunk + kSub - 1) / kSub;
+
+    u32x4 kr[C::kp], vr0[C::vp], vr1[C::vp];
+    // Global -> registers: sub-tile s (zero beyond the chunk end).
+    auto load = [&](int s) {
+        const int32_t left = n_keys_chunk - kSub * s;
+        const char* kb = kbase + static_cast<int64_t>(kSub) * s * a.ks[1] * 2;
+        const char* vb = vbase + static_cast<int64_t>(kSub) * s * a.vs[1] * 2;
+#pragma unroll
+        for (int p = 0; p < C::kp; ++p) {
+            const int idx = tid + p * NT;
+            kr[p] = u32x4{0u, 0u, 0u, 0u};
+            if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
+                const int kk = idx / C::c8;
+                const int c8 = idx - kk * C::c8;
+                if (kk < left) kr[p] = *reinterpret_cast<const u32x4*>(kb + (kk * ks1 + 8 * c8) * 2);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < C::vp; ++p) {
+            const int idx = tid + p * NT;
+            vr0[p] = u32x4{0u, 0u, 0u, 0u};
+            vr1[p] = u32x4{0u, 0u, 0u, 0u};
+            if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
+                const int pr = idx & 31;
+                const int c8 = idx >> 5;
+                const int kk = 2 * pr;
+                if (kk < left) vr0[p] = *reinterpret_cast<const u32x4*>(vb + (kk * vs1 + 8 * c8) * 2);
+                if (kk + 1 < left) vr1[p] = *reinterpret_cast<const u32x4*>(vb + ((kk + 1) * vs1 + 8 * c8) * 2);
+            }
+        }
+    };
+    // Registers -> LDS buffer: K as is, V transposed (key pairs packed per dim).
+    auto store = [&](uint16_t* buf) {
+        uint16_t* Ks = buf;
+        uint16_t* Vt = buf + C::k_elems;
+#pragma unroll
+        for (int p = 0; p < C::kp; ++p) {
+            const int idx = tid + p * NT;
+            if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
+                const int kk = idx / C::c8;
+                const int c8 = idx - kk * C::c8;
+                *reinterpret_cast<u32x4*>(Ks + kk * C::kstr + 8 * c8) = kr[p];
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < C::vp; ++p) {
+            const int idx = tid + p * NT;
+            if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
+                const int pr = idx & 31;
+                const int c8 = idx >> 5;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t x0 = vr0[p][j], x1 = vr1[p][j];
+                    uint16_t* col = Vt + (8 * c8 + 2 * j) * C::vstr + 2 * pr;
+                    *reinterpret_cast<uint32_t*>(col) = (x0 & 0xffffu) | (x1 << 16);
+                    *reinterpret_cast<uint32_t*>(col + C::vstr) = (x0 >> 16) | (x1 & 0xffff0000u);
+                }
+            }
+        }
+    };
+
+    if (n_sub > 0) {
+        load(0);
+        store(lds);
+    }
+    for (int s = 0; s < n_sub; ++s) {
+        const bool more = s + 1 < n_sub;
+        if (more) load(s + 1);
+        __syncthreads();  // sub-tile s is staged; buffer (s+1)&1 is no longer read
+        const uint16_t* Ks = lds + (s & 1) * C::buf_elems;
+        const uint16_t* Vt = Ks + C::k_elems;
+        const int32_t key0 = key_begin + kSub * s;
+        const bool a0 = key0 < w.kmax[0];
+        const bool a1 = key0 < w.kmax[1];
+        // rows of an active tile all see every key of the sub-tile unless the
+        // sub-tile reaches past the tile's first (smallest) position
+        const int32_t key_stop = key0 + kSub;
+        const bool mask = a0 ? (key_stop > w.nomask_end[0] || key_stop > w.nomask_end[1])
+                             : key_stop > w.nomask_end[1];
+        if (mask)
+            w.template dispatch<true>(a0, a1, Ks, Vt, key0, lq, lj, a.scale_log2);
+        else
+            w.template dispatch<false>(a0, a1, Ks, Vt, key0, lq, lj, a.scale_log2);
+        if (more) store(lds + ((s + 1) & 1) * C::buf_elems);
+    }
+
+    // ---- epilogue: row sums across the 4 lane groups, then output or partial ----
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        float l = w.l_run[t];
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
-        l_run[h] = l;
+        w.l_run[t] = l;
     }
-    if (my_row >= a.n_sel) return;
-    const int r = static_cast<int>(my_row - group_row0);
 #pragma unroll
-    for (int h = 0; h < QT; ++h) {
-        const int q_head = q_head0 + h;
+    for (int t = 0; t < 2; ++t) {
+        const int r = kRowTile * (half + 2 * t) + lq;  // row within the group
+        const int64_t row = group_row0 + r;
+        if (w.kmax[t] <= key_begin || row >= a.n_sel) continue;  // tile does not attend into this chunk
         if (n_chunks == 1) {
-            const float inv = 1.f / l_run[h];
-            uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + q_head * a.os[0] + my_row * a.os[1];
+            const float inv = 1.f / w.l_run[t];
+            uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + q_head * a.os[0] + row * a.os[1];
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
+            for (int dt = 0; dt < W::DT; ++dt) {
+                uint16_t e[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    dst[(16 * dt + 4 * lj + i) * a.os[2]] = elem<T>::from_float(o[h][dt][i] * inv);
+                for (int i = 0; i < 4; ++i) e[i] = elem<T>::from_float(w.o[t][dt][i] * inv);
+                if (a.out_vec) {
+                    *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * lj) =
+                        uint2{e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16)};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dst[(16 * dt + 4 * lj + i) * a.os[2]] = e[i];
+                }
+            }
         } else {
             const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kGroupRows + r;
             float* po = a.ws_o + slot * D;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lj) = o[h][dt];
+            for (int dt = 0; dt < W::DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lj) = w.o[t][dt];
             if (lj == 0) {
-                a.ws_ml[slot * 2 + 0] = m_run[h];
-                a.ws_ml[slot * 2 + 1] = l_run[h];
+                a.ws_ml[slot * 2 + 0] = w.m_run[t];
+                a.ws_ml[slot * 2 + 1] = w.l_run[t];
             }
         }
     }
@@ -384,19 +488,16 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
     float* Sf = Vf + kGenSub * D;                // [kGenSub][kGenThreads] scores
 
     const int tid = threadIdx.x;
-    const int32_t* wk = work_table(a.sched);
     const int work = blockIdx.y;
-    const int grp = wk[2 * work];
-    const int chunk = wk[2 * work + 1];
+    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int grp = wk[0];
+    const int64_t key_begin = wk[2];
+    const int64_t key_end = wk[3];
     const int n_chunks = group_table(a.sched)[2 * grp + 1];
     const int kv_head = blockIdx.x / a.n_head_groups;
     const int hg = blockIdx.x - kv_head * a.n_head_groups;
 
     const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
-    const int64_t key_begin = static_cast<int64_t>(chunk) * a.kc;
-    const int64_t group_kmax = rows_kmax(a, group_row0, kGroupRows);
-    const int64_t key_end = (key_begin + a.kc < group_kmax) ? key_begin + a.kc : group_kmax;
-
     const int tile = tid / 64;
     const int h = (tid % 64) / kRowTile;
     const int r = tile * kRowTile + (tid % kRowTile);
@@ -475,8 +576,10 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
 
 // ===========================================================================
 // Merge of multi-chunk groups. Grid (q_head, group, row block of 8 rows).
-// Phase 1 stages per-(row, chunk) weights exp2(m_c - M) and the total l in
-// LDS; phase 2 gives each thread one (row, dim) element to accumulate.
+// Phase 1 finds, per row, the chunks its tile attended into (a prefix of the
+// group's chunks: those starting below the tile's causal limit), and stages
+// their weights exp2(m_c - M) and the total l in LDS; phase 2 gives each
+// thread four consecutive dims of one row.
 // ===========================================================================
 constexpr int kMergeThreads = 256;
 constexpr int kMergeRows = 8;
@@ -492,57 +595,71 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     const int base = gt[2 * grp];
     const int n_chunks = gt[2 * grp + 1];
     if (n_chunks <= 1) return;
+    const int32_t* wk = work_table(a.sched) + kWorkInts * base;
     const int D = a.head_dim;
-    const int r0 = blockIdx.z * kMergeRows;  // first row (within the group) of this block
-    float* W = reinterpret_cast<float*>(smem);  // [kMergeRows][n_chunks]
-    float* Linv = W + kMergeRows * n_chunks;    // [kMergeRows]
+    const int r0 = blockIdx.z * kMergeRows;      // first row (within the group) of this block
+    float* W = reinterpret_cast<float*>(smem);   // [kMergeRows][n_chunks]
+    float* Linv = W + kMergeRows * n_chunks;     // [kMergeRows]
+    int* NV = reinterpret_cast<int*>(Linv + kMergeRows);  // [kMergeRows] attended chunks
     const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * kGroupRows;
+    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
 
-    // phase 1: 32 lanes per row reduce over chunks
+    // phase 1: 32 lanes per row reduce over the row's chunks
     const int tr = threadIdx.x / 32;
     const int tl = threadIdx.x % 32;
     {
         const int r = r0 + tr;
-        float mx = -INFINITY;
-        for (int c = tl; c < n_chunks; c += 32)
-            mx = fmaxf(mx, a.ws_ml[(slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2]);
+        const int64_t row = group_row0 + r;
+        int nv = 0;
+        if (row < a.n_sel) {
+            const int32_t tk = rows_kmax(a, group_row0 + (r / kRowTile) * kRowTile, kRowTile);
+            while (nv < n_chunks && wk[kWorkInts * nv + 2] < tk) ++nv;
+            float mx = -INFINITY;
+            for (int c = tl; c < nv; c += 32)
+                mx = fmaxf(mx, a.ws_ml[(slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2]);
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 32));
-        const float m_use = (mx == -INFINITY) ? 0.f : mx;
-        float l = 0.f;
-        for (int c = tl; c < n_chunks; c += 32) {
-            const int64_t s = (slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2;
-            const float w = exp2f(a.ws_ml[s] - m_use);
-            W[tr * n_chunks + c] = w;
-            l += w * a.ws_ml[s + 1];
+            for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 32));
+            const float m_use = (mx == -INFINITY) ? 0.f : mx;
+            float l = 0.f;
+            for (int c = tl; c < nv; c += 32) {
+                const int64_t s = (slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2;
+                const float w = exp2f(a.ws_ml[s] - m_use);
+                W[tr * n_chunks + c] = w;
+                l += w * a.ws_ml[s + 1];
+            }
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) l += __shfl_xor(l, off, 32);
+            if (tl == 0) Linv[tr] = 1.f / l;
         }
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) l += __shfl_xor(l, off, 32);
-        if (tl == 0) Linv[tr] = 1.f / l;
+        if (tl == 0) NV[tr] = nv;
     }
     __syncthreads();
 
-    // phase 2: one (row, d) element per thread-iteration
-    for (int e = threadIdx.x; e < kMergeRows * D; e += kMergeThreads) {
-        const int rr = e / D;
-        const int d = e - rr * D;
+    // phase 2: four consecutive dims of one row per thread-iteration
+    const int d4n = D / 4;
+    for (int e = threadIdx.x; e < kMergeRows * d4n; e += kMergeThreads) {
+        const int rr = e / d4n;
+        const int d = 4 * (e - rr * d4n);
         const int r = r0 + rr;
-        const int64_t row = static_cast<int64_t>(grp) * kGroupRows + r;
+        const int64_t row = group_row0 + r;
+        const int nv = NV[rr];
         if (row >= a.n_sel) continue;
         const float* po = a.ws_o + (slot0 + r) * D + d;
         const float* w = W + rr * n_chunks;
-        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        const int64_t cstride = static_cast<int64_t>(kGroupRows) * D;
+        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
         int c = 0;
-        for (; c + 4 <= n_chunks; c += 4) {
-            acc0 += w[c] * po[static_cast<int64_t>(c) * kGroupRows * D];
-            acc1 += w[c + 1] * po[static_cast<int64_t>(c + 1) * kGroupRows * D];
-            acc2 += w[c + 2] * po[static_cast<int64_t>(c + 2) * kGroupRows * D];
-            acc3 += w[c + 3] * po[static_cast<int64_t>(c + 3) * kGroupRows * D];
+        for (; c + 4 <= nv; c += 4) {
+            acc0 += w[c] * *reinterpret_cast<const f32x4*>(po + c * cstride);
+            acc1 += w[c + 1] * *reinterpret_cast<const f32x4*>(po + (c + 1) * cstride);
+            acc2 += w[c + 2] * *reinterpret_cast<const f32x4*>(po + (c + 2) * cstride);
+            acc3 += w[c + 3] * *reinterpret_cast<const f32x4*>(po + (c + 3) * cstride);
         }
-        for (; c < n_chunks; ++c) acc0 += w[c] * po[static_cast<int64_t>(c) * kGroupRows * D];
-        bits* op = reinterpret_cast<bits*>(a.out);
-        op[q_head * a.os[0] + row * a.os[1] + d * a.os[2]] =
-            E::from_float(((acc0 + acc1) + (acc2 + acc3)) * Linv[rr]);
+        for (; c < nv; ++c) acc0 += w[c] * *reinterpret_cast<const f32x4*>(po + c * cstride);
+        const f32x4 acc = ((acc0 + acc1) + (acc2 + acc3)) * Linv[rr];
+        bits* op = reinterpret_cast<bits*>(a.out) + q_head * a.os[0] + row * a.os[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) op[(d + i) * a.os[2]] = E::from_float(acc[i]);
     }
 }
 
@@ -577,10 +694,10 @@ bool allow_lds(F fn, size_t bytes) {
 
 template <typename T, int D, int QT>
 int launch_mfma_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
-    const size_t smem = MfmaSmem<D>::bytes;
-    static const bool ok = allow_lds(attn_mfma_kernel<T, D, QT>, smem);
+    using C = MfmaCfg<D, QT>;
+    static const bool ok = allow_lds(attn_mfma_kernel<T, D, QT>, C::bytes);
     if (!ok) return KVR_E_LAUNCH_FAILED;
-    attn_mfma_kernel<T, D, QT><<<grid, kMfmaThreads, smem, s>>>(a);
+    attn_mfma_kernel<T, D, QT><<<grid, C::threads, C::bytes, s>>>(a);
     return launch_status();
 }
 
@@ -611,21 +728,55 @@ int launch_generic(const AttnArgs& a, int dmax, dim3 grid, hipStream_t s) {
     }
 }
 
+size_t merge_lds_bytes(int max_chunks) {
+    return (static_cast<size_t>(kMergeRows) * max_chunks + 2 * kMergeRows) * sizeof(float);
+}
+
 template <typename T>
 int launch_merge(const AttnArgs& a, int max_chunks, hipStream_t s) {
-    const size_t smem = (static_cast<size_t>(kMergeRows) * max_chunks + kMergeRows) * sizeof(float);
-    static const bool ok = allow_lds(attn_merge_kernel<T>, static_cast<size_t>(kMergeRows) *
-                                                               (kMaxChunksPerGroup + 1) * sizeof(float));
+    static const bool ok = allow_lds(attn_merge_kernel<T>, merge_lds_bytes(kMaxChunksPerGroup));
     if (!ok) return KVR_E_LAUNCH_FAILED;
     dim3 grid(a.n_q_heads, a.n_groups, kGroupRows / kMergeRows);
-    attn_merge_kernel<T><<<grid, kMergeThreads, smem, s>>>(a);
+    attn_merge_kernel<T><<<grid, kMergeThreads, merge_lds_bytes(max_chunks), s>>>(a);
     return launch_status();
 }
 
-int64_t group_kmax_host(const int64_t* positions, int64_t n_sel, int64_t g) {
+// Per-group causal limits on the host: group limit and the limits of its four row tiles.
+struct GroupKeys {
+    int64_t kmax;
+    int64_t tile_kmax[kTilesPerGroup];
+};
+
+GroupKeys group_keys(const int64_t* positions, int64_t n_sel, int64_t g) {
+    GroupKeys k;
     const int64_t last = (g + 1) * kGroupRows - 1 < n_sel ? (g + 1) * kGroupRows - 1 : n_sel - 1;
-    return positions[last] + 1;
+    k.kmax = positions[last] + 1;
+    for (int t = 0; t < kTilesPerGroup; ++t) {
+        const int64_t row0 = g * kGroupRows + t * kRowTile;
+        if (row0 >= n_sel) {
+            k.tile_kmax[t] = 0;
+            continue;
+        }
+        const int64_t tl = row0 + kRowTile - 1 < n_sel ? row0 + kRowTile - 1 : n_sel - 1;
+        k.tile_kmax[t] = positions[tl] + 1;
+    }
+    return k;
 }
+
+// Cost of one 64-key sub-tile: staging it (every sub-tile) plus the MFMA work
+// of each row tile that still attends to it.
+constexpr int64_t kCostStage = 3;
+constexpr int64_t kCostTile = 1;
+
+int64_t subtile_cost(const GroupKeys& k, int64_t s) {
+    int64_t c = kCostStage;
+    for (int t = 0; t < kTilesPerGroup; ++t) c += (k.tile_kmax[t] > s * kSub) ? kCostTile : 0;
+    return c;
+}
+
+struct Chunk {
+    int32_t group, index, begin, end;
+};
 
 }  // namespace
 }  // namespace kvr
@@ -637,7 +788,7 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
                                           int32_t* schedule, int64_t capacity) {
     if (dtype_size(dtype) == 0) return KVR_E_UNSUPPORTED_DTYPE;
     if (n_sel < 0 || n_keys < 0 || n_sel > n_keys) return KVR_E_INVALID_ARGUMENT;
-    if (n_keys >= (int64_t(1) << 31) || n_sel >= (int64_t(1) << 31)) return KVR_E_UNSUPPORTED_SHAPE;
+    if (n_keys >= (int64_t(1) << 31) - kSub || n_sel >= (int64_t(1) << 31)) return KVR_E_UNSUPPORTED_SHAPE;
     if (n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads || head_dim <= 0) return KVR_E_UNSUPPORTED_SHAPE;
     if (n_sel > 0 && !positions) return KVR_E_NULL_POINTER;
     for (int64_t i = 0; i < n_sel; ++i) {
@@ -653,43 +804,84 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     const int64_t n_groups = (n_sel + kGroupRows - 1) / kGroupRows;
     const int64_t heads = static_cast<int64_t>(n_kv_heads) * n_head_groups;
 
-    int64_t maxk = kSub;
-    for (int64_t g = 0; g < n_groups; ++g) {
-        const int64_t k = group_kmax_host(positions, n_sel, g);
-        maxk = k > maxk ? k : maxk;
-    }
-    auto chunks_for = [&](int64_t kc) {
-        int64_t blocks = 0, worst = 0;
-        for (int64_t g = 0; g < n_groups; ++g) {
-            const int64_t c = (group_kmax_host(positions, n_sel, g) + kc - 1) / kc;
-            blocks += c;
-            worst = c > worst ? c : worst;
+    std::vector<GroupKeys> keys(static_cast<size_t>(n_groups));
+    for (int64_t g = 0; g < n_groups; ++g) keys[g] = group_keys(positions, n_sel, g);
+
+    std::vector<Chunk> chunks;
+    if (chunk_keys > 0) {
+        // Fixed chunk length (grown by 64 keys while a group would need more
+        // chunks than the merge can weigh).
+        int64_t kc = chunk_keys;
+        for (;;) {
+            int64_t worst = 0;
+            for (int64_t g = 0; g < n_groups; ++g) {
+                const int64_t c = (keys[g].kmax + kc - 1) / kc;
+                worst = c > worst ? c : worst;
+            }
+            if (worst <= kMaxChunksPerGroup) break;
+            kc += kSub;
         }
-        return std::pair<int64_t, int64_t>(blocks, worst);
-    };
-    // Chunk size: the smallest multiple of 64 keys that keeps the grid within
-    // one block per CU (256 CUs, one 4-wave block each); when even unsplit
-    // groups exceed that, groups are not split. A group whose keys fit one
-    // chunk needs no merge.
-    int64_t kc = chunk_keys;
-    if (kc == 0) {
-        const int64_t target = 256;
-        const int64_t whole = ((maxk + kSub - 1) / kSub) * kSub;
-        kc = whole;
-        for (int64_t cand = kSub; cand < whole; cand += kSub) {
-            if (chunks_for(cand).first * heads <= target) {
-                kc = cand;
-                break;
+        for (int64_t g = 0; g < n_groups; ++g) {
+            const int64_t c = (keys[g].kmax + kc - 1) / kc;
+            for (int64_t i = 0; i < c; ++i) {
+                const int64_t end = (i + 1) * kc < keys[g].kmax ? (i + 1) * kc : keys[g].kmax;
+                chunks.push_back({static_cast<int32_t>(g), static_cast<int32_t>(i), static_cast<int32_t>(i * kc),
+                                  static_cast<int32_t>(end)});
+            }
+        }
+    } else {
+        // Cost-balanced chunks: about kTargetBlocks blocks over the whole grid;
+        // a group whose cost fits one block's share is not split (no merge).
+        int64_t total = 0;
+        std::vector<int64_t> group_cost(static_cast<size_t>(n_groups), 0);
+        for (int64_t g = 0; g < n_groups; ++g) {
+            const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
+            for (int64_t s = 0; s < n_sub; ++s) group_cost[g] += subtile_cost(keys[g], s);
+            total += group_cost[g];
+        }
+        const int64_t per_head = kTargetBlocks / heads > 1 ? kTargetBlocks / heads : 1;
+        const int64_t cap = (total + per_head - 1) / per_head;
+        for (int64_t g = 0; g < n_groups; ++g) {
+            const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
+            int64_t nc = (group_cost[g] + cap - 1) / cap;
+            nc = nc < 1 ? 1 : nc;
+            nc = nc > n_sub ? n_sub : nc;
+            nc = nc > kMaxChunksPerGroup ? kMaxChunksPerGroup : nc;
+            // Boundary i closes the chunk once the running cost reaches i/nc of
+            // the group's cost, leaving at least one sub-tile per later chunk.
+            int64_t s = 0, acc = 0;
+            for (int64_t i = 0; i < nc; ++i) {
+                const int64_t begin = s;
+                if (i == nc - 1) {
+                    s = n_sub;
+                } else {
+                    const int64_t goal = group_cost[g] * (i + 1) / nc;
+                    do {
+                        acc += subtile_cost(keys[g], s);
+                        ++s;
+                    } while (acc < goal && n_sub - s > nc - 1 - i);
+                }
+                const int64_t end = s * kSub < keys[g].kmax ? s * kSub : keys[g].kmax;
+                chunks.push_back({static_cast<int32_t>(g), static_cast<int32_t>(i),
+                                  static_cast<int32_t>(begin * kSub), static_cast<int32_t>(end)});
             }
         }
     }
-    while (chunks_for(kc).second > kMaxChunksPerGroup) kc += kSub;
-    const auto counts = chunks_for(kc);
-    const int64_t n_work = counts.first;
+    const int64_t n_work = static_cast<int64_t>(chunks.size());
     if (n_work > 65535) return KVR_E_UNSUPPORTED_SHAPE;  // grid.y limit
-    int64_t n_multi = 0;
-    for (int64_t g = 0; g < n_groups; ++g) n_multi += (group_kmax_host(positions, n_sel, g) + kc - 1) / kc > 1;
-    const int64_t need = kHeader + 2 * n_groups + 2 * n_work;
+    int64_t n_multi = 0, max_chunks = 0, longest = 0;
+    std::vector<int32_t> first(static_cast<size_t>(n_groups), 0), count(static_cast<size_t>(n_groups), 0);
+    for (int64_t w = 0; w < n_work; ++w) {
+        const Chunk& c = chunks[w];
+        if (count[c.group]++ == 0) first[c.group] = static_cast<int32_t>(w);
+        const int64_t len = c.end - c.begin;
+        longest = len > longest ? len : longest;
+    }
+    for (int64_t g = 0; g < n_groups; ++g) {
+        n_multi += count[g] > 1;
+        max_chunks = count[g] > max_chunks ? count[g] : max_chunks;
+    }
+    const int64_t need = kHeader + 2 * n_groups + kWorkInts * n_work;
     if (!schedule) return need;
     if (capacity < need) return KVR_E_CAPACITY;
     int32_t* h = schedule;
@@ -698,7 +890,7 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     h[H_VERSION] = kVersion;
     h[H_NSEL] = static_cast<int32_t>(n_sel);
     h[H_NGROUPS] = static_cast<int32_t>(n_groups);
-    h[H_KC] = static_cast<int32_t>(kc);
+    h[H_KC] = static_cast<int32_t>(longest);
     h[H_NWORK] = static_cast<int32_t>(n_work);
     h[H_QT] = qt;
     h[H_NHG] = n_head_groups;
@@ -709,18 +901,18 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     h[H_NMULTI] = static_cast<int32_t>(n_multi);
     h[H_NKEYS] = static_cast<int32_t>(n_keys);
     h[H_DTYPE] = dtype;
-    h[H_MAXCHUNKS] = static_cast<int32_t>(counts.second);
+    h[H_MAXCHUNKS] = static_cast<int32_t>(max_chunks);
     int32_t* groups = h + kHeader;
     int32_t* works = groups + 2 * n_groups;
-    int64_t w = 0;
     for (int64_t g = 0; g < n_groups; ++g) {
-        const int64_t c = (group_kmax_host(positions, n_sel, g) + kc - 1) / kc;
-        groups[2 * g] = static_cast<int32_t>(w);
-        groups[2 * g + 1] = static_cast<int32_t>(c);
-        for (int64_t i = 0; i < c; ++i, ++w) {
-            works[2 * w] = static_cast<int32_t>(g);
-            works[2 * w + 1] = static_cast<int32_t>(i);
-        }
+        groups[2 * g] = first[g];
+        groups[2 * g + 1] = count[g];
+    }
+    for (int64_t w = 0; w < n_work; ++w) {
+        works[kWorkInts * w + 0] = chunks[w].group;
+        works[kWorkInts * w + 1] = chunks[w].index;
+        works[kWorkInts * w + 2] = chunks[w].begin;
+        works[kWorkInts * w + 3] = chunks[w].end;
     }
     return need;
 }
@@ -755,9 +947,9 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     if (hs[H_NSEL] != n_sel || hs[H_HQ] != n_q_heads || hs[H_HKV] != n_kv_heads || hs[H_D] != head_dim ||
         hs[H_NKEYS] != n_keys || hs[H_DTYPE] != dtype)
         return KVR_E_BAD_SCHEDULE;
-    if (schedule_len != kHeader + 2 * static_cast<int64_t>(hs[H_NGROUPS]) + 2 * static_cast<int64_t>(hs[H_NWORK]))
+    if (schedule_len != kHeader + 2 * static_cast<int64_t>(hs[H_NGROUPS]) + kWorkInts * static_cast<int64_t>(hs[H_NWORK]))
         return KVR_E_BAD_SCHEDULE;
-    if (hs[H_MAXCHUNKS] > kMaxChunksPerGroup || hs[H_KC] <= 0 || hs[H_KC] % kSub) return KVR_E_BAD_SCHEDULE;
+    if (hs[H_MAXCHUNKS] > kMaxChunksPerGroup || hs[H_NWORK] <= 0 || hs[H_NWORK] > 65535) return KVR_E_BAD_SCHEDULE;
     const int64_t ws_need = kvr_attention_workspace_bytes(hs, schedule_len, n_q_heads, head_dim);
     if (ws_need < 0) return KVR_E_BAD_SCHEDULE;
     if (workspace_bytes < ws_need || (ws_need > 0 && !workspace)) return KVR_E_WORKSPACE_TOO_SMALL;
@@ -784,26 +976,30 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     a.n_head_groups = hs[H_NHG];
     a.n_groups = hs[H_NGROUPS];
     a.n_work = hs[H_NWORK];
-    a.kc = hs[H_KC];
     a.head_dim = head_dim;
     a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
     if (ws_need > 0) {
         a.ws_ml = static_cast<float*>(workspace);
         a.ws_o = a.ws_ml + static_cast<int64_t>(n_q_heads) * a.n_work * kGroupRows * 2;
     }
-    if (a.qt * a.n_head_groups != a.group) return KVR_E_BAD_SCHEDULE;
+    if (a.qt <= 0 || a.qt * a.n_head_groups != a.group) return KVR_E_BAD_SCHEDULE;
 
-    // The MFMA kernel reads 16-byte fragments of q/k/v: unit dim strides and
-    // 16-byte aligned rows. Other layouts (strided slices, odd offsets) take
-    // the generic kernel, which accepts every schedule.
+    // The MFMA kernel reads 16-byte fragments of q/k/v (unit dim strides,
+    // 16-byte aligned rows) and indexes rows of one 64-key sub-tile in 32 bits.
+    // Other layouts (strided slices, odd offsets) take the generic kernel,
+    // which accepts every schedule.
     bool use_mfma = hs[H_KIND] == KIND_MFMA;
     if (use_mfma && !mfma_eligible(dtype, head_dim)) return KVR_E_BAD_SCHEDULE;
     for (int t = 0; t < 3 && use_mfma; ++t) {
         const int64_t* st3 = strides + 3 * t;
         if (st3[2] != 1 || (st3[0] * esize) % 16 || (st3[1] * esize) % 16) use_mfma = false;
     }
+    if (strides[4] * kSub >= (int64_t(1) << 30) || strides[7] * kSub >= (int64_t(1) << 30)) use_mfma = false;
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u)
         use_mfma = false;
+    if (!(scale > 0.f)) use_mfma = false;  // the MFMA softmax takes row maxima of unscaled scores
+    a.out_vec = strides[11] == 1 && strides[9] % 4 == 0 && strides[10] % 4 == 0 &&
+                (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
 
     hipStream_t s = as_stream(stream);
     const dim3 grid(static_cast<unsigned>(n_kv_heads * a.n_head_groups), static_cast<unsigned>(a.n_work));

@@ -73,27 +73,34 @@ def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
 
 @pytest.mark.parametrize("positions,n_keys,chunk", [
     ([0, 1, 2], 3, 0), (list(range(928, 992)), 1920, 0), (list(range(0, 4000, 7)), 4000, 256),
-    ([5, 9, 4095], 4096, 0), (list(range(1024, 2048)), 2048, 512), (list(range(100, 200)), 300, 64)])
+    ([5, 9, 4095], 4096, 0), (list(range(1024, 2048)), 2048, 512), (list(range(100, 200)), 300, 64),
+    (list(range(0, 40000, 37)), 40000, 0), ([7], 8, 0)])
 def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_keys, chunk):
     s = schedule(positions, n_keys, 32, 8, 128, chunk=chunk)
-    header, n_groups, kc, n_work = s[:16], s[3], s[4], s[5]
-    assert header[0] == 0x4B565253 and header[2] == len(positions)
+    header, n_groups, longest, n_work = s[:16], s[3], s[4], s[5]
+    assert header[0] == 0x4B565253 and header[1] == 3 and header[2] == len(positions)
     assert n_groups == (len(positions) + 63) // 64
+    assert len(s) == 16 + 2 * n_groups + 4 * n_work
     groups = [(s[16 + 2 * g], s[17 + 2 * g]) for g in range(n_groups)]
-    work = [(s[16 + 2 * n_groups + 2 * w], s[17 + 2 * n_groups + 2 * w]) for w in range(n_work)]
-    assert kc % 64 == 0 and (chunk == 0 or kc == chunk)
+    work = [tuple(s[16 + 2 * n_groups + 4 * w:20 + 2 * n_groups + 4 * w]) for w in range(n_work)]
     assert len(work) == n_work == sum(c for _, c in groups) and header[15] == max(c for _, c in groups)
-    # the work items of group g are exactly chunks 0..c-1, contiguous from its base, and
-    # the chunks reach the group's last causal key and no further
+    assert longest == max(e - b for _, _, b, e in work)
     for g, (base, count) in enumerate(groups):
-        assert work[base:base + count] == [(g, c) for c in range(count)]
+        chunks = work[base:base + count]
+        # the work items of group g are its chunks 0..c-1 in key order, contiguous from
+        # its base; they tile [0, last causal key + 1) with boundaries on 64-key multiples
+        assert [(grp, i) for grp, i, _, _ in chunks] == [(g, c) for c in range(count)]
         last = positions[min(64 * g + 63, len(positions) - 1)]
-        assert (count - 1) * kc <= last < count * kc
+        assert chunks[0][2] == 0 and chunks[-1][3] == last + 1
+        assert all(a[3] == b[2] for a, b in zip(chunks, chunks[1:]))
+        assert all(b < e and b % 64 == 0 for _, _, b, e in chunks)
+        if chunk:
+            assert all(e - b == chunk for _, _, b, e in chunks[:-1]) and chunks[-1][3] - chunks[-1][2] <= chunk
     # every (row, key <= pos) pair lies in exactly one chunk of its group
     for r, p in enumerate(positions):
         base, count = groups[r // 64]
         for key in (0, p // 2, p):
-            assert sum(1 for c in range(count) if c * kc <= key < (c + 1) * kc) == 1
+            assert sum(1 for _, _, b, e in work[base:base + count] if b <= key < e) == 1
     assert header[12] == sum(1 for _, c in groups if c > 1)  # groups needing a merge
 
 
@@ -103,9 +110,14 @@ def test_default_chunking_keeps_one_block_per_cu_for_the_c3_support():
     slots = sorted(random.Random(2).sample(range(5632 // 8), 16))
     positions = [2048 + 8 * k + i for k in slots for i in range(4)]
     s = schedule(positions, 7680, 32, 8, 128)
-    n_work, kc = s[5], s[4]
-    assert n_work * 8 <= 256 < (-(-max(positions) // (kc - 64)) if kc > 64 else 10 ** 9) * 8
-    # a group that fits one chunk is never split
+    n_work = s[5]
+    assert 24 * 8 <= n_work * 8 <= 256
+    # chunks are cost balanced: keys attended by all four row tiles cost more, so
+    # the chunks over the early keys are no longer than those over the late keys
+    work = [tuple(s[18 + 4 * w:22 + 4 * w]) for w in range(n_work)]
+    lengths = [e - b for _, _, b, e in work]
+    assert lengths[0] <= lengths[-2]
+    # a group that fits one block's share is never split
     s = schedule(list(range(15104)), 16128, 32, 8, 128)
     assert s[12] == 0 and s[5] == s[3]
 
