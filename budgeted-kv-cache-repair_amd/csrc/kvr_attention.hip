@@ -312,29 +312,6 @@ attn_mfma_kernel(AttnArgs a) {
     const int q_head = kv_head * a.group + hg * QT + hq;
     const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
 
-    W w;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int64_t row0 = group_row0 + kRowTile * (half + 2 * t);
-        const int64_t row = row0 + lq;
-        w.kmax[t] = rows_kmax(a, row0, kRowTile);
-        w.nomask_end[t] = (row0 + kRowTile <= a.n_sel) ? static_cast<int32_t>(a.positions[row0] + 1) : 0;
-        w.pos[t] = (row < a.n_sel) ? static_cast<int32_t>(a.positions[row]) : -1;
-        w.m_run[t] = -INFINITY;
-        w.l_run[t] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < W::DT; ++dt) w.o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ds = 0; ds < W::DS; ++ds) {
-            u32x4 raw = {0u, 0u, 0u, 0u};
-            if (row < a.n_sel) {
-                const int64_t off = q_head * a.qs[0] + row * a.qs[1] + (32 * ds + 8 * lj);
-                raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
-            }
-            w.qf[t][ds] = __builtin_bit_cast(v8, raw);
-        }
-    }
-
     const int32_t ks1 = static_cast<int32_t>(a.ks[1]);
     const int32_t vs1 = static_cast<int32_t>(a.vs[1]);
     const char* kbase = a.k + (static_cast<int64_t>(kv_head) * a.ks[0] + static_cast<int64_t>(key_begin) * a.ks[1]) * 2;
@@ -401,6 +378,29 @@ attn_mfma_kernel(AttnArgs a) {
             }
         }
     };
+
+    W w;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int64_t row0 = group_row0 + kRowTile * (half + 2 * t);
+        const int64_t row = row0 + lq;
+        w.kmax[t] = rows_kmax(a, row0, kRowTile);
+        w.nomask_end[t] = (row0 + kRowTile <= a.n_sel) ? static_cast<int32_t>(a.positions[row0] + 1) : 0;
+        w.pos[t] = (row < a.n_sel) ? static_cast<int32_t>(a.positions[row]) : -1;
+        w.m_run[t] = -INFINITY;
+        w.l_run[t] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < W::DT; ++dt) w.o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < W::DS; ++ds) {
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (row < a.n_sel) {
+                const int64_t off = q_head * a.qs[0] + row * a.qs[1] + (32 * ds + 8 * lj);
+                raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
+            }
+            w.qf[t][ds] = __builtin_bit_cast(v8, raw);
+        }
+    }
 
     if (n_sub > 0) {
         load(0);
@@ -575,91 +575,115 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
 }
 
 // ===========================================================================
-// Merge of multi-chunk groups. Grid (q_head, group, row block of 8 rows).
+// Merge of multi-chunk groups. Grid x = KV head x head group (as the main
+// kernel, so a head's merge blocks run on the XCD whose L2 holds its
+// partials), grid y = (group, query head of the head group, block of rows).
 // Phase 1 finds, per row, the chunks its tile attended into (a prefix of the
-// group's chunks: those starting below the tile's causal limit), and stages
-// their weights exp2(m_c - M) and the total l in LDS; phase 2 gives each
-// thread four consecutive dims of one row.
+// group's chunks: those starting below the tile's causal limit) and stages
+// their weights exp2(m_c - M) and 1 / l in LDS. Phase 2 gives each thread VEC
+// dims of one row and one of kSlices interleaved chunk slices, so a thread's
+// loads are independent; the slices are summed through LDS.
 // ===========================================================================
 constexpr int kMergeThreads = 256;
-constexpr int kMergeRows = 8;
+constexpr int kSlices = 4;
 
-template <typename T>
+__host__ __device__ inline int merge_rows_per_block(int head_dim, int vec) {
+    const int per_row = kSlices * (head_dim / vec);
+    const int rows = kMergeThreads / per_row;
+    return rows < 1 ? 1 : (rows > 8 ? 8 : rows);
+}
+
+template <typename T, int VEC>
 __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     using E = elem<T>;
     using bits = typename E::bits;
+    typedef float fvec __attribute__((ext_vector_type(VEC)));
     extern __shared__ __align__(16) char smem[];
-    const int q_head = blockIdx.x;
-    const int grp = blockIdx.y;
+    const int D = a.head_dim;
+    const int RB = merge_rows_per_block(D, VEC);
+    const int blocks_per_group = a.qt * ((kGroupRows + RB - 1) / RB);
+    const int grp = blockIdx.y / blocks_per_group;
+    const int rem = blockIdx.y - grp * blocks_per_group;
+    const int hq = rem / ((kGroupRows + RB - 1) / RB);
+    const int r0 = (rem - hq * ((kGroupRows + RB - 1) / RB)) * RB;  // first row (within the group)
+    const int kv_head = blockIdx.x / a.n_head_groups;
+    const int hg = blockIdx.x - kv_head * a.n_head_groups;
+    const int q_head = kv_head * a.group + hg * a.qt + hq;
     const int32_t* gt = group_table(a.sched);
     const int base = gt[2 * grp];
     const int n_chunks = gt[2 * grp + 1];
     if (n_chunks <= 1) return;
     const int32_t* wk = work_table(a.sched) + kWorkInts * base;
-    const int D = a.head_dim;
-    const int r0 = blockIdx.z * kMergeRows;      // first row (within the group) of this block
-    float* W = reinterpret_cast<float*>(smem);   // [kMergeRows][n_chunks]
-    float* Linv = W + kMergeRows * n_chunks;     // [kMergeRows]
-    int* NV = reinterpret_cast<int*>(Linv + kMergeRows);  // [kMergeRows] attended chunks
+    float* Red = reinterpret_cast<float*>(smem);          // [RB][kSlices][D] (16-byte aligned)
+    float* W = Red + RB * kSlices * D;                     // [RB][n_chunks]
+    float* Linv = W + RB * n_chunks;                       // [RB]
+    int* NV = reinterpret_cast<int*>(Linv + RB);           // [RB] attended chunks
     const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * kGroupRows;
     const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
+    const int64_t cstride = static_cast<int64_t>(kGroupRows);
 
-    // phase 1: 32 lanes per row reduce over the row's chunks
-    const int tr = threadIdx.x / 32;
-    const int tl = threadIdx.x % 32;
-    {
-        const int r = r0 + tr;
+    // phase 1: one wave per row
+    const int wave = threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    for (int rr = wave; rr < RB; rr += kMergeThreads / 64) {
+        const int r = r0 + rr;
         const int64_t row = group_row0 + r;
         int nv = 0;
-        if (row < a.n_sel) {
+        if (r < kGroupRows && row < a.n_sel) {
             const int32_t tk = rows_kmax(a, group_row0 + (r / kRowTile) * kRowTile, kRowTile);
-            while (nv < n_chunks && wk[kWorkInts * nv + 2] < tk) ++nv;
+            // chunk starts increase, so the attended chunks are the count of starts below tk
+            for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+                const int c = c0 + lane;
+                nv += __popcll(__ballot(c < n_chunks && wk[kWorkInts * c + 2] < tk));
+            }
             float mx = -INFINITY;
-            for (int c = tl; c < nv; c += 32)
-                mx = fmaxf(mx, a.ws_ml[(slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2]);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 32));
+            for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, a.ws_ml[(slot0 + c * cstride + r) * 2]);
+            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
             const float m_use = (mx == -INFINITY) ? 0.f : mx;
             float l = 0.f;
-            for (int c = tl; c < nv; c += 32) {
-                const int64_t s = (slot0 + static_cast<int64_t>(c) * kGroupRows + r) * 2;
+            for (int c = lane; c < nv; c += 64) {
+                const int64_t s = (slot0 + c * cstride + r) * 2;
                 const float w = exp2f(a.ws_ml[s] - m_use);
-                W[tr * n_chunks + c] = w;
+                W[rr * n_chunks + c] = w;
                 l += w * a.ws_ml[s + 1];
             }
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) l += __shfl_xor(l, off, 32);
-            if (tl == 0) Linv[tr] = 1.f / l;
+            for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+            if (lane == 0) Linv[rr] = 1.f / l;
         }
-        if (tl == 0) NV[tr] = nv;
+        if (lane == 0) NV[rr] = nv;
     }
     __syncthreads();
 
-    // phase 2: four consecutive dims of one row per thread-iteration
-    const int d4n = D / 4;
-    for (int e = threadIdx.x; e < kMergeRows * d4n; e += kMergeThreads) {
-        const int rr = e / d4n;
-        const int d = 4 * (e - rr * d4n);
+    // phase 2: (row, slice, VEC dims) per thread-iteration; independent loads
+    const int dv = D / VEC;
+    for (int e = threadIdx.x; e < RB * kSlices * dv; e += kMergeThreads) {
+        const int rr = e / (kSlices * dv);
+        const int sl = (e / dv) % kSlices;
+        const int d = (e % dv) * VEC;
+        const int r = r0 + rr;
+        fvec acc = {};
+        if (r < kGroupRows && group_row0 + r < a.n_sel) {
+            const int nv = NV[rr];
+            const float* po = a.ws_o + (slot0 + r) * D + d;
+            const float* w = W + rr * n_chunks;
+#pragma unroll 8
+            for (int c = sl; c < nv; c += kSlices)
+                acc += w[c] * *reinterpret_cast<const fvec*>(po + c * cstride * D);
+        }
+        *reinterpret_cast<fvec*>(Red + (rr * kSlices + sl) * D + d) = acc;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < RB * D; e += kMergeThreads) {
+        const int rr = e / D;
+        const int d = e - rr * D;
         const int r = r0 + rr;
         const int64_t row = group_row0 + r;
-        const int nv = NV[rr];
-        if (row >= a.n_sel) continue;
-        const float* po = a.ws_o + (slot0 + r) * D + d;
-        const float* w = W + rr * n_chunks;
-        const int64_t cstride = static_cast<int64_t>(kGroupRows) * D;
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-        int c = 0;
-        for (; c + 4 <= nv; c += 4) {
-            acc0 += w[c] * *reinterpret_cast<const f32x4*>(po + c * cstride);
-            acc1 += w[c + 1] * *reinterpret_cast<const f32x4*>(po + (c + 1) * cstride);
-            acc2 += w[c + 2] * *reinterpret_cast<const f32x4*>(po + (c + 2) * cstride);
-            acc3 += w[c + 3] * *reinterpret_cast<const f32x4*>(po + (c + 3) * cstride);
-        }
-        for (; c < nv; ++c) acc0 += w[c] * *reinterpret_cast<const f32x4*>(po + c * cstride);
-        const f32x4 acc = ((acc0 + acc1) + (acc2 + acc3)) * Linv[rr];
-        bits* op = reinterpret_cast<bits*>(a.out) + q_head * a.os[0] + row * a.os[1];
+        if (r >= kGroupRows || row >= a.n_sel) continue;
+        float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) op[(d + i) * a.os[2]] = E::from_float(acc[i]);
+        for (int sl = 0; sl < kSlices; ++sl) sum += Red[(rr * kSlices + sl) * D + d];
+        bits* op = reinterpret_cast<bits*>(a.out) + q_head * a.os[0] + row * a.os[1];
+        op[d * a.os[2]] = E::from_float(sum * Linv[rr]);
     }
 }
 
@@ -728,17 +752,27 @@ int launch_generic(const AttnArgs& a, int dmax, dim3 grid, hipStream_t s) {
     }
 }
 
-size_t merge_lds_bytes(int max_chunks) {
-    return (static_cast<size_t>(kMergeRows) * max_chunks + 2 * kMergeRows) * sizeof(float);
+size_t merge_lds_bytes(int max_chunks, int head_dim, int vec) {
+    const int rb = merge_rows_per_block(head_dim, vec);
+    return (static_cast<size_t>(rb) * max_chunks + 2 * rb + static_cast<size_t>(rb) * kSlices * head_dim) *
+           sizeof(float);
+}
+
+template <typename T, int VEC>
+int launch_merge_vec(const AttnArgs& a, int max_chunks, hipStream_t s) {
+    static const bool ok = allow_lds(attn_merge_kernel<T, VEC>, merge_lds_bytes(kMaxChunksPerGroup, 256, VEC));
+    if (!ok) return KVR_E_LAUNCH_FAILED;
+    const int rb = merge_rows_per_block(a.head_dim, VEC);
+    const unsigned y = static_cast<unsigned>(a.n_groups) * a.qt * ((kGroupRows + rb - 1) / rb);
+    if (y > 65535u) return KVR_E_UNSUPPORTED_SHAPE;
+    dim3 grid(a.n_q_heads / a.qt, y);
+    attn_merge_kernel<T, VEC><<<grid, kMergeThreads, merge_lds_bytes(max_chunks, a.head_dim, VEC), s>>>(a);
+    return launch_status();
 }
 
 template <typename T>
 int launch_merge(const AttnArgs& a, int max_chunks, hipStream_t s) {
-    static const bool ok = allow_lds(attn_merge_kernel<T>, merge_lds_bytes(kMaxChunksPerGroup));
-    if (!ok) return KVR_E_LAUNCH_FAILED;
-    dim3 grid(a.n_q_heads, a.n_groups, kGroupRows / kMergeRows);
-    attn_merge_kernel<T><<<grid, kMergeThreads, merge_lds_bytes(max_chunks), s>>>(a);
-    return launch_status();
+    return a.head_dim % 4 == 0 ? launch_merge_vec<T, 4>(a, max_chunks, s) : launch_merge_vec<T, 1>(a, max_chunks, s);
 }
 
 // Per-group causal limits on the host: group limit and the limits of its four row tiles.
