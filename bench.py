@@ -266,6 +266,36 @@ def reference_stage(model, old, old_ids, new_ids, intervals):
     return output
 
 
+# ----------------------------------------------------------------------------- HBM traffic (rocprofv3 PMC)
+TRAFFIC_SUMMARY = ROOT / "profiles" / "attention_c3_hbm_traffic.md"
+KERNEL_SOURCES = {"kvr_packed_causal_attention": "kvr_attention.hip", "kvr_shift_cache_build": "kvr_rotate.hip",
+                  "kvr_indexed_scatter_kv": "kvr_scatter.hip"}
+
+
+def source_digest(name: str) -> str:
+    import hashlib
+
+    path = ROOT / "budgeted-kv-cache-repair_amd" / "csrc" / name
+    return hashlib.sha256(path.read_bytes()).hexdigest()[:16]
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counts), or None when the
+    summary is absent or was measured on another version of the kernel source."""
+    if kernel not in KERNEL_SOURCES or not TRAFFIC_SUMMARY.exists():
+        return None
+    fields = {}
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("traffic:"):
+            for item in line[len("traffic:"):].split():
+                key, _, value = item.partition("=")
+                fields[key] = value
+    if fields.get("kernel") != kernel or fields.get("source_sha256") != source_digest(KERNEL_SOURCES[kernel]):
+        return None
+    return int(fields["bytes_per_launch"])
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(layers_sample: int, repeats: int = 10) -> dict:
     """The oracle's torch restatement of the reference stage (rotate chain +
@@ -315,6 +345,9 @@ def main(argv=None) -> int:
     parser.add_argument("--cpu-layers", type=int, default=4, help="layers in the bounded CPU-baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-reference", action="store_true", help="skip the same-GPU reference stage")
+    parser.add_argument("--calibration-copy-mib", type=int, default=0,
+                        help="after the run, copy a buffer of this many MiB three times with a plain device-to-device "
+                             "copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build runs on a single GPU (--gpus {args.gpus} requested). "
@@ -415,8 +448,9 @@ def main(argv=None) -> int:
         attn_flops / (kernels["kvr_packed_causal_attention"]["avg_us"] * 1e6)
     dominant = max(per_kernel, key=lambda n: kernels.get(n, {}).get("total_us_per_step", 0.0))
     achieved = kernels[dominant]["achieved_GBps"]
+    traffic = measured_traffic(dominant)
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                 "avg_launch_us": kernels[dominant]["avg_us"], "algorithmic_bytes_per_launch": per_kernel[dominant]}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_layers)
@@ -435,6 +469,12 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
     }
     print(json.dumps(line), flush=True)
+    if args.calibration_copy_mib > 0:
+        src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     return 0
 
 

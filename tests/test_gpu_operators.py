@@ -175,6 +175,27 @@ def test_attention_with_cancelling_large_value_channels(gpu_device, dtype):
     assert_attention_close(actual, oracle_attention(query, key, value, positions, 1.0))
 
 
+@pytest.mark.parametrize("direction", [1.0, -1.0])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_scores_drifting_along_the_key_axis(gpu_device, dtype, direction):
+    """Scores that grow (or shrink) steadily with the key index: a growing row
+    maximum moves the kernel's running softmax reference many times inside one
+    chunk and across chunks, so every rescale path and the chunk merge run."""
+    ia = ops()
+    length = 1500
+    positions = [0, 1, 2, 63, 64, 65, 200, 511, 512, 777, 1000, 1023, 1024, 1300, 1498, 1499, 1100, 1101]
+    positions = sorted(set(positions))
+    plan = ia.IndexedPlan(positions, length).to(gpu_device)
+    gen = torch.Generator(device=gpu_device).manual_seed(77)
+    q = (torch.randn((1, 8, len(positions), 128), device=gpu_device, generator=gen) * 0.1).to(dtype)
+    q[..., 0] = 1.0
+    k = (torch.randn((1, 2, length, 128), device=gpu_device, generator=gen) * 0.1).to(dtype)
+    k[..., 0] = (direction * torch.arange(length, device=gpu_device, dtype=torch.float32) * 0.25).to(dtype)
+    v = torch.randn((1, 2, length, 128), device=gpu_device, generator=gen).to(dtype)
+    actual = ia.indexed_causal_attention(q, k, v, plan, scale=0.125)
+    assert_attention_close(actual, oracle_attention(q, k, v, positions, 0.125))
+
+
 @pytest.mark.parametrize("layout", ["native", "holes"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_attention_accepts_native_transposes_storage_offsets_and_custom_scale(gpu_device, layout, dtype):
