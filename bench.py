@@ -10,8 +10,9 @@ random suffix slots (seed 2).
 
 One step = one full refresh stage, inputs resident in HBM: shift-cache build
 (prefix copy + RoPE delta rotation of every suffix K row + V copy, all layers)
--> plan upload -> packed forward through all 32 layers with the per-layer
-scatter and packed attention. Prefill, tokenisation and selection are outside
+-> plan upload -> packed forward through all 32 layers with, per layer, the
+fused fresh-row epilogue (RoPE of the fresh Q/K + K/V scatter, one launch) and
+the packed attention. Prefill, tokenisation and selection are outside
 the step, as in the reference benchmark (benchmark_refresh.py:3-9); unlike it,
 the rotation is inside.
 
@@ -120,8 +121,8 @@ def hip_stage(shim, old, old_ids, new_ids, intervals):
 class KernelTimer:
     """Brackets every libkvrepair launch with HIP events on the launching stream."""
 
-    NAMES = ("kvr_shift_cache_build", "kvr_indexed_scatter_kv", "kvr_packed_causal_attention",
-             "kvr_rope_delta_rotate")
+    NAMES = ("kvr_shift_cache_build", "kvr_rope_scatter_kv", "kvr_indexed_scatter_kv",
+             "kvr_packed_causal_attention", "kvr_rope_delta_rotate")
 
     def __init__(self):
         from kv_cache_repair_amd import _native
@@ -437,9 +438,11 @@ def main(argv=None) -> int:
     attn_bytes = (2 * len(positions) * HQ * DIM + 2 * HKV * (max_pos + 1) * DIM) * esz
     attn_flops = 4 * HQ * DIM * sum(p + 1 for p in positions)
     scatter_bytes = 2 * 2 * HKV * len(positions) * DIM * esz
+    # fresh-row epilogue: read q, k, v and cos/sin, write rotated q, cache K and V rows
+    rope_scatter_bytes = (2 * (HQ + 2 * HKV) + 2) * len(positions) * DIM * esz
     per_kernel = {
         "kvr_shift_cache_build": build_bytes, "kvr_packed_causal_attention": attn_bytes,
-        "kvr_indexed_scatter_kv": scatter_bytes}
+        "kvr_rope_scatter_kv": rope_scatter_bytes, "kvr_indexed_scatter_kv": scatter_bytes}
     for name, b in per_kernel.items():
         if name in kernels:
             kernels[name]["algorithmic_bytes"] = b

@@ -1,0 +1,281 @@
+// Fresh-row epilogue of one packed layer in ONE launch:
+//   q_out[h, r]              = rope(q[h, r], cos[r], sin[r])        (query heads)
+//   out_k[h, positions[r]]   = rope(fresh_k[h, r], cos[r], sin[r])  (KV heads)
+//   out_v[h, positions[r]]   = fresh_v[h, r]                        (bit copy)
+// where rope(x) = x * cos + rotate_half(x) * sin with split-half pairs.
+//
+// Reference semantics: the fresh rows' RoPE at absolute positions that the
+// native decoder applies before the cache update (transformers 5.15.0
+// models/llama/modeling_llama.py:137-160, apply_rotary_pos_emb with the
+// cos/sin of the model's rotary_emb), followed by the packed layer's
+// index_copy_ writeback (src/kv_cache_repair/kernels/packed_cache.py:189-191).
+// Each multiply and the add round to the storage type exactly as the eager
+// elementwise ops do, so the outputs are bit-identical to that op sequence.
+// A position outside [0, n_keys) writes no K/V row (as the scatter).
+#include "kvr_internal.h"
+
+#include <type_traits>
+
+namespace kvr {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct FreshArgs {
+    const char* q;
+    char* q_out;
+    const char* fresh[2];  // K, V
+    char* out[2];          // K, V
+    const char* cos;
+    const char* sin;
+    int64_t qs[3], qos[3], fs[2][3], os[2][3];  // {head,row,dim} element strides
+    int64_t cs[2], ss[2];                       // cos/sin {row,dim} element strides
+    const int64_t* positions;
+    int64_t n_sel;
+    int64_t n_keys;
+    int32_t n_q_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+};
+
+// One rotated pair with distinct cos/sin for the two halves (the rotary
+// embedding's halves are equal by construction, but the values are read as
+// given): lo' = lo*c_lo + (-hi)*s_lo ; hi' = hi*c_hi + lo*s_hi.
+template <typename T>
+__device__ inline void rope_pair(float lo, float hi, float c_lo, float s_lo, float c_hi, float s_hi, float& out_lo,
+                                 float& out_hi) {
+#pragma clang fp contract(off)
+    const float a0 = round_through<T>(lo * c_lo);
+    const float b0 = round_through<T>((-hi) * s_lo);
+    const float a1 = round_through<T>(hi * c_hi);
+    const float b1 = round_through<T>(lo * s_hi);
+    out_lo = round_through<T>(a0 + b0);
+    out_hi = round_through<T>(a1 + b1);
+}
+
+// Rows of the launch: [0, Hq*B) queries, then Hkv*B keys, then Hkv*B values;
+// within each part row index = r * heads + h, so the lanes of a wave walk the
+// heads of one token (contiguous in the projections' token-major storage).
+__device__ inline void decode_row(const FreshArgs& a, int64_t g, int& part, int64_t& h, int64_t& r) {
+    const int64_t nq = static_cast<int64_t>(a.n_q_heads) * a.n_sel;
+    const int64_t nkv = static_cast<int64_t>(a.n_kv_heads) * a.n_sel;
+    if (g < nq) {
+        part = 0;
+        r = g / a.n_q_heads;
+        h = g - r * a.n_q_heads;
+    } else {
+        g -= nq;
+        part = g < nkv ? 1 : 2;
+        if (part == 2) g -= nkv;
+        r = g / a.n_kv_heads;
+        h = g - r * a.n_kv_heads;
+    }
+}
+
+// Vector path: unit dim strides, 16-byte aligned rows. TPR threads share a
+// row; thread c owns the 16-byte chunk c of the first half and chunk c of the
+// second half (its rotate_half partner).
+template <typename T>
+__global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tpr_log2) {
+    using E = elem<T>;
+    using bits = typename E::bits;
+    constexpr int EPV = 16 / E::size;
+    const int tpr = 1 << tpr_log2;
+    const int64_t g = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> tpr_log2;
+    const int c = threadIdx.x & (tpr - 1);
+    const int64_t rows = (static_cast<int64_t>(a.n_q_heads) + 2 * a.n_kv_heads) * a.n_sel;
+    if (g >= rows) return;
+    int part;
+    int64_t h, r;
+    decode_row(a, g, part, h, r);
+    const int half = a.head_dim >> 1;
+    const int64_t lo_off = static_cast<int64_t>(c) * EPV;
+    const int64_t hi_off = lo_off + half;
+
+    const char* src;
+    char* dst;
+    if (part == 0) {
+        src = a.q + (h * a.qs[0] + r * a.qs[1]) * E::size;
+        dst = a.q_out + (h * a.qos[0] + r * a.qos[1]) * E::size;
+    } else {
+        const int kv = part - 1;
+        const int64_t pos = a.positions[r];
+        if (pos < 0 || pos >= a.n_keys) return;
+        src = a.fresh[kv] + (h * a.fs[kv][0] + r * a.fs[kv][1]) * E::size;
+        dst = a.out[kv] + (h * a.os[kv][0] + pos * a.os[kv][1]) * E::size;
+    }
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(src + lo_off * E::size);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(src + hi_off * E::size);
+    if (part == 2) {  // values: bit copy
+        *reinterpret_cast<u32x4*>(dst + lo_off * E::size) = lo;
+        *reinterpret_cast<u32x4*>(dst + hi_off * E::size) = hi;
+        return;
+    }
+    const char* crow = a.cos + r * a.cs[0] * E::size;
+    const char* srow = a.sin + r * a.ss[0] * E::size;
+    const u32x4 c_lo = *reinterpret_cast<const u32x4*>(crow + lo_off * E::size);
+    const u32x4 c_hi = *reinterpret_cast<const u32x4*>(crow + hi_off * E::size);
+    const u32x4 s_lo = *reinterpret_cast<const u32x4*>(srow + lo_off * E::size);
+    const u32x4 s_hi = *reinterpret_cast<const u32x4*>(srow + hi_off * E::size);
+    bits xl[EPV], xh[EPV], cl[EPV], ch[EPV], sl[EPV], sh[EPV], ol[EPV], oh[EPV];
+    __builtin_memcpy(xl, &lo, 16);
+    __builtin_memcpy(xh, &hi, 16);
+    __builtin_memcpy(cl, &c_lo, 16);
+    __builtin_memcpy(ch, &c_hi, 16);
+    __builtin_memcpy(sl, &s_lo, 16);
+    __builtin_memcpy(sh, &s_hi, 16);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+        float yl, yh;
+        rope_pair<T>(E::to_float(xl[e]), E::to_float(xh[e]), E::to_float(cl[e]), E::to_float(sl[e]),
+                     E::to_float(ch[e]), E::to_float(sh[e]), yl, yh);
+        ol[e] = E::from_float(yl);
+        oh[e] = E::from_float(yh);
+    }
+    u32x4 out_lo, out_hi;
+    __builtin_memcpy(&out_lo, ol, 16);
+    __builtin_memcpy(&out_hi, oh, 16);
+    *reinterpret_cast<u32x4*>(dst + lo_off * E::size) = out_lo;
+    *reinterpret_cast<u32x4*>(dst + hi_off * E::size) = out_hi;
+}
+
+// Scalar path: one thread per (row, pair index i < head_dim/2), any strides.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) fresh_scalar_kernel(FreshArgs a) {
+    using E = elem<T>;
+    using bits = typename E::bits;
+    const int half = a.head_dim >> 1;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t rows = (static_cast<int64_t>(a.n_q_heads) + 2 * a.n_kv_heads) * a.n_sel;
+    if (idx >= rows * half) return;
+    const int64_t g = idx / half;
+    const int64_t i = idx - g * half;
+    int part;
+    int64_t h, r;
+    decode_row(a, g, part, h, r);
+    const bits* src;
+    bits* dst;
+    int64_t sd, dd;
+    if (part == 0) {
+        src = reinterpret_cast<const bits*>(a.q) + h * a.qs[0] + r * a.qs[1];
+        dst = reinterpret_cast<bits*>(a.q_out) + h * a.qos[0] + r * a.qos[1];
+        sd = a.qs[2];
+        dd = a.qos[2];
+    } else {
+        const int kv = part - 1;
+        const int64_t pos = a.positions[r];
+        if (pos < 0 || pos >= a.n_keys) return;
+        src = reinterpret_cast<const bits*>(a.fresh[kv]) + h * a.fs[kv][0] + r * a.fs[kv][1];
+        dst = reinterpret_cast<bits*>(a.out[kv]) + h * a.os[kv][0] + pos * a.os[kv][1];
+        sd = a.fs[kv][2];
+        dd = a.os[kv][2];
+    }
+    const bits lo = src[i * sd], hi = src[(i + half) * sd];
+    if (part == 2) {
+        dst[i * dd] = lo;
+        dst[(i + half) * dd] = hi;
+        return;
+    }
+    const bits* cr = reinterpret_cast<const bits*>(a.cos) + r * a.cs[0];
+    const bits* sr = reinterpret_cast<const bits*>(a.sin) + r * a.ss[0];
+    float yl, yh;
+    rope_pair<T>(E::to_float(lo), E::to_float(hi), E::to_float(cr[i * a.cs[1]]), E::to_float(sr[i * a.ss[1]]),
+                 E::to_float(cr[(i + half) * a.cs[1]]), E::to_float(sr[(i + half) * a.ss[1]]), yl, yh);
+    dst[i * dd] = E::from_float(yl);
+    dst[(i + half) * dd] = E::from_float(yh);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T>
+int launch(const FreshArgs& a, bool vec, int tpr_log2, hipStream_t s) {
+    const int64_t rows = (static_cast<int64_t>(a.n_q_heads) + 2 * a.n_kv_heads) * a.n_sel;
+    // fp16 rows always take the scalar kernel: the vector kernel's fp16
+    // instantiation does not compile with packed fp32 instructions disabled.
+    if constexpr (!std::is_same<T, f16_t>::value) {
+        if (vec) {
+            const int64_t threads = rows << tpr_log2;
+            fresh_vec_kernel<T><<<static_cast<unsigned>(ceil_div(threads, kThreads)), kThreads, 0, s>>>(a, tpr_log2);
+            return launch_status();
+        }
+    }
+    const int64_t threads = rows * (a.head_dim / 2);
+    fresh_scalar_kernel<T><<<static_cast<unsigned>(ceil_div(threads, kThreads)), kThreads, 0, s>>>(a);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace kvr
+
+extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh_k, const void* fresh_v, void* out_k,
+                                   void* out_v, const void* cos, const void* sin, const int64_t* positions,
+                                   int64_t n_sel, int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys,
+                                   int32_t head_dim, const int64_t strides[18], const int64_t cs_strides[4],
+                                   int32_t dtype, void* stream) {
+    using namespace kvr;
+    const int esize = dtype_size(dtype);
+    if (esize == 0) return KVR_E_UNSUPPORTED_DTYPE;
+    if (n_sel < 0 || n_keys < 0) return KVR_E_INVALID_ARGUMENT;
+    if (n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || (head_dim & 1)) return KVR_E_UNSUPPORTED_SHAPE;
+    if (!strides || !cs_strides) return KVR_E_NULL_POINTER;
+    for (int i = 0; i < 18; ++i)
+        if (strides[i] <= 0) return KVR_E_BAD_STRIDE;
+    for (int i = 0; i < 4; ++i)
+        if (cs_strides[i] < 0 || (i % 2 == 1 && cs_strides[i] == 0)) return KVR_E_BAD_STRIDE;
+    if (n_sel == 0) return KVR_OK;
+    if (!q || !q_out || !fresh_k || !fresh_v || !out_k || !out_v || !cos || !sin || !positions)
+        return KVR_E_NULL_POINTER;
+
+    FreshArgs a;
+    a.q = static_cast<const char*>(q);
+    a.q_out = static_cast<char*>(q_out);
+    a.fresh[0] = static_cast<const char*>(fresh_k);
+    a.fresh[1] = static_cast<const char*>(fresh_v);
+    a.out[0] = static_cast<char*>(out_k);
+    a.out[1] = static_cast<char*>(out_v);
+    a.cos = static_cast<const char*>(cos);
+    a.sin = static_cast<const char*>(sin);
+    for (int i = 0; i < 3; ++i) {
+        a.qs[i] = strides[i];
+        a.qos[i] = strides[3 + i];
+        a.fs[0][i] = strides[6 + i];
+        a.fs[1][i] = strides[9 + i];
+        a.os[0][i] = strides[12 + i];
+        a.os[1][i] = strides[15 + i];
+    }
+    a.cs[0] = cs_strides[0];
+    a.cs[1] = cs_strides[1];
+    a.ss[0] = cs_strides[2];
+    a.ss[1] = cs_strides[3];
+    a.positions = positions;
+    a.n_sel = n_sel;
+    a.n_keys = n_keys;
+    a.n_q_heads = n_q_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+
+    // Vector path: each half splits into a power-of-two number of 16-byte chunks.
+    const int64_t half_bytes = static_cast<int64_t>(head_dim / 2) * esize;
+    bool vec = half_bytes % 16 == 0;
+    int tpr_log2 = 0;
+    if (vec) {
+        const int64_t chunks = half_bytes / 16;
+        while ((int64_t(1) << tpr_log2) < chunks) ++tpr_log2;
+        vec = (int64_t(1) << tpr_log2) == chunks && tpr_log2 <= 6;
+    }
+    for (int t = 0; t < 6 && vec; ++t) {
+        const int64_t* st = strides + 3 * t;
+        vec = st[2] == 1 && (st[0] * esize) % 16 == 0 && (st[1] * esize) % 16 == 0;
+    }
+    vec = vec && cs_strides[1] == 1 && cs_strides[3] == 1 && (cs_strides[0] * esize) % 16 == 0 &&
+          (cs_strides[2] * esize) % 16 == 0;
+    vec = vec && aligned16(q) && aligned16(q_out) && aligned16(fresh_k) && aligned16(fresh_v) && aligned16(out_k) &&
+          aligned16(out_v) && aligned16(cos) && aligned16(sin);
+
+    hipStream_t s = as_stream(stream);
+    switch (dtype) {
+        case KVR_DTYPE_F32: return launch<f32_t>(a, vec, tpr_log2, s);
+        case KVR_DTYPE_F16: return launch<f16_t>(a, vec, tpr_log2, s);
+        default: return launch<bf16_t>(a, vec, tpr_log2, s);
+    }
+}

@@ -212,6 +212,21 @@ def _scatter_native(out_k, out_v, fresh_k, fresh_v, positions: torch.Tensor, n_s
     _native.check(status, "kvr_indexed_scatter_kv")
 
 
+def _rope_scatter_native(query, query_out, out_k, out_v, fresh_k, fresh_v, cos, sin, positions: torch.Tensor,
+                        n_sel: int) -> None:
+    """Launch kvr_rope_scatter_kv on the current stream (shapes already checked)."""
+    _, hq, _, dim = query.shape
+    _, hkv, n_keys, _ = out_k.shape
+    strides = _native.i64_array(_native.strides3(query) + _native.strides3(query_out) + _native.strides3(fresh_k)
+                                + _native.strides3(fresh_v) + _native.strides3(out_k) + _native.strides3(out_v))
+    cs = _native.i64_array([int(cos.stride(-2)), int(cos.stride(-1)), int(sin.stride(-2)), int(sin.stride(-1))])
+    status = _native.lib().kvr_rope_scatter_kv(
+        query.data_ptr(), query_out.data_ptr(), fresh_k.data_ptr(), fresh_v.data_ptr(), out_k.data_ptr(),
+        out_v.data_ptr(), cos.data_ptr(), sin.data_ptr(), positions.data_ptr(), int(n_sel), int(hq), int(hkv),
+        int(n_keys), int(dim), strides, cs, _native.DTYPE_CODES[query.dtype], _native.stream_handle(query.device))
+    _native.check(status, "kvr_rope_scatter_kv")
+
+
 def _attention_native(q, k, v, out, device_plan: "DeviceIndexedPlan", scale: float) -> None:
     """Launch kvr_packed_causal_attention into ``out`` (shapes already checked)."""
     _, hq, n_sel, dim = q.shape
@@ -258,6 +273,50 @@ def indexed_kv_scatter_(out_k, out_v, fresh_k, fresh_v, device_plan) -> None:
     _require_gfx950(out_k.device)
     with torch.cuda.device(out_k.device):
         _scatter_native(out_k, out_v, fresh_k, fresh_v, device_plan.positions, device_plan.selected_count)
+
+
+def rope_indexed_kv_scatter_(query, query_out, out_k, out_v, fresh_k, fresh_v, cos, sin, device_plan) -> None:
+    """Fresh-row epilogue of one layer in one launch: RoPE of the fresh queries
+    (into ``query_out``) and keys at their absolute positions, then the keys and
+    values scattered into ``out_k``/``out_v`` at the plan's positions.
+
+    query/query_out=[1,Hq,B,D], fresh_k/fresh_v=[1,Hkv,B,D], out_k/out_v=
+    [1,Hkv,N,D], cos/sin=[1,B,D] (the rotary embedding of the selected
+    positions, in the tensors' dtype). Bit-identical to the native
+    ``apply_rotary_pos_emb`` (transformers 5.15.0 modeling_llama.py:137-160)
+    followed by ``indexed_kv_scatter_`` (reference indexed_attention.py:179-204);
+    the reference runs these as separate eager ops. Every other storage byte of
+    the outputs is preserved.
+    """
+    tensors = (query, query_out, out_k, out_v, fresh_k, fresh_v)
+    _validate_tensors(tensors, dtypes=_NATIVE_DTYPES, dims=None)
+    _validate_plan(device_plan, out_k.device)
+    _, hq, n_sel, dim = query.shape
+    _, hkv, _, _ = out_k.shape
+    if dim % 2:
+        raise ValueError("rotary head dimension must be even")
+    if query_out.shape != query.shape or any(t.shape[1] != hkv or t.shape[3] != dim for t in tensors[2:]):
+        raise ValueError("query/KV head geometry must match")
+    if any(t.shape[2] != device_plan.logical_length for t in (out_k, out_v)):
+        raise ValueError("output sequence length must match the plan")
+    if any(t.shape[2] != device_plan.selected_count for t in (query, fresh_k, fresh_v)):
+        raise ValueError("fresh sequence length must match selected_count")
+    for table in (cos, sin):
+        if (not isinstance(table, torch.Tensor) or table.dtype != query.dtype or table.device != query.device
+                or table.shape[-2:] != (n_sel, dim) or table.numel() != n_sel * dim or table.stride(-1) <= 0
+                or table.stride(-2) < 0):
+            raise ValueError("cos/sin must be [1, selected_count, head_dim] in the query dtype and device")
+    if not device_plan.selected_count:
+        return
+    storage = [t.untyped_storage().data_ptr() for t in tensors]
+    writes, reads = storage[1:4], [storage[0], *storage[4:], cos.untyped_storage().data_ptr(),
+                                   sin.untyped_storage().data_ptr()]
+    if len(set(writes)) != 3 or any(w == r for w in writes for r in reads):
+        raise ValueError("output query/K/V storage must be independent of each other and of the inputs")
+    _require_gfx950(out_k.device)
+    with torch.cuda.device(out_k.device):
+        _rope_scatter_native(query, query_out, out_k, out_v, fresh_k, fresh_v, cos, sin, device_plan.positions,
+                             device_plan.selected_count)
 
 
 def indexed_causal_attention(q, k, v, device_plan, scale=None):

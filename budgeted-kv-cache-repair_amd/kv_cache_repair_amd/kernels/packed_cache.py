@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import copy
 import ctypes
+import types
 from dataclasses import dataclass, field
 from threading import Lock
 from typing import Any, Sequence
@@ -83,6 +84,16 @@ class _Launcher:
             _native.stream_handle(self.device))
         _native.check(status, "kvr_indexed_scatter_kv")
 
+    def rope_scatter(self, q, q_out, fresh_k, fresh_v, keys, values, cos, sin) -> None:
+        status = _native.lib().kvr_rope_scatter_kv(
+            q.data_ptr(), q_out.data_ptr(), fresh_k.data_ptr(), fresh_v.data_ptr(), keys.data_ptr(),
+            values.data_ptr(), cos.data_ptr(), sin.data_ptr(), self.positions_ptr, self.n_sel, self.q_heads,
+            self.kv_heads, self.n_keys, self.head_dim,
+            self._stride_array((q, q_out, fresh_k, fresh_v, keys, values)),
+            _native.i64_array([int(cos.stride(-2)), int(cos.stride(-1)), int(sin.stride(-2)), int(sin.stride(-1))]),
+            self.dtype_code, _native.stream_handle(self.device))
+        _native.check(status, "kvr_rope_scatter_kv")
+
     def attention(self, q, k, v, out_view, scale: float) -> None:
         status = _native.lib().kvr_packed_causal_attention(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out_view.data_ptr(), self.positions_ptr, self.n_sel,
@@ -132,9 +143,53 @@ def _register_attention() -> None:
             ALL_ATTENTION_FUNCTIONS.register(_ATTENTION_NAME, _packed_attention)
 
 
-def _make_native_view(base):
+def _fused_attention_forward(self, hidden_states, position_embeddings=None, attention_mask=None,
+                             past_key_values=None, sur_packed_context=None, **kwargs):
+    """Attention block of a packed layer shell with the fresh-row epilogue fused.
+
+    The same computation as the native Llama/Qwen3 attention forward
+    (transformers 5.15.0 modeling_llama.py:243-293, modeling_qwen3.py:231-276)
+    routed through the packed plugin points: projections (and Qwen3's per-head
+    q/k RMSNorm) run as the module's own layers; RoPE of the fresh queries and
+    keys at their absolute positions, the key/value scatter into the cache and
+    the cache-update bookkeeping are ONE libkvrepair launch
+    (kvr_rope_scatter_kv, bit-identical to apply_rotary_pos_emb + the packed
+    layer's scatter); then the packed attention and o_proj. Bound only to the
+    executor's private module shells, never to the caller's modules.
+    """
+    context = sur_packed_context
+    if not isinstance(context, _PackedContext):
+        raise RuntimeError("packed attention requires explicit per-call request context")
+    if attention_mask is not None:
+        raise RuntimeError("native dense mask construction must be bypassed for packed attention")
+    if position_embeddings is None:
+        raise RuntimeError("packed fused epilogue requires the model's rotary embeddings")
+    if not isinstance(past_key_values, Cache) or not isinstance(past_key_values.layers[self.layer_idx], _PackedLayer):
+        raise RuntimeError("packed fused epilogue requires the packed cache layers")
+    input_shape = hidden_states.shape[:-1]
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    query = self.q_proj(hidden_states).view(hidden_shape)
+    key = self.k_proj(hidden_states).view(hidden_shape)
+    value = self.v_proj(hidden_states).view(hidden_shape)
+    q_norm = getattr(self, "q_norm", None)
+    if q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
+        query = q_norm(query)
+        key = self.k_norm(key)
+    cos, sin = position_embeddings
+    layer = past_key_values.layers[self.layer_idx]
+    rotated = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    layer.fused_update(query.transpose(1, 2), rotated.transpose(1, 2), key.transpose(1, 2), value.transpose(1, 2),
+                       cos, sin)
+    launcher = context.launcher
+    out = torch.empty(query.shape, dtype=query.dtype, device=query.device)  # [1, B, Hq, D]
+    launcher.attention(rotated.transpose(1, 2), layer.keys, layer.values, out.transpose(1, 2), float(self.scaling))
+    return self.o_proj(out.reshape(*input_shape, -1)), None
+
+
+def _make_native_view(base, fused_epilogue: bool = True):
     """Shallow module shells sharing parameters, with a private config naming the
-    packed attention; the caller's modules and config are never modified."""
+    packed attention; the caller's modules and config are never modified. With
+    ``fused_epilogue`` the attention shells run _fused_attention_forward."""
     _register_attention()
     config = copy.deepcopy(base.config)
     config._attn_implementation = _ATTENTION_NAME
@@ -150,6 +205,8 @@ def _make_native_view(base):
         attention = copy.copy(original.self_attn)
         attention._modules = original.self_attn._modules.copy()
         attention.config = config
+        if fused_epilogue:
+            attention.forward = types.MethodType(_fused_attention_forward, attention)
         layer._modules["self_attn"] = attention
         layers.append(layer)
     view._modules["layers"] = torch.nn.ModuleList(layers)
@@ -232,6 +289,30 @@ class _PackedLayer(DynamicLayer):
         self.updated = True
         return self.keys, self.values
 
+    def fused_update(self, query, query_out, key_states, value_states, cos, sin):
+        """Fresh-row epilogue: rotate queries (into ``query_out``) and keys at the
+        context positions, scatter the keys and values into this layer."""
+        if self.updated:
+            raise RuntimeError("packed native forward updated one layer more than once")
+        positions = self._context.positions
+        n_sel = positions.numel()
+        expected = (*self.keys.shape[:2], n_sel, self.keys.shape[-1])
+        for source, target in ((key_states, self.keys), (value_states, self.values)):
+            if source.shape != expected or source.dtype != target.dtype or source.device != target.device:
+                raise RuntimeError("packed native projection geometry/dtype/device drifted")
+        if (query.shape != query_out.shape or query.shape[2:] != (n_sel, self.keys.shape[-1])
+                or query.dtype != self.keys.dtype):
+            raise RuntimeError("packed native query geometry/dtype drifted")
+        for table in (cos, sin):
+            if table.shape[-2:] != (n_sel, self.keys.shape[-1]) or table.dtype != self.keys.dtype \
+                    or table.numel() != n_sel * self.keys.shape[-1]:
+                raise RuntimeError("packed native rotary embedding geometry/dtype drifted")
+        if self._backend != "hip":
+            raise RuntimeError("unknown packed writeback backend")
+        self._context.launcher.rope_scatter(query, query_out, key_states, value_states, self.keys, self.values,
+                                            cos, sin)
+        self.updated = True
+
 
 def _launcher(device_plan: DeviceIndexedPlan, config, key: torch.Tensor) -> _Launcher:
     q_heads, kv_heads, dim = int(config.num_attention_heads), int(key.shape[1]), int(key.shape[3])
@@ -279,7 +360,7 @@ def _receipt(intervals, selected, length, layer_count, attention_backend, writeb
 
 @torch.no_grad()
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
-                  attention_backend: str, writeback_backend: str) -> None:
+                  attention_backend: str, writeback_backend: str, fused_epilogue: bool = True) -> None:
     """Run the packed forward, scattering into the caller-owned ``output`` cache."""
     base = shim._base_transformer(shim.generator)
     device_plan = host_plan.to(edited_ids_t.device)
@@ -287,7 +368,7 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
     key0 = layer_kv(output, 0)[0]
     context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan,
                              _launcher(device_plan, base.config, key0))
-    native_view = _make_native_view(base)
+    native_view = _make_native_view(base, fused_epilogue)
     layers = [_PackedLayer(*layer_kv(output, i), context, writeback_backend) for i in range(layer_count)]
     cache = Cache(layers=layers)
     result = native_view(input_ids=edited_ids_t.index_select(1, positions), position_ids=positions.unsqueeze(0),
@@ -299,7 +380,8 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
 @torch.no_grad()
 def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
                            intervals: Sequence[tuple[int, int]], *, attention_backend: str = "hip",
-                           writeback_backend: str = "hip", plan: Any = None) -> tuple[Any, dict[str, Any]]:
+                           writeback_backend: str = "hip", plan: Any = None,
+                           fused_epilogue: bool = True) -> tuple[Any, dict[str, Any]]:
     """Recompute sorted selected rows in one native layer-major forward.
 
     Same signature, validation order, receipt and ownership contract as the
@@ -308,6 +390,9 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     exactly these intervals and length. The borrowed ``base_cache`` is never
     mutated: a nonempty repair returns an independently owned cache (one
     libkvrepair copy launch), an empty one returns ``base_cache`` itself.
+    ``fused_epilogue`` (default) fuses each layer's fresh-row RoPE with the
+    K/V scatter (one launch); False runs the native RoPE ops and the registered
+    cache-update/attention plugin points. Both give bit-identical caches.
     """
     _check_backends(attention_backend, writeback_backend)
     _check_ids(edited_ids_t)
@@ -326,13 +411,15 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     from ..cache import clone_cache
 
     output = clone_cache(base_cache)
-    _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend)
+    _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend,
+                  bool(fused_epilogue))
     return output, receipt
 
 
 @torch.no_grad()
 def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tensor,
-                          intervals: Sequence[tuple[int, int]], *, plan: Any = None) -> dict[str, Any]:
+                          intervals: Sequence[tuple[int, int]], *, plan: Any = None,
+                          fused_epilogue: bool = True) -> dict[str, Any]:
     """Packed refresh that scatters IN PLACE into a cache the caller owns.
 
     For a cache the caller has just built and nobody else references (the
@@ -354,5 +441,5 @@ def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tenso
         return receipt
     _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
-    _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip")
+    _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue))
     return receipt

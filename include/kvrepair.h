@@ -118,6 +118,30 @@ int kvr_indexed_scatter_kv(void* out_k, void* out_v, const void* fresh_k, const 
                            int32_t head_dim, const int64_t strides[12], int32_t dtype, void* stream);
 
 /*
+ * Fresh-row epilogue of one packed layer in ONE launch (RoPE at absolute
+ * positions fused with the indexed K/V scatter):
+ *   q_out[0, h, r, :]            = rope(q[0, h, r, :], cos[r], sin[r])        h < n_q_heads
+ *   out_k[0, h, positions[r], :] = rope(fresh_k[0, h, r, :], cos[r], sin[r])  h < n_kv_heads
+ *   out_v[0, h, positions[r], :] = fresh_v[0, h, r, :]                        (bit copy)
+ * rope(x) = x * cos + rotate_half(x) * sin (split-half pairs), every multiply
+ * and the add rounded to `dtype` as the eager elementwise ops round them, so
+ * the result is bit-identical to the native decoder's apply_rotary_pos_emb
+ * (transformers 5.15.0 models/llama/modeling_llama.py:137-160) followed by the
+ * packed layer's index_copy_ writeback
+ * (src/kv_cache_repair/kernels/packed_cache.py:189-191). The reference runs
+ * these as separate eager ops; this entry fuses them (no reference
+ * counterpart of its own). cos/sin: the rotary embedding's [1, n_sel, head_dim]
+ * values in `dtype`; cs_strides = {cos row, cos dim, sin row, sin dim} element
+ * strides (row strides may be 0). strides: 18 element strides {head,row,dim}
+ * for q, q_out, fresh_k, fresh_v, out_k, out_v. Positions outside [0, n_keys)
+ * write no K/V row. head_dim must be even. n_sel == 0 enqueues nothing.
+ */
+int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh_k, const void* fresh_v, void* out_k,
+                        void* out_v, const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,
+                        int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
+                        const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream);
+
+/*
  * Host-side work schedule for kvr_packed_causal_attention (no device access).
  * Splits the selected rows into row groups and each group's causal key range
  * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`

@@ -133,6 +133,80 @@ def test_empty_plan_has_no_writes_and_empty_attention_result(gpu_device, length)
     assert bits_equal(key, saved) and bits_equal(value, saved)
 
 
+# --------------------------------------------------------------------------- fused fresh-row epilogue
+def rotary_tables(positions, dim, dtype, device, theta=10000.0):
+    """cos/sin of the selected positions exactly as HF's default rotary_emb makes them."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    config = LlamaConfig(hidden_size=4 * dim, num_attention_heads=4, head_dim=dim, rope_theta=theta)
+    rotary = LlamaRotaryEmbedding(config).to(device)
+    pos = torch.tensor(positions, device=device).unsqueeze(0)
+    probe = torch.empty(1, dtype=dtype, device=device)
+    return rotary(probe, pos)
+
+
+@pytest.mark.parametrize("layout", ["contiguous", "native", "holes"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim", [64, 128])
+def test_rope_scatter_matches_native_rotary_then_index_copy(gpu_device, dtype, dim, layout):
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    ia = ops()
+    torch.manual_seed(dim + len(layout))
+    positions = [0, 3, 4, 8, 9, 63, 64, 129, 200, 4000]
+    n = 4001
+    plan = ia.IndexedPlan(positions, n).to(gpu_device)
+    q = view((1, 8, len(positions), dim), dtype, layout, gpu_device)[1]
+    fk = view((1, 2, len(positions), dim), dtype, layout, gpu_device)[1]
+    fv = view((1, 2, len(positions), dim), dtype, layout, gpu_device)[1]
+    q.mul_(4)  # in place: the views keep their layouts
+    fk.mul_(4)
+    out_k_backing, out_k = view((1, 2, n, dim), dtype, "holes" if layout == "holes" else "contiguous", gpu_device)
+    out_v_backing, out_v = view((1, 2, n, dim), dtype, "contiguous", gpu_device)
+    ref_k_backing, ref_v_backing = out_k_backing.clone(), out_v_backing.clone()
+    ref_k = ref_k_backing.as_strided(out_k.shape, out_k.stride(), out_k.storage_offset())
+    ref_v = ref_v_backing.as_strided(out_v.shape, out_v.stride(), out_v.storage_offset())
+    cos, sin = rotary_tables(positions, dim, dtype, gpu_device)
+    q_out = torch.empty_like(q)
+    ia.rope_indexed_kv_scatter_(q, q_out, out_k, out_v, fk, fv, cos, sin, plan)
+    q_ref, k_ref = apply_rotary_pos_emb(q, fk, cos, sin)
+    ref_k.index_copy_(2, plan.positions, k_ref)
+    ref_v.index_copy_(2, plan.positions, fv)
+    assert bits_equal(q_out, q_ref)
+    assert bits_equal(out_k_backing, ref_k_backing) and bits_equal(out_v_backing, ref_v_backing)
+    # oracle: the reference rotation (cache.py:47-77 arithmetic) of each row with its own cos/sin
+    c_host = cos[0].float().cpu().numpy()
+    s_host = sin[0].float().cpu().numpy()
+    qh, kh = host_bits(q[0]), host_bits(fk[0])
+    for r in range(len(positions)):
+        cs = (c_host[r, : dim // 2], s_host[r, : dim // 2])
+        expect_q = orc.rope_rotate(np.ascontiguousarray(qh[:, r:r + 1]), CODE[dtype], 1, np.zeros(dim // 2, np.float32),
+                                   cos_sin=cs)
+        expect_k = orc.rope_rotate(np.ascontiguousarray(kh[:, r:r + 1]), CODE[dtype], 1, np.zeros(dim // 2, np.float32),
+                                   cos_sin=cs)
+        assert np.array_equal(host_bits(q_out[0][:, r:r + 1]), expect_q)
+        assert np.array_equal(host_bits(out_k[0][:, positions[r]:positions[r] + 1]), expect_k)
+
+
+def test_rope_scatter_rejects_aliasing_and_bad_tables(gpu_device):
+    ia = ops()
+    positions = [1, 5]
+    plan = ia.IndexedPlan(positions, 8).to(gpu_device)
+    q = torch.randn(1, 4, 2, 64, device=gpu_device, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 2, 64, device=gpu_device, dtype=torch.bfloat16)
+    ck = torch.zeros(1, 2, 8, 64, device=gpu_device, dtype=torch.bfloat16)
+    cv = torch.zeros_like(ck)
+    cos, sin = rotary_tables(positions, 64, torch.bfloat16, gpu_device)
+    with pytest.raises(ValueError, match="independent"):
+        ia.rope_indexed_kv_scatter_(q, q, ck, cv, k, k.clone(), cos, sin, plan)
+    with pytest.raises(ValueError, match="cos/sin"):
+        ia.rope_indexed_kv_scatter_(q, torch.empty_like(q), ck, cv, k, k.clone(), cos.float(), sin, plan)
+    with pytest.raises(ValueError, match="cos/sin"):
+        ia.rope_indexed_kv_scatter_(q, torch.empty_like(q), ck, cv, k, k.clone(), cos[:, :1], sin, plan)
+    assert not ck.any() and not cv.any()
+
+
 # --------------------------------------------------------------------------- attention
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dim", [64, 128])

@@ -200,7 +200,7 @@ def test_failed_transaction_keeps_model_and_base_unchanged(gpu_device, monkeypat
             raise RuntimeError("injected failure")
         return SimpleNamespace(past_key_values=DynamicCache() if failure == "replaced_cache" else cache)
 
-    monkeypatch.setattr(module, "_make_native_view", lambda base: failing_forward)
+    monkeypatch.setattr(module, "_make_native_view", lambda base, *args: failing_forward)
     with pytest.raises(RuntimeError):
         module.packed_interval_repair(shim, base, ids + 13, [(3, 5)])
     for i, layer in enumerate(base.layers):
@@ -325,3 +325,27 @@ def test_bf16_8b_layer_geometry_refresh_matches_reference(gpu_device):
             assert_north_star_close(a[:, :, 928:992], e[:, :, 928:992], ref.layer_kv(control, i)[c][:, :, 928:992])
             assert_within_native_precision_floor(a[:, :, 928:992], e[:, :, 928:992],
                                                  ref.layer_kv(control, i)[c][:, :, 928:992])
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fused_fresh_row_epilogue_is_bit_identical_to_native_rope_and_scatter(gpu_device, family, dtype):
+    """The fused epilogue (kvr_rope_scatter_kv inside the attention shells) and the
+    plugin path (native apply_rotary_pos_emb, then the cache layer's scatter and
+    the registered attention) produce the same cache bits and next-token logits."""
+    from kv_cache_repair_amd.kernels.packed_cache import packed_interval_repair
+
+    model = make_model(gpu_device, family, kv_heads=2, head_dim=64, dtype=dtype, layers=3)
+    shim, ids, base = make_request(model, length=140)
+    edited = ids.clone()
+    edited[0, 70:] = (edited[0, 70:] + 7) % 97
+    intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
+    fused, _ = packed_interval_repair(shim, base, edited, intervals)
+    plain, _ = packed_interval_repair(shim, base, edited, intervals, fused_epilogue=False)
+    for a, b in zip(fused.layers, plain.layers):
+        assert bits_equal(a.keys, b.keys) and bits_equal(a.values, b.values)
+    with torch.no_grad():
+        nxt = torch.tensor([[5]], device=gpu_device)
+        la = model(input_ids=nxt, past_key_values=fused, use_cache=True).logits
+        lb = model(input_ids=nxt, past_key_values=plain, use_cache=True).logits
+    assert bits_equal(la, lb)

@@ -23,7 +23,7 @@ def declared_symbols() -> list[str]:
 def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted([
         "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
-        "kvr_indexed_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
+        "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
         "kvr_packed_causal_attention"])
 
 
@@ -57,6 +57,14 @@ def test_entry_points_validate_before_any_launch():
                                            None, None, 0, 2, None) == -3  # heads not divisible
     assert lib.kvr_packed_causal_attention(None, None, None, None, None, 3, 4, 2, 9, 64, float("nan"), strides,
                                            None, 0, None, None, 0, 2, None) == -1
+    s18, cs4 = _native.i64_array([1] * 18), _native.i64_array([128, 1, 128, 1])
+    nine = (None,) * 9
+    assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 64, s18, cs4, 9, None) == -2  # dtype
+    assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 63, s18, cs4, 2, None) == -3  # odd head_dim
+    assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 64, _native.i64_array([0] * 18), cs4, 2, None) == -4
+    assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 64, s18, _native.i64_array([128, 0, 128, 1]), 2, None) == -4
+    assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 64, s18, cs4, 2, None) == -5
+    assert lib.kvr_rope_scatter_kv(*nine, 0, 4, 2, 8, 64, s18, cs4, 2, None) == 0
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
