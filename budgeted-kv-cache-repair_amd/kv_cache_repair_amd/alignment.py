@@ -6,6 +6,8 @@ starts). Same definitions as the reference (src/kv_cache_repair/alignment.py:6-3
 
 from __future__ import annotations
 
+import numpy as np
+
 
 def shared_prefix_len(left: list[int], right: list[int]) -> int:
     limit = min(len(left), len(right))
@@ -35,5 +37,33 @@ def token_alignment(old_ids: list[int], new_ids: list[int]) -> dict[str, int]:
         "old_suffix_start": old_start,
         "new_suffix_start": new_start,
         "mandatory_changed_tokens": len(new_ids) - prefix - suffix,
+        "position_shift": new_start - old_start,
+    }
+
+
+def token_alignment_arrays(old_ids: np.ndarray, new_ids: np.ndarray) -> dict[str, int]:
+    """token_alignment of two 1-D integer arrays (same definitions, vectorised):
+    the shared prefix is the first mismatch of the common-length heads, the
+    shared suffix the first mismatch of the reversed tails, capped so it does
+    not overlap the prefix."""
+    old_ids = np.asarray(old_ids).reshape(-1)
+    new_ids = np.asarray(new_ids).reshape(-1)
+    limit = min(old_ids.size, new_ids.size)
+    diff = np.flatnonzero(old_ids[:limit] != new_ids[:limit])
+    prefix = int(diff[0]) if diff.size else limit
+    tail = limit - prefix
+    if tail:
+        rdiff = np.flatnonzero(old_ids[old_ids.size - tail:][::-1] != new_ids[new_ids.size - tail:][::-1])
+        suffix = int(rdiff[0]) if rdiff.size else tail
+    else:
+        suffix = 0
+    old_start = int(old_ids.size) - suffix
+    new_start = int(new_ids.size) - suffix
+    return {
+        "prefix": prefix,
+        "suffix": suffix,
+        "old_suffix_start": old_start,
+        "new_suffix_start": new_start,
+        "mandatory_changed_tokens": int(new_ids.size) - prefix - suffix,
         "position_shift": new_start - old_start,
     }

@@ -17,7 +17,7 @@ import torch
 from transformers.cache_utils import DynamicCache, DynamicLayer
 
 from . import _native
-from .alignment import token_alignment
+from .alignment import token_alignment, token_alignment_arrays
 from .kernels.executor import layer_kv
 
 
@@ -187,9 +187,11 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     into freshly allocated, independently owned tensors; the old cache is
     never mutated.
     """
-    old_ids = [int(v) for v in old_input_ids[0].tolist()]
-    new_ids = [int(v) for v in new_input_ids[0].tolist()]
-    align = token_alignment(old_ids, new_ids)
+    n_old = int(old_input_ids.shape[1])
+    ids = torch.cat((old_input_ids[0].reshape(-1), new_input_ids[0].reshape(-1).to(old_input_ids.dtype)))
+    ids = ids.cpu().numpy()  # one device-to-host copy for both id rows
+    align = token_alignment_arrays(ids[:n_old], ids[n_old:])
+    n_new = int(new_input_ids.shape[1])
     halo = min(max(int(halo_tokens), 0), align["suffix"])
     recompute_end = align["new_suffix_start"] + halo
     old_tail_start = align["old_suffix_start"] + halo
@@ -199,12 +201,12 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     generator = getattr(model, "generator", model)
     k0 = old[0][0]
     inv_freq, scaling, rotary_dim = _rotary(generator, k0.device)
-    shape = (1, k0.shape[1], len(new_ids), k0.shape[3])
-    new = [(torch.empty(shape, dtype=k0.dtype, device=k0.device), torch.empty(shape, dtype=k0.dtype, device=k0.device))
-           for _ in old]
+    # one allocation for every layer's K and V; each layer gets contiguous [1, Hkv, N, D] views
+    slab = torch.empty((len(old), 2, 1, k0.shape[1], n_new, k0.shape[3]), dtype=k0.dtype, device=k0.device)
+    new = [(slab[i, 0], slab[i, 1]) for i in range(len(old))]
     if recompute_end == align["prefix"]:
         # No recomputed rows: prefix copy + shifted tail in one launch.
-        if len(new_ids):
+        if n_new:
             _shift_rows([k for k, _ in old], [v for _, v in old], [k for k, _ in new], [v for _, v in new],
                         prefix_rows=align["prefix"], old_tail_start=old_tail_start, new_tail_start=recompute_end,
                         tail_rows=tail_rows, shift=align["position_shift"], inv_freq=inv_freq, scaling=scaling,

@@ -143,6 +143,74 @@ def _register_attention() -> None:
             ALL_ATTENTION_FUNCTIONS.register(_ATTENTION_NAME, _packed_attention)
 
 
+def _silu_activations() -> tuple[type, ...]:
+    from transformers.activations import SiLUActivation
+
+    return (torch.nn.SiLU, SiLUActivation)
+
+
+_SILU_ACTIVATIONS = _silu_activations()
+
+
+def _rms_norm(module, x: torch.Tensor, residual: torch.Tensor | None = None):
+    """One kvr_rms_norm launch with ``module``'s weight and epsilon over the last
+    dim of contiguous ``x``; with ``residual`` also returns s = residual + x."""
+    weight = module.weight
+    if x.dtype != weight.dtype or not x.is_contiguous() or weight.numel() != x.shape[-1] \
+            or (residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype
+                                          or not residual.is_contiguous())):
+        raise RuntimeError("packed fused RMSNorm geometry/dtype drifted")
+    hidden = int(x.shape[-1])
+    rows = x.numel() // hidden
+    out = torch.empty_like(x)
+    summed = torch.empty_like(x) if residual is not None else None
+    status = _native.lib().kvr_rms_norm(
+        x.data_ptr(), residual.data_ptr() if residual is not None else None,
+        summed.data_ptr() if summed is not None else None, out.data_ptr(), weight.data_ptr(), rows, hidden,
+        _native.i64_array([hidden] * 4), float(module.variance_epsilon), _native.DTYPE_CODES[x.dtype],
+        _native.stream_handle(x.device))
+    _native.check(status, "kvr_rms_norm")
+    return out if residual is None else (out, summed)
+
+
+def _silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    if gate.shape != up.shape or gate.dtype != up.dtype or not gate.is_contiguous() or not up.is_contiguous():
+        raise RuntimeError("packed fused MLP activation geometry/dtype drifted")
+    out = torch.empty_like(gate)
+    status = _native.lib().kvr_silu_mul(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                                        _native.DTYPE_CODES[gate.dtype], _native.stream_handle(gate.device))
+    _native.check(status, "kvr_silu_mul")
+    return out
+
+
+def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
+                         use_cache=False, position_embeddings=None, **kwargs):
+    """Decoder layer of a packed shell with its elementwise work fused.
+
+    The native Llama/Qwen3 decoder layer (transformers 5.15.0
+    modeling_llama.py:301-330, modeling_qwen3.py:287-316): input RMSNorm,
+    attention, residual add, post-attention RMSNorm, SiLU-gated MLP, residual
+    add. Each RMSNorm is one kvr_rms_norm launch (the first residual add fused
+    into the second norm) and the MLP activation product one kvr_silu_mul
+    launch; projections stay the module's own linear layers.
+    """
+    normed = _rms_norm(self.input_layernorm, hidden_states)
+    attended, _ = self.self_attn(hidden_states=normed, attention_mask=attention_mask, position_ids=position_ids,
+                                 past_key_values=past_key_values, use_cache=use_cache,
+                                 position_embeddings=position_embeddings, **kwargs)
+    normed, residual = _rms_norm(self.post_attention_layernorm, attended, residual=hidden_states)
+    mlp = self.mlp
+    if isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
+        out = mlp.down_proj(_silu_mul(mlp.gate_proj(normed), mlp.up_proj(normed)))
+    else:
+        out = mlp(normed)
+    return residual + out
+
+
+def _fused_norm_forward(self, hidden_states):
+    return _rms_norm(self, hidden_states)
+
+
 def _fused_attention_forward(self, hidden_states, position_embeddings=None, attention_mask=None,
                              past_key_values=None, sur_packed_context=None, **kwargs):
     """Attention block of a packed layer shell with the fresh-row epilogue fused.
@@ -173,8 +241,12 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     value = self.v_proj(hidden_states).view(hidden_shape)
     q_norm = getattr(self, "q_norm", None)
     if q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
-        query = q_norm(query)
-        key = self.k_norm(key)
+        if getattr(self, "_kvr_fused_norms", False):
+            query = _rms_norm(q_norm, query)
+            key = _rms_norm(self.k_norm, key)
+        else:
+            query = q_norm(query)
+            key = self.k_norm(key)
     cos, sin = position_embeddings
     layer = past_key_values.layers[self.layer_idx]
     rotated = torch.empty(query.shape, dtype=query.dtype, device=query.device)
@@ -186,10 +258,11 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     return self.o_proj(out.reshape(*input_shape, -1)), None
 
 
-def _make_native_view(base, fused_epilogue: bool = True):
+def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True):
     """Shallow module shells sharing parameters, with a private config naming the
     packed attention; the caller's modules and config are never modified. With
-    ``fused_epilogue`` the attention shells run _fused_attention_forward."""
+    ``fused_epilogue`` the attention shells run _fused_attention_forward; with
+    ``fused_layers`` the layer and final-norm shells run their fused forwards."""
     _register_attention()
     config = copy.deepcopy(base.config)
     config._attn_implementation = _ATTENTION_NAME
@@ -207,10 +280,17 @@ def _make_native_view(base, fused_epilogue: bool = True):
         attention.config = config
         if fused_epilogue:
             attention.forward = types.MethodType(_fused_attention_forward, attention)
+            attention._kvr_fused_norms = fused_layers
+        if fused_layers:
+            layer.forward = types.MethodType(_fused_layer_forward, layer)
         layer._modules["self_attn"] = attention
         layers.append(layer)
     view._modules["layers"] = torch.nn.ModuleList(layers)
     view.layers.training = False
+    if fused_layers:
+        norm = copy.copy(base.norm)
+        norm.forward = types.MethodType(_fused_norm_forward, norm)
+        view._modules["norm"] = norm
     return view
 
 
@@ -359,8 +439,18 @@ def _receipt(intervals, selected, length, layer_count, attention_backend, writeb
 
 
 @torch.no_grad()
+def _fused_layers_for(fused_layers, dtype: torch.dtype) -> bool:
+    """Default: fuse the layer elementwise ops for 16-bit caches only. Their fp32
+    mean of squares may differ from the eager chain by an ulp, which is below
+    16-bit storage precision; fp32 runs keep the eager ops unless asked."""
+    if fused_layers is None:
+        return dtype in (torch.float16, torch.bfloat16)
+    return bool(fused_layers)
+
+
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
-                  attention_backend: str, writeback_backend: str, fused_epilogue: bool = True) -> None:
+                  attention_backend: str, writeback_backend: str, fused_epilogue: bool = True,
+                  fused_layers: bool | None = None) -> None:
     """Run the packed forward, scattering into the caller-owned ``output`` cache."""
     base = shim._base_transformer(shim.generator)
     device_plan = host_plan.to(edited_ids_t.device)
@@ -368,7 +458,7 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
     key0 = layer_kv(output, 0)[0]
     context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan,
                              _launcher(device_plan, base.config, key0))
-    native_view = _make_native_view(base, fused_epilogue)
+    native_view = _make_native_view(base, fused_epilogue, _fused_layers_for(fused_layers, key0.dtype))
     layers = [_PackedLayer(*layer_kv(output, i), context, writeback_backend) for i in range(layer_count)]
     cache = Cache(layers=layers)
     result = native_view(input_ids=edited_ids_t.index_select(1, positions), position_ids=positions.unsqueeze(0),
@@ -380,8 +470,8 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
 @torch.no_grad()
 def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
                            intervals: Sequence[tuple[int, int]], *, attention_backend: str = "hip",
-                           writeback_backend: str = "hip", plan: Any = None,
-                           fused_epilogue: bool = True) -> tuple[Any, dict[str, Any]]:
+                           writeback_backend: str = "hip", plan: Any = None, fused_epilogue: bool = True,
+                           fused_layers: bool | None = None) -> tuple[Any, dict[str, Any]]:
     """Recompute sorted selected rows in one native layer-major forward.
 
     Same signature, validation order, receipt and ownership contract as the
@@ -393,6 +483,10 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     ``fused_epilogue`` (default) fuses each layer's fresh-row RoPE with the
     K/V scatter (one launch); False runs the native RoPE ops and the registered
     cache-update/attention plugin points. Both give bit-identical caches.
+    ``fused_layers`` runs each decoder layer's RMSNorms (with the residual
+    add) and MLP activation as single launches; its fp32 mean of squares can
+    differ from the eager chain by an ulp, so the default (None) fuses them for
+    fp16/bf16 caches only.
     """
     _check_backends(attention_backend, writeback_backend)
     _check_ids(edited_ids_t)
@@ -412,14 +506,14 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
 
     output = clone_cache(base_cache)
     _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend,
-                  bool(fused_epilogue))
+                  bool(fused_epilogue), fused_layers)
     return output, receipt
 
 
 @torch.no_grad()
 def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tensor,
                           intervals: Sequence[tuple[int, int]], *, plan: Any = None,
-                          fused_epilogue: bool = True) -> dict[str, Any]:
+                          fused_epilogue: bool = True, fused_layers: bool | None = None) -> dict[str, Any]:
     """Packed refresh that scatters IN PLACE into a cache the caller owns.
 
     For a cache the caller has just built and nobody else references (the
@@ -441,5 +535,6 @@ def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tenso
         return receipt
     _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
-    _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue))
+    _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue),
+                  fused_layers)
     return receipt

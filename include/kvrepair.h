@@ -142,6 +142,34 @@ int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh_k, const v
                         const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream);
 
 /*
+ * RMSNorm of `rows` rows of `hidden` elements, with an optional residual add
+ * in front (one launch):
+ *   s   = residual == NULL ? x : dtype(residual + x)      (s written to residual_out)
+ *   out = dtype(weight * dtype(s * rsqrt(mean(s^2) + eps)))
+ * Replaces the native decoder's RMSNorm op chain (transformers 5.15.0
+ * models/llama/modeling_llama.py:52-69, models/qwen3/modeling_qwen3.py:50-64)
+ * and the residual add before the post-attention norm (modeling_llama.py:316-320)
+ * for the packed refresh rows; the reference runs them as eager ops (no
+ * counterpart of its own). The mean of squares is accumulated in fp32 in this
+ * kernel's order, so an element may differ from the eager chain by one unit in
+ * the last place of `dtype`. All rows have unit-stride dims; row_strides =
+ * {x, residual, residual_out, out} row strides in elements. weight: `hidden`
+ * elements of `dtype`. rows == 0 enqueues nothing.
+ */
+int kvr_rms_norm(const void* x, const void* residual, void* residual_out, void* out, const void* weight,
+                 int64_t rows, int32_t hidden, const int64_t row_strides[4], float eps, int32_t dtype,
+                 void* stream);
+
+/*
+ * Gated activation of the MLP, one launch over n contiguous elements:
+ *   out = dtype(dtype(silu(gate)) * up),  silu(g) = g / (1 + exp(-g)) in fp32
+ * Replaces act_fn(gate_proj(x)) * up_proj(x) of the native MLP
+ * (transformers 5.15.0 models/llama/modeling_llama.py:174-175) for the packed
+ * rows (two eager launches; no reference counterpart of its own).
+ */
+int kvr_silu_mul(const void* gate, const void* up, void* out, int64_t n, int32_t dtype, void* stream);
+
+/*
  * Host-side work schedule for kvr_packed_causal_attention (no device access).
  * Splits the selected rows into row groups and each group's causal key range
  * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`

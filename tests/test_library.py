@@ -24,7 +24,7 @@ def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted([
         "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
         "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
-        "kvr_packed_causal_attention"])
+        "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -65,6 +65,16 @@ def test_entry_points_validate_before_any_launch():
     assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 64, s18, _native.i64_array([128, 0, 128, 1]), 2, None) == -4
     assert lib.kvr_rope_scatter_kv(*nine, 4, 4, 2, 8, 64, s18, cs4, 2, None) == -5
     assert lib.kvr_rope_scatter_kv(*nine, 0, 4, 2, 8, 64, s18, cs4, 2, None) == 0
+    rs = _native.i64_array([4096] * 4)
+    assert lib.kvr_rms_norm(None, None, None, None, None, 4, 4096, rs, 1e-5, 7, None) == -2
+    assert lib.kvr_rms_norm(None, None, None, None, None, 4, 0, rs, 1e-5, 2, None) == -1
+    assert lib.kvr_rms_norm(None, None, None, None, None, 4, 4096, rs, float("nan"), 2, None) == -1
+    assert lib.kvr_rms_norm(None, None, None, None, None, 4, 4096, _native.i64_array([-1] * 4), 1e-5, 2, None) == -4
+    assert lib.kvr_rms_norm(None, None, None, None, None, 4, 4096, rs, 1e-5, 2, None) == -5
+    assert lib.kvr_rms_norm(None, None, None, None, None, 0, 4096, rs, 1e-5, 2, None) == 0
+    assert lib.kvr_silu_mul(None, None, None, 8, 5, None) == -2
+    assert lib.kvr_silu_mul(None, None, None, -1, 2, None) == -1
+    assert lib.kvr_silu_mul(None, None, None, 8, 2, None) == -5
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):

@@ -300,6 +300,33 @@ def test_alignment_golden_vectors(old, new, expect):
     assert tuple(got.values()) == expect
 
 
+@pytest.mark.parametrize("old,new,expect", [
+    ([1, 2, 9, 3, 4], [1, 2, 3, 4], (2, 2, 3, 2, 0, -1)),
+    ([1, 2], [1, 2], (2, 0, 2, 2, 0, 0)),
+    ([1, 2], [], (0, 0, 2, 0, 0, -2)),
+    ([1, 2, 3], [1, 8, 9, 3], (1, 1, 2, 3, 2, 1)),
+])
+def test_package_alignment_matches_golden_vectors_and_oracle(old, new, expect):
+    """The package's list and vectorised alignments against the reference's
+    golden tuples (tests/test_cache.py:43-68) and the C oracle on random edits."""
+    import numpy as np
+
+    from kv_cache_repair_amd.alignment import token_alignment, token_alignment_arrays
+
+    assert tuple(token_alignment(old, new).values()) == expect
+    assert tuple(token_alignment_arrays(np.array(old, dtype=np.int64), np.array(new, dtype=np.int64)).values()) == \
+        expect
+    rng = random.Random(len(old) * 7 + len(new))
+    for _ in range(300):
+        base = [rng.randrange(4) for _ in range(rng.randrange(0, 40))]
+        a, b = rng.randrange(len(base) + 1), rng.randrange(len(base) + 1)
+        a, b = min(a, b), max(a, b)
+        edited = base[:a] + [rng.randrange(4) for _ in range(rng.randrange(0, 5))] + base[b:]
+        want = orc.token_alignment(base, edited)
+        assert token_alignment(base, edited) == want
+        assert token_alignment_arrays(np.array(base, dtype=np.int64), np.array(edited, dtype=np.int64)) == want
+
+
 def test_positions_to_intervals_kat_and_brute_force():
     # reference tests/test_cache.py:161-162
     assert orc.positions_to_intervals([5, 2, 3, 2, 8, 6]) == [(2, 4), (5, 7), (8, 9)]
