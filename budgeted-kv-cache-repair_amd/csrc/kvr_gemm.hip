@@ -1,0 +1,477 @@
+// Skinny projection GEMMs of the packed refresh rows (gfx950 MFMA):
+//   y[m, r] = sum_k x[m, k] * w[r, k]        m < M <= 64, bf16 / fp16, fp32 accumulation
+// i.e. torch.nn.functional.linear(x, w) without bias, the q/k/v/o and MLP
+// projections of every decoder layer (transformers 5.15.0
+// models/llama/modeling_llama.py:165-175, 243-252). With only the selected
+// rows (M = 64 at a 64-token budget) the projections stream the layer's
+// weights once and do little arithmetic per byte, so the kernel is built to
+// stream W from HBM: every weight byte is read once, straight into MFMA
+// registers with a deep prefetch, while the block's rows of x sit in LDS.
+//
+// One launch can stream up to three weights (their rows concatenated, e.g.
+// q/k/v into one [M, nq + nk + nv] output), or a gate/up pair whose epilogue
+// applies the SiLU-gated product (the MLP's act_fn(gate) * up) so the two
+// projections never reach HBM.
+//
+// Work split: block = 4 waves x 16 streamed weight rows (64 rows) x one K
+// slice. The slice is walked in chunks of 256: x[:, chunk] is staged in one of
+// two LDS buffers (the next chunk's global loads are in flight while the
+// current one is multiplied) and shared by the 4 waves; W streams straight
+// into MFMA registers through a ring of 8 fragments per lane (one chunk
+// ahead). Split-K slices (S > 1) write fp32 partial tiles to a workspace and a
+// second launch sums them in slice order, so results are deterministic.
+#include "kvr_internal.h"
+
+#include <string.h>
+
+namespace kvr {
+namespace {
+
+#ifndef KVR_GEMM_WAVES
+#define KVR_GEMM_WAVES 4
+#endif
+#ifndef KVR_GEMM_CHUNK_STEPS
+#define KVR_GEMM_CHUNK_STEPS 8
+#endif
+#ifndef KVR_GEMM_NT
+#define KVR_GEMM_NT 1
+#endif
+#ifndef KVR_GEMM_RING_CHUNKS
+#define KVR_GEMM_RING_CHUNKS 1
+#endif
+#ifndef KVR_GEMM_BURST
+#define KVR_GEMM_BURST 0
+#endif
+
+constexpr int kWaves = KVR_GEMM_WAVES;      // waves per block, 16 streamed weight rows each
+constexpr int kGemmThreads = 64 * kWaves;
+constexpr int kTileN = 16 * kWaves;         // streamed weight rows per block
+constexpr int kHalf = kTileN / 2;           // gated: output columns per block
+constexpr int kRowsMax = 64;                // M <= 64 (four 16-row MFMA tiles)
+constexpr int kStep = 32;                   // K per MFMA
+constexpr int kChunkSteps = KVR_GEMM_CHUNK_STEPS;  // k-steps per staged x chunk = W ring depth
+constexpr int kChunk = kChunkSteps * kStep; // K per chunk
+constexpr int kXStride = kChunk + 8;        // LDS row stride (elements): 16 B pad, conflict-free B reads
+constexpr int kXBuf = kRowsMax * kXStride;  // one chunk buffer (elements)
+constexpr int kRingChunks = KVR_GEMM_RING_CHUNKS;  // W ring depth in chunks
+constexpr int kRing = kRingChunks * kChunkSteps;   // W fragments in flight per lane (k-steps)
+static_assert(kRingChunks == 1 || kRingChunks == 2, "chunk buffers alternate with the ring");
+constexpr int kGranules = kChunk / 8;       // 16-B x granules per row per chunk
+constexpr int kXLoads = kRowsMax * kGranules / kGemmThreads;  // x granules per thread per chunk
+static_assert(kXLoads * kGemmThreads == kRowsMax * kGranules && kGemmThreads % kGranules == 0, "x staging map");
+constexpr int kMinSlice = 512;              // K per split at least (bounds the partial traffic)
+constexpr int kTargetBlocks = 256;          // split until the grid covers every CU once
+constexpr int kRedStride = kTileN + 4;      // fp32 LDS tile of the gated epilogue
+constexpr int kTile = kRowsMax * kTileN;    // fp32 elements of one partial tile
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct gemm_t;
+template <> struct gemm_t<bf16_t> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct gemm_t<f16_t> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+struct GemmArgs {
+    const char* x;                  // [M][ldx]
+    const char* w0;                 // weights: [rows_i][ldw_i]
+    const char* w1;
+    const char* w2;
+    char* y;                        // [M][ldy]
+    float* partial;                 // [n_tiles][S][64][kTileN] fp32 (S > 1)
+    int64_t ldx, ldy, ldw0, ldw1, ldw2;
+    int32_t end0, end1;             // concatenated row boundaries of w0 | w1 | w2
+    int32_t rows;                   // streamed rows in total
+    int32_t n_out;                  // output columns (gated: rows / 2)
+    int32_t gated;                  // 1: y = silu(x w0^T) * (x w1^T)
+    int32_t m, k;
+    int32_t slice;                  // K per split (multiple of kStep)
+    int32_t splits;                 // S
+};
+
+// MFMA roles: A = W (16 streamed rows x 32 k; lane holds w[row lq][k + 8lj ..]),
+// B = x^T (32 k x 16 rows of x; lane holds x[m0 + lq][k + 8lj ..]) from LDS;
+// D: lane holds the products of x row m0 + lq with streamed rows 4lj + i, i < 4.
+//
+// Streamed row layout of a block (tile): the rows of wave w are
+// tile*kTileN + 16w + 0..15 (concatenated weights); gated: the first half of
+// the waves stream gate rows tile*kHalf + 16w + 0..15 and the second half the
+// same rows of up. The fp32 tile (column c = 16w + 4lj + i) thus holds gate
+// in columns [0, kHalf) and up in [kHalf, kTileN) in gated mode.
+template <typename T, int MT>
+__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+skinny_gemm_kernel(GemmArgs a) {
+    using G = gemm_t<T>;
+    using E = elem<T>;
+    using v8 = typename G::v8;
+    extern __shared__ __align__(16) char smem[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // two chunk buffers [64][kXStride]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lq = lane & 15;
+    const int lj = lane >> 4;
+    const int tile = blockIdx.x;
+    const int split = blockIdx.y;
+    const int k0 = split * a.slice;
+    const int klen = (a.k - k0 < a.slice) ? a.k - k0 : a.slice;  // > 0, multiple of 8
+
+    // ---- this lane's streamed weight row ----
+    const char* wb;
+    int64_t ldw;
+    int local;
+    bool row_ok;
+    if (a.gated) {
+        const bool up = wave >= kWaves / 2;
+        local = tile * kHalf + 16 * (up ? wave - kWaves / 2 : wave) + lq;
+        row_ok = local < a.n_out;
+        wb = up ? a.w1 : a.w0;
+        ldw = up ? a.ldw1 : a.ldw0;
+    } else {
+        const int g = tile * kTileN + 16 * wave + lq;
+        row_ok = g < a.rows;
+        if (g < a.end0) {
+            wb = a.w0; ldw = a.ldw0; local = g;
+        } else if (g < a.end1) {
+            wb = a.w1; ldw = a.ldw1; local = g - a.end0;
+        } else {
+            wb = a.w2; ldw = a.ldw2; local = g - a.end1;
+        }
+    }
+    if (!row_ok) local = 0;
+
+    // ---- W ring: the fragment of k-step s lives in wf[s % kRing] ----
+    // Loads are unconditional, so the wait before each MFMA covers only the
+    // fragment it consumes: rows past the end read row 0 (their outputs are
+    // never written) and k offsets past the slice are clamped to its last 8
+    // elements (in bounds; they meet the zeroed tail of the staged x, so they
+    // contribute 0 * w = 0 for finite w).
+    const char* wrow = wb + (static_cast<int64_t>(local) * ldw + k0) * 2;
+    const int klast = klen - 8;
+    u32x4 wf[kRing];
+    auto load_w = [&](int s) __attribute__((always_inline)) -> u32x4 {
+        const int kk = min(s * kStep + 8 * lj, klast);
+#if KVR_GEMM_NT
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + kk * 2));
+#else
+        return *reinterpret_cast<const u32x4*>(wrow + kk * 2);
+#endif
+    };
+
+    // ---- x chunks: thread t stages granules (row (threads / G) i + t / G, 8 (t % G)) ----
+    const int xrow = tid / kGranules;
+    const int xcol = 8 * (tid % kGranules);
+    const char* xbase = a.x + k0 * 2;
+    u32x4 xr[kXLoads];
+    auto load_x = [&](int c) __attribute__((always_inline)) {
+        const int kk = min(c * kChunk + xcol, klast);
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            const int r = (kGemmThreads / kGranules) * i + xrow;
+            xr[i] = *reinterpret_cast<const u32x4*>(xbase + (static_cast<int64_t>(r < a.m ? r : 0) * a.ldx + kk) * 2);
+        }
+    };
+    auto store_x = [&](int c, uint16_t* buf) __attribute__((always_inline)) {
+        const bool k_ok = c * kChunk + xcol < klen;  // klen is a multiple of 8
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            const int r = (kGemmThreads / kGranules) * i + xrow;
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(buf + r * kXStride + xcol) = (k_ok && r < a.m) ? xr[i] : zero;
+        }
+    };
+
+    const int chunks = (klen + kChunk - 1) / kChunk;
+    load_x(0);
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) wf[d] = load_w(d);
+    store_x(0, xs);
+    __syncthreads();
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Chunk c: issue chunk c + 1's x loads, multiply chunk c (refilling each W
+    // slot with the fragment kRing steps ahead right after its MFMAs, so the
+    // load reuses the slot's registers), then store chunk c + 1 into the other
+    // buffer. The loop advances kRingChunks chunks at a time so every ring slot
+    // index is static; a chunk past the last one multiplies an all-zero x
+    // buffer (store_x zeroes k >= klen) and adds nothing. Past the slice the
+    // loads repeat in-bounds addresses into the idle buffer or unread slots.
+    // sched_barrier pins the loads where they are written: left alone, the
+    // scheduler sinks them to the end of the chunk and exposes their latency.
+    for (int c = 0; c < chunks; c += kRingChunks) {
+#pragma unroll
+        for (int r = 0; r < kRingChunks; ++r) {
+            const int cc = c + r;
+            const uint16_t* cur = xs + (cc & 1) * kXBuf;
+            load_x(cc + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int d = 0; d < kChunkSteps; ++d) {
+                const int slot = r * kChunkSteps + d;
+                const v8 af = __builtin_bit_cast(v8, wf[slot]);
+                u32x4 bf[MT];
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    bf[t] = *reinterpret_cast<const u32x4*>(cur + (16 * t + lq) * kXStride + d * kStep + 8 * lj);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) acc[t] = G::mma(af, __builtin_bit_cast(v8, bf[t]), acc[t]);
+#if !KVR_GEMM_BURST
+                wf[slot] = load_w(cc * kChunkSteps + d + kRing);
+                __builtin_amdgcn_sched_barrier(0);
+#endif
+            }
+#if KVR_GEMM_BURST
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int d = 0; d < kChunkSteps; ++d) wf[r * kChunkSteps + d] = load_w(cc * kChunkSteps + d + kRing);
+            __builtin_amdgcn_sched_barrier(0);
+#endif
+            store_x(cc + 1, xs + ((cc + 1) & 1) * kXBuf);
+            __syncthreads();
+        }
+    }
+
+    uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+    // ---- single split: write y from registers (gated: through an LDS tile) ----
+    if (a.splits == 1) {
+        if (!a.gated) {
+            const int c0 = tile * kTileN + 16 * wave + 4 * lj;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int m = 16 * t + lq;
+                if (m >= a.m) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (c0 + i < a.rows) y[static_cast<int64_t>(m) * a.ldy + c0 + i] = E::from_float(acc[t][i]);
+            }
+            return;
+        }
+        float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            *reinterpret_cast<f32x4*>(red + (16 * t + lq) * kRedStride + 16 * wave + 4 * lj) = acc[t];
+        __syncthreads();
+        for (int e = tid; e < 16 * MT * kHalf; e += kGemmThreads) {
+            const int m = e / kHalf;
+            const int c = e % kHalf;
+            const int col = tile * kHalf + c;
+            if (m < a.m && col < a.n_out) {
+                const float g = round_through<T>(red[m * kRedStride + c]);
+                const float u = round_through<T>(red[m * kRedStride + kHalf + c]);
+                y[static_cast<int64_t>(m) * a.ldy + col] = E::from_float(silu_gate<T>(g, u));
+            }
+        }
+        return;
+    }
+
+    // ---- split K: fp32 partial tile [64 rows of x][kTileN streamed rows] ----
+    float* part = a.partial + (static_cast<int64_t>(tile) * a.splits + split) * kTile;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        *reinterpret_cast<f32x4*>(part + (16 * t + lq) * kTileN + 16 * wave + 4 * lj) = acc[t];
+}
+
+// Split-K reduction (a second launch, so every partial is visible): block
+// (tile, 16-row group) sums the S partials of its rows in slice order, four
+// columns per thread, four slices' loads in flight at a time, and writes y
+// (gated: the SiLU-gated product of the gate and up sums).
+constexpr int kReduceThreads = 256;
+
+template <typename T>
+__global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(GemmArgs a) {
+    using E = elem<T>;
+    const int tile = blockIdx.x;
+    const int group = blockIdx.y;
+    const f32x4* base = reinterpret_cast<const f32x4*>(a.partial) + static_cast<int64_t>(tile) * a.splits * (kTile / 4);
+    auto sum_splits = [&](int e4) __attribute__((always_inline)) -> f32x4 {
+        f32x4 sum = base[e4];
+        int sp = 1;
+        for (; sp + 4 <= a.splits; sp += 4) {
+            const f32x4 p0 = base[(sp + 0) * (kTile / 4) + e4];
+            const f32x4 p1 = base[(sp + 1) * (kTile / 4) + e4];
+            const f32x4 p2 = base[(sp + 2) * (kTile / 4) + e4];
+            const f32x4 p3 = base[(sp + 3) * (kTile / 4) + e4];
+            sum += p0;
+            sum += p1;
+            sum += p2;
+            sum += p3;
+        }
+        for (; sp < a.splits; ++sp) sum += base[sp * (kTile / 4) + e4];
+        return sum;
+    };
+    uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+    if (!a.gated) {
+        for (int e = threadIdx.x; e < 16 * kTileN / 4; e += kReduceThreads) {
+            const int m = 16 * group + e / (kTileN / 4);
+            const int c = 4 * (e % (kTileN / 4));
+            if (m >= a.m) continue;
+            const f32x4 sum = sum_splits(m * (kTileN / 4) + c / 4);
+            const int col = tile * kTileN + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (col + i < a.rows) y[static_cast<int64_t>(m) * a.ldy + col + i] = E::from_float(sum[i]);
+        }
+    } else {
+        for (int e = threadIdx.x; e < 16 * kHalf / 4; e += kReduceThreads) {
+            const int m = 16 * group + e / (kHalf / 4);
+            const int c = 4 * (e % (kHalf / 4));
+            if (m >= a.m) continue;
+            const f32x4 g = sum_splits(m * (kTileN / 4) + c / 4);
+            const f32x4 u = sum_splits(m * (kTileN / 4) + kHalf / 4 + c / 4);
+            const int col = tile * kHalf + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (col + i < a.n_out)
+                    y[static_cast<int64_t>(m) * a.ldy + col + i] =
+                        E::from_float(silu_gate<T>(round_through<T>(g[i]), round_through<T>(u[i])));
+        }
+    }
+}
+
+constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2;  // two x chunk buffers
+static_assert(kLdsBytes >= static_cast<size_t>(kRowsMax) * kRedStride * 4, "gated epilogue tile fits");
+
+template <typename F>
+bool allow_lds(F fn, size_t bytes) {
+    if (bytes <= 65536) return true;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(bytes)) == hipSuccess;
+}
+
+template <typename T, int MT>
+int launch_mt(const GemmArgs& a, hipStream_t s) {
+    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT>, kLdsBytes);
+    if (!ok) return KVR_E_LAUNCH_FAILED;
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, kTileN)), static_cast<unsigned>(a.splits));
+    skinny_gemm_kernel<T, MT><<<grid, kGemmThreads, kLdsBytes, s>>>(a);
+    if (a.splits > 1)
+        splitk_reduce_kernel<T><<<dim3(grid.x, static_cast<unsigned>(MT)), kReduceThreads, 0, s>>>(a);
+    return launch_status();
+}
+
+template <typename T>
+int launch(const GemmArgs& a, hipStream_t s) {
+    switch ((a.m + 15) / 16) {
+        case 1: return launch_mt<T, 1>(a, s);
+        case 2: return launch_mt<T, 2>(a, s);
+        case 3: return launch_mt<T, 3>(a, s);
+        default: return launch_mt<T, 4>(a, s);
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace kvr
+
+using namespace kvr;
+
+// K split of a launch: the smallest power of two giving >= kTargetBlocks
+// blocks, at most k / kMinSlice; slices are whole 256-chunks, so the split
+// count is then ceil(k / slice).
+namespace {
+struct Split {
+    int32_t splits;
+    int32_t slice;
+};
+
+Split plan_split(int32_t rows, int32_t k) {
+    const int64_t tiles = ceil_div(rows, kTileN);
+    int32_t want = 1;
+    while (tiles * want < kTargetBlocks && want < 64) want *= 2;
+    const int32_t cap = k / kMinSlice > 1 ? k / kMinSlice : 1;
+    const int32_t s = want < cap ? want : cap;
+    const int32_t slice = static_cast<int32_t>(ceil_div(ceil_div(k, s), kChunk) * kChunk);
+    return Split{static_cast<int32_t>(ceil_div(k, slice)), slice};
+}
+}  // namespace
+
+extern "C" int32_t kvr_linear_splits(int32_t m, int32_t rows, int32_t k) {
+    if (m <= 0 || m > kRowsMax || rows <= 0 || k <= 0 || k % 8) return KVR_E_UNSUPPORTED_SHAPE;
+    return plan_split(rows, k).splits;
+}
+
+extern "C" int64_t kvr_linear_workspace_bytes(int32_t m, int32_t rows, int32_t k) {
+    const int32_t splits = kvr_linear_splits(m, rows, k);
+    if (splits < 0) return splits;
+    if (splits == 1) return 0;
+    return ceil_div(rows, kTileN) * splits * static_cast<int64_t>(kRowsMax) * kTileN * 4;
+}
+
+extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
+                                const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy,
+                                int32_t epilogue, void* workspace, int64_t workspace_bytes, int32_t dtype,
+                                void* stream) {
+    if (dtype != KVR_DTYPE_BF16 && dtype != KVR_DTYPE_F16) return KVR_E_UNSUPPORTED_DTYPE;
+    if (n_weights < 1 || n_weights > 3 || !w || !rows || !ldw) return KVR_E_INVALID_ARGUMENT;
+    if (epilogue != KVR_LINEAR_CONCAT && epilogue != KVR_LINEAR_SILU_GATE) return KVR_E_INVALID_ARGUMENT;
+    const bool gated = epilogue == KVR_LINEAR_SILU_GATE;
+    if (gated && (n_weights != 2 || rows[0] != rows[1])) return KVR_E_UNSUPPORTED_SHAPE;
+    int64_t total = 0;
+    for (int i = 0; i < n_weights; ++i) {
+        if (rows[i] <= 0) return KVR_E_UNSUPPORTED_SHAPE;
+        total += rows[i];
+    }
+    if (total > (1 << 30)) return KVR_E_UNSUPPORTED_SHAPE;
+    const int32_t n_out = gated ? rows[0] : static_cast<int32_t>(total);
+    const int32_t splits = kvr_linear_splits(m, static_cast<int32_t>(total), k);
+    if (splits < 0) return splits;
+    if (ldx < k || ldy < n_out || ldx % 8) return KVR_E_BAD_STRIDE;
+    for (int i = 0; i < n_weights; ++i)
+        if (ldw[i] < k || ldw[i] % 8) return KVR_E_BAD_STRIDE;
+    if (!x || !y) return KVR_E_NULL_POINTER;
+    for (int i = 0; i < n_weights; ++i)
+        if (!w[i]) return KVR_E_NULL_POINTER;
+    if (!aligned16(x)) return KVR_E_BAD_STRIDE;
+    for (int i = 0; i < n_weights; ++i)
+        if (!aligned16(w[i])) return KVR_E_BAD_STRIDE;
+    const int64_t need = kvr_linear_workspace_bytes(m, static_cast<int32_t>(total), k);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return KVR_E_WORKSPACE_TOO_SMALL;
+    GemmArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = static_cast<const char*>(x);
+    a.w0 = static_cast<const char*>(w[0]);
+    a.w1 = static_cast<const char*>(n_weights > 1 ? w[1] : w[0]);
+    a.w2 = static_cast<const char*>(n_weights > 2 ? w[2] : a.w1);
+    a.ldw0 = ldw[0];
+    a.ldw1 = n_weights > 1 ? ldw[1] : ldw[0];
+    a.ldw2 = n_weights > 2 ? ldw[2] : a.ldw1;
+    a.end0 = rows[0];
+    a.end1 = n_weights > 1 ? rows[0] + rows[1] : rows[0];
+    a.rows = static_cast<int32_t>(total);
+    a.n_out = n_out;
+    a.gated = gated ? 1 : 0;
+    a.y = static_cast<char*>(y);
+    a.partial = static_cast<float*>(workspace);
+    a.ldx = ldx;
+    a.ldy = ldy;
+    a.m = m;
+    a.k = k;
+    const Split sp = plan_split(static_cast<int32_t>(total), k);
+    a.splits = sp.splits;
+    a.slice = sp.slice;
+    hipStream_t s = as_stream(stream);
+    return dtype == KVR_DTYPE_BF16 ? launch<bf16_t>(a, s) : launch<f16_t>(a, s);
+}
+
+extern "C" int kvr_linear(const void* x, const void* w, void* y, int32_t m, int32_t n, int32_t k, int64_t ldx,
+                          int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, int32_t dtype,
+                          void* stream) {
+    const void* ws[1] = {w};
+    const int32_t rows[1] = {n};
+    const int64_t lds[1] = {ldw};
+    return kvr_linear_multi(x, 1, ws, rows, lds, y, m, k, ldx, ldy, KVR_LINEAR_CONCAT, workspace, workspace_bytes,
+                            dtype, stream);
+}

@@ -58,6 +58,15 @@ __device__ inline float round_through(float x) {
     return elem<T>::to_float(elem<T>::from_float(x));
 }
 
+// SiLU-gated product of one element, as the eager chain computes it:
+// dtype(silu(g)) * u in fp32 (the caller rounds the product to dtype).
+template <typename T>
+__device__ inline float silu_gate(float g, float u) {
+#pragma clang fp contract(off)
+    const float act = round_through<T>(g / (1.f + expf(-g)));  // silu, rounded to dtype
+    return act * u;
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

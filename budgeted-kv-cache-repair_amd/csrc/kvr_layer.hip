@@ -163,13 +163,6 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, 
 
 constexpr int kEltThreads = 256;
 
-template <typename T>
-__device__ inline float silu_gate(float g, float u) {
-#pragma clang fp contract(off)
-    const float act = round_through<T>(g / (1.f + expf(-g)));  // silu, rounded to dtype
-    return act * u;
-}
-
 // One element per thread (any alignment) ...
 template <typename T>
 __global__ void __launch_bounds__(kEltThreads) silu_mul_kernel(const char* gate, const char* up, char* out, int64_t n) {

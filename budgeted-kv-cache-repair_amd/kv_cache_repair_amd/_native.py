@@ -58,6 +58,17 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.kvr_rms_norm.restype = ctypes.c_int
     lib.kvr_silu_mul.argtypes = [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, _vp]
     lib.kvr_silu_mul.restype = ctypes.c_int
+    lib.kvr_linear_splits.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    lib.kvr_linear_splits.restype = ctypes.c_int32
+    lib.kvr_linear_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    lib.kvr_linear_workspace_bytes.restype = ctypes.c_int64
+    lib.kvr_linear.argtypes = [_vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                               ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int32, _vp]
+    lib.kvr_linear.restype = ctypes.c_int
+    lib.kvr_linear_multi.argtypes = [_vp, ctypes.c_int32, _vpp, _i32p, _i64p, _vp, ctypes.c_int32, ctypes.c_int32,
+                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int64,
+                                     ctypes.c_int32, _vp]
+    lib.kvr_linear_multi.restype = ctypes.c_int
     lib.kvr_attention_schedule.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _i32p, ctypes.c_int64]
     lib.kvr_attention_schedule.restype = ctypes.c_int64

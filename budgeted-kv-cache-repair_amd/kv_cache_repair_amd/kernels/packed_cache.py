@@ -21,6 +21,7 @@ from __future__ import annotations
 import copy
 import ctypes
 import types
+import weakref
 from dataclasses import dataclass, field
 from threading import Lock
 from typing import Any, Sequence
@@ -30,6 +31,7 @@ import transformers
 from transformers.cache_utils import Cache, DynamicLayer
 
 from .. import _native
+from . import projection as _projection
 from .executor import _validate_cache, _validate_intervals, layer_kv
 from .indexed_attention import IndexedPlan, DeviceIndexedPlan, _require_gfx950
 
@@ -183,6 +185,63 @@ def _silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return out
 
 
+@dataclass
+class _LayerPlans:
+    """kvr_linear_multi plans of one decoder layer's projections: q/k/v in one
+    launch (separate launches when the layer normalises q/k per head), o, the
+    SiLU-gated gate/up pair in one launch, down."""
+
+    pointers: tuple
+    qkv: Any
+    q: Any
+    k: Any
+    v: Any
+    o: Any
+    gate_up: Any
+    down: Any
+    q_cols: int
+    k_cols: int
+
+
+_PLAN_CACHE: "weakref.WeakKeyDictionary[Any, _LayerPlans]" = weakref.WeakKeyDictionary()
+_PLAN_LOCK = Lock()
+
+
+def _plain_linear(module) -> bool:
+    return (type(module) is torch.nn.Linear and module.bias is None
+            and _projection.supported_weight(module.weight))
+
+
+def _layer_plans(layer) -> _LayerPlans | None:
+    """Plans for ``layer`` (one of the caller's decoder layers), cached per layer
+    and rebuilt when a weight's storage moves; None when any projection has a
+    bias, is not a plain fp16/bf16 nn.Linear, or the MLP activation is not SiLU."""
+    attention, mlp = layer.self_attn, layer.mlp
+    modules = (attention.q_proj, attention.k_proj, attention.v_proj, attention.o_proj, mlp.gate_proj,
+               mlp.up_proj, mlp.down_proj)
+    if not all(_plain_linear(m) for m in modules) or not isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
+        return None
+    weights = [m.weight for m in modules]
+    if len({(w.dtype, w.device) for w in weights}) != 1 or weights[4].shape != weights[5].shape:
+        return None
+    pointers = tuple(int(w.data_ptr()) for w in weights)
+    with _PLAN_LOCK:
+        cached = _PLAN_CACHE.get(layer)
+        if cached is not None and cached.pointers == pointers:
+            return cached
+    q, k, v, o, gate, up, down = weights
+    plan = _projection.ProjectionPlan
+    separate = getattr(attention, "q_norm", None) is not None
+    plans = _LayerPlans(
+        pointers=pointers, qkv=None if separate else plan([q, k, v]), q=plan([q]) if separate else None,
+        k=plan([k]) if separate else None, v=plan([v]) if separate else None, o=plan([o]),
+        gate_up=plan([gate, up], _projection.SILU_GATE), down=plan([down]), q_cols=int(q.shape[0]),
+        k_cols=int(k.shape[0]))
+    with _PLAN_LOCK:
+        _PLAN_CACHE[layer] = plans
+    return plans
+
+
 def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
                          use_cache=False, position_embeddings=None, **kwargs):
     """Decoder layer of a packed shell with its elementwise work fused.
@@ -191,8 +250,9 @@ def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=
     modeling_llama.py:301-330, modeling_qwen3.py:287-316): input RMSNorm,
     attention, residual add, post-attention RMSNorm, SiLU-gated MLP, residual
     add. Each RMSNorm is one kvr_rms_norm launch (the first residual add fused
-    into the second norm) and the MLP activation product one kvr_silu_mul
-    launch; projections stay the module's own linear layers.
+    into the second norm); the MLP is kvr_linear_multi's SiLU-gated gate/up
+    launch plus the down projection when the shell carries projection plans,
+    else the module's linear layers around one kvr_silu_mul launch.
     """
     normed = _rms_norm(self.input_layernorm, hidden_states)
     attended, _ = self.self_attn(hidden_states=normed, attention_mask=attention_mask, position_ids=position_ids,
@@ -200,7 +260,10 @@ def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=
                                  position_embeddings=position_embeddings, **kwargs)
     normed, residual = _rms_norm(self.post_attention_layernorm, attended, residual=hidden_states)
     mlp = self.mlp
-    if isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
+    plans = getattr(self, "_kvr_plans", None)
+    if plans is not None:
+        out = plans.down(plans.gate_up(normed))
+    elif isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
         out = mlp.down_proj(_silu_mul(mlp.gate_proj(normed), mlp.up_proj(normed)))
     else:
         out = mlp(normed)
@@ -217,8 +280,9 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
 
     The same computation as the native Llama/Qwen3 attention forward
     (transformers 5.15.0 modeling_llama.py:243-293, modeling_qwen3.py:231-276)
-    routed through the packed plugin points: projections (and Qwen3's per-head
-    q/k RMSNorm) run as the module's own layers; RoPE of the fresh queries and
+    routed through the packed plugin points: projections run as kvr_linear_multi
+    launches when the shell carries projection plans (q/k/v in one), else as
+    the module's own layers, Qwen3's per-head q/k RMSNorm as kvr_rms_norm; RoPE of the fresh queries and
     keys at their absolute positions, the key/value scatter into the cache and
     the cache-update bookkeeping are ONE libkvrepair launch
     (kvr_rope_scatter_kv, bit-identical to apply_rotary_pos_emb + the packed
@@ -236,9 +300,21 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
         raise RuntimeError("packed fused epilogue requires the packed cache layers")
     input_shape = hidden_states.shape[:-1]
     hidden_shape = (*input_shape, -1, self.head_dim)
-    query = self.q_proj(hidden_states).view(hidden_shape)
-    key = self.k_proj(hidden_states).view(hidden_shape)
-    value = self.v_proj(hidden_states).view(hidden_shape)
+    plans = getattr(self, "_kvr_plans", None)
+    if plans is None:
+        query = self.q_proj(hidden_states).view(hidden_shape)
+        key = self.k_proj(hidden_states).view(hidden_shape)
+        value = self.v_proj(hidden_states).view(hidden_shape)
+    elif plans.qkv is not None:  # one launch, three column blocks of one output
+        qkv = plans.qkv(hidden_states)
+        split = plans.q_cols + plans.k_cols
+        query = qkv[..., :plans.q_cols].view(hidden_shape)
+        key = qkv[..., plans.q_cols:split].view(hidden_shape)
+        value = qkv[..., split:].view(hidden_shape)
+    else:
+        query = plans.q(hidden_states).view(hidden_shape)
+        key = plans.k(hidden_states).view(hidden_shape)
+        value = plans.v(hidden_states).view(hidden_shape)
     q_norm = getattr(self, "q_norm", None)
     if q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
         if getattr(self, "_kvr_fused_norms", False):
@@ -255,14 +331,17 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     launcher = context.launcher
     out = torch.empty(query.shape, dtype=query.dtype, device=query.device)  # [1, B, Hq, D]
     launcher.attention(rotated.transpose(1, 2), layer.keys, layer.values, out.transpose(1, 2), float(self.scaling))
-    return self.o_proj(out.reshape(*input_shape, -1)), None
+    attended = out.reshape(*input_shape, -1)
+    return (plans.o(attended) if plans is not None else self.o_proj(attended)), None
 
 
-def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True):
+def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True, plans=None):
     """Shallow module shells sharing parameters, with a private config naming the
     packed attention; the caller's modules and config are never modified. With
     ``fused_epilogue`` the attention shells run _fused_attention_forward; with
-    ``fused_layers`` the layer and final-norm shells run their fused forwards."""
+    ``fused_layers`` the layer and final-norm shells run their fused forwards.
+    ``plans`` (one _LayerPlans or None per layer) routes the shells'
+    projections through kvr_linear_multi."""
     _register_attention()
     config = copy.deepcopy(base.config)
     config._attn_implementation = _ATTENTION_NAME
@@ -278,11 +357,14 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
         attention = copy.copy(original.self_attn)
         attention._modules = original.self_attn._modules.copy()
         attention.config = config
+        layer_plans = plans[len(layers)] if plans is not None else None
         if fused_epilogue:
             attention.forward = types.MethodType(_fused_attention_forward, attention)
             attention._kvr_fused_norms = fused_layers
+            attention._kvr_plans = layer_plans
         if fused_layers:
             layer.forward = types.MethodType(_fused_layer_forward, layer)
+            layer._kvr_plans = layer_plans
         layer._modules["self_attn"] = attention
         layers.append(layer)
     view._modules["layers"] = torch.nn.ModuleList(layers)
@@ -305,7 +387,17 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     base = shim._base_transformer(model)
     if (type(model), type(base)) not in {(LlamaForCausalLM, LlamaModel), (Qwen3ForCausalLM, Qwen3Model)}:
         raise ValueError("packed executor requires exact native dense Llama or Qwen3 classes")
-    if model.training or base.training or any(module.training for module in base.modules()):
+    device = edited_ids.device
+    # One walk over the module tree gathers every per-module condition below.
+    base_ids = {id(module) for module in base.modules()}
+    training = hooked = overridden = off_device = False
+    for module in model.modules():
+        in_base = id(module) in base_ids
+        training |= in_base and module.training
+        hooked |= getattr(module, "_hf_hook", None) is not None
+        overridden |= in_base and "forward" in module.__dict__
+        off_device |= any(p is not None and p.device != device for p in module._parameters.values())
+    if model.training or base.training or training:
         raise ValueError("packed executor requires eval mode on all decoder modules")
     config = model.config
     if config.num_hidden_layers != len(base_cache.layers) or len(base.layers) != len(base_cache.layers):
@@ -317,17 +409,16 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
         raise ValueError("packed executor requires full attention")
     if any(kind != "full_attention" for kind in getattr(config, "layer_types", []) or []):
         raise ValueError("packed executor rejects sliding/hybrid attention")
-    device = edited_ids.device
     if device.type != "cuda" or torch.version.hip is None:
         raise ValueError("packed HIP executor requires one ROCm GPU device")
-    if any(parameter.device != device for parameter in model.parameters()):
+    if off_device:
         raise ValueError("packed executor requires all model parameters on the request device")
     if any(layer_kv(base_cache, i)[0].device != device or layer_kv(base_cache, i)[1].device != device
            for i in range(len(base_cache.layers))):
         raise ValueError("packed executor requires all cache layers on the request device")
-    if any(getattr(module, "_hf_hook", None) is not None for module in model.modules()):
+    if hooked:
         raise ValueError("packed executor does not support dispatch/offload hooks")
-    if any("forward" in module.__dict__ for module in base.modules()):
+    if overridden:
         raise ValueError("packed executor does not support per-instance decoder forward overrides")
     key = layer_kv(base_cache, 0)[0]
     if key.dtype not in _native.DTYPE_CODES:
@@ -448,9 +539,20 @@ def _fused_layers_for(fused_layers, dtype: torch.dtype) -> bool:
     return bool(fused_layers)
 
 
+def _projection_plans_for(base, fused_projections, dtype: torch.dtype, selected: int):
+    """Per-layer projection plans, or None for the modules' own linear layers.
+    Default (None): on for fp16/bf16 caches when the selected rows fit one
+    kvr_linear_multi launch (at most 64); fp32 has no such kernel."""
+    if fused_projections is None:
+        fused_projections = dtype in (torch.float16, torch.bfloat16) and selected <= _projection.MAX_ROWS
+    if not fused_projections or dtype not in (torch.float16, torch.bfloat16) or selected > _projection.MAX_ROWS:
+        return None
+    return [_layer_plans(layer) for layer in base.layers]
+
+
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
                   attention_backend: str, writeback_backend: str, fused_epilogue: bool = True,
-                  fused_layers: bool | None = None) -> None:
+                  fused_layers: bool | None = None, fused_projections: bool | None = None) -> None:
     """Run the packed forward, scattering into the caller-owned ``output`` cache."""
     base = shim._base_transformer(shim.generator)
     device_plan = host_plan.to(edited_ids_t.device)
@@ -458,7 +560,8 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
     key0 = layer_kv(output, 0)[0]
     context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan,
                              _launcher(device_plan, base.config, key0))
-    native_view = _make_native_view(base, fused_epilogue, _fused_layers_for(fused_layers, key0.dtype))
+    plans = _projection_plans_for(base, fused_projections, key0.dtype, device_plan.selected_count)
+    native_view = _make_native_view(base, fused_epilogue, _fused_layers_for(fused_layers, key0.dtype), plans)
     layers = [_PackedLayer(*layer_kv(output, i), context, writeback_backend) for i in range(layer_count)]
     cache = Cache(layers=layers)
     result = native_view(input_ids=edited_ids_t.index_select(1, positions), position_ids=positions.unsqueeze(0),
@@ -471,7 +574,8 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
 def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
                            intervals: Sequence[tuple[int, int]], *, attention_backend: str = "hip",
                            writeback_backend: str = "hip", plan: Any = None, fused_epilogue: bool = True,
-                           fused_layers: bool | None = None) -> tuple[Any, dict[str, Any]]:
+                           fused_layers: bool | None = None,
+                           fused_projections: bool | None = None) -> tuple[Any, dict[str, Any]]:
     """Recompute sorted selected rows in one native layer-major forward.
 
     Same signature, validation order, receipt and ownership contract as the
@@ -486,7 +590,11 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     ``fused_layers`` runs each decoder layer's RMSNorms (with the residual
     add) and MLP activation as single launches; its fp32 mean of squares can
     differ from the eager chain by an ulp, so the default (None) fuses them for
-    fp16/bf16 caches only.
+    fp16/bf16 caches only. ``fused_projections`` runs each layer's projections
+    as kvr_linear_multi launches (q/k/v in one, gate/up with the SiLU gate in
+    one; fp32 accumulation rounded once, like the library GEMM up to summation
+    order); the default (None) uses them for fp16/bf16 caches with at most 64
+    selected rows, where the modules' GEMMs are weight-streaming bound.
     """
     _check_backends(attention_backend, writeback_backend)
     _check_ids(edited_ids_t)
@@ -506,14 +614,15 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
 
     output = clone_cache(base_cache)
     _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend,
-                  bool(fused_epilogue), fused_layers)
+                  bool(fused_epilogue), fused_layers, fused_projections)
     return output, receipt
 
 
 @torch.no_grad()
 def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tensor,
                           intervals: Sequence[tuple[int, int]], *, plan: Any = None,
-                          fused_epilogue: bool = True, fused_layers: bool | None = None) -> dict[str, Any]:
+                          fused_epilogue: bool = True, fused_layers: bool | None = None,
+                          fused_projections: bool | None = None) -> dict[str, Any]:
     """Packed refresh that scatters IN PLACE into a cache the caller owns.
 
     For a cache the caller has just built and nobody else references (the
@@ -536,5 +645,5 @@ def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tenso
     _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
     _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue),
-                  fused_layers)
+                  fused_layers, fused_projections)
     return receipt

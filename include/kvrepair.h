@@ -40,6 +40,12 @@ enum kvr_dtype {
     KVR_DTYPE_BF16 = 2,
 };
 
+/* Epilogue of kvr_linear_multi. */
+enum kvr_linear_epilogue {
+    KVR_LINEAR_CONCAT = 0,     /* y[:, off_i + r] = x . w_i[r]; off_i = rows of the weights before i */
+    KVR_LINEAR_SILU_GATE = 1,  /* y[:, r] = silu(x . w_0[r]) * (x . w_1[r]), eager rounding */
+};
+
 enum kvr_status {
     KVR_OK = 0,
     KVR_E_INVALID_ARGUMENT = -1,
@@ -168,6 +174,42 @@ int kvr_rms_norm(const void* x, const void* residual, void* residual_out, void* 
  * rows (two eager launches; no reference counterpart of its own).
  */
 int kvr_silu_mul(const void* gate, const void* up, void* out, int64_t n, int32_t dtype, void* stream);
+
+/*
+ * Projection GEMMs of the packed refresh rows (no bias), bf16 / fp16:
+ *   y[m, r] = sum_k x[m, k] * w[r, k]     m < M <= 64, fp32 accumulation
+ * i.e. torch.nn.functional.linear(x, w) for the few selected rows, replacing
+ * the library GEMMs of the native decoder's q/k/v/o and MLP projections
+ * (transformers 5.15.0 models/llama/modeling_llama.py:165-175, 243-252; no
+ * reference counterpart of its own). Every weight byte is streamed from HBM
+ * once. x: row-major [M][ldx]; weights: row-major [rows][ldw] (ldx, ldw
+ * multiples of 8 elements, 16-byte aligned bases); y: row-major [M][ldy]; k a
+ * multiple of 8. The work is split over K when that fills the GPU better:
+ * `workspace` then holds the fp32 partials (kvr_linear_workspace_bytes(m,
+ * rows, k) bytes, no initialisation needed) and a second launch on the same
+ * stream sums them in slice order. Calls sharing `workspace` must not overlap
+ * (one per stream). Results are deterministic (fixed summation order).
+ *
+ * `rows` of kvr_linear_splits / kvr_linear_workspace_bytes is the number of
+ * weight rows one call streams (the sum over its weights).
+ */
+int32_t kvr_linear_splits(int32_t m, int32_t rows, int32_t k);
+int64_t kvr_linear_workspace_bytes(int32_t m, int32_t rows, int32_t k);
+
+/* One weight: y = x w^T (w: [n][ldw]). */
+int kvr_linear(const void* x, const void* w, void* y, int32_t m, int32_t n, int32_t k, int64_t ldx, int64_t ldw,
+               int64_t ldy, void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream);
+
+/* Up to three weights in one launch. KVR_LINEAR_CONCAT: outputs side by side
+ * (the q/k/v projections of one layer into [M][nq + nk + nv]);
+ * KVR_LINEAR_SILU_GATE: two weights of equal rows (gate_proj, up_proj), y =
+ * dtype(dtype(silu(dtype(x gate^T))) * dtype(x up^T)) -- the MLP's
+ * act_fn(gate_proj(x)) * up_proj(x) (modeling_llama.py:174) with the
+ * rounding of the eager ops, bit-identical to two kvr_linear calls of the
+ * same split count followed by kvr_silu_mul. */
+int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
+                     const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy, int32_t epilogue,
+                     void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream);
 
 /*
  * Host-side work schedule for kvr_packed_causal_attention (no device access).

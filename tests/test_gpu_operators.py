@@ -270,6 +270,124 @@ def test_silu_mul_matches_native_mlp_activation(gpu_device, dtype):
     assert dist.max().item() <= 1 and (dist == 0).float().mean().item() >= 0.99
 
 
+# --------------------------------------------------------------------------- projection GEMMs
+def exact_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x w^T in fp64 (exact for these sizes up to fp64 rounding), rounded once to the dtype."""
+    return (x.double() @ w.double().T).to(x.dtype)
+
+
+def assert_linear_close(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> None:
+    """y = x w^T accumulated in fp32 and rounded once: >= 99% of the elements
+    equal the exactly rounded product, and every element is within the rounding
+    (eps |p|) plus an fp32 accumulation bound (2^-20 sum |x w|) of the fp64 one."""
+    ref = x.double() @ w.double().T
+    bound = torch.finfo(y.dtype).eps * ref.abs() + 2.0 ** -20 * (x.double().abs() @ w.double().abs().T)
+    assert ((y.double() - ref).abs() <= bound + torch.finfo(y.dtype).tiny).all()
+    assert (y == ref.to(y.dtype)).float().mean().item() >= 0.99
+
+
+# (n, k): split counts 4 / 2 / 4 / 1 / 1 / 3; k = 136 and 1000 end inside a
+# 32-wide step and a 256-chunk, n = 100 inside a 64-row tile, k = 2000 splits
+# into 768 + 768 + 464
+LINEAR_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (100, 136), (1024, 1000), (512, 2000)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", LINEAR_SHAPES)
+@pytest.mark.parametrize("rows", [1, 17, 64])
+def test_linear_matches_exact_product(gpu_device, dtype, shape, rows):
+    """kvr_linear = round(x w^T) with fp32 accumulation (assert_linear_close)."""
+    from kv_cache_repair_amd.kernels import projection
+
+    n, k = shape
+    torch.manual_seed(n + k + rows)
+    x = torch.randn(1, rows, k, device=gpu_device).to(dtype)
+    w = (torch.randn(n, k, device=gpu_device) * 0.03).to(dtype)
+    y = projection.linear(x, w)
+    assert y.shape == (1, rows, n) and y.dtype == dtype
+    assert_linear_close(y, x, w)
+
+
+def test_linear_is_deterministic_and_uses_the_callers_stream(gpu_device):
+    from kv_cache_repair_amd.kernels import projection
+
+    torch.manual_seed(3)
+    x = torch.randn(1, 64, 14336, device=gpu_device).to(torch.bfloat16)
+    w = (torch.randn(4096, 14336, device=gpu_device) * 0.01).to(torch.bfloat16)
+    plan = projection.ProjectionPlan([w])
+    first = plan(x)
+    for _ in range(3):
+        assert bits_equal(plan(x), first)
+    side = torch.cuda.Stream(gpu_device)
+    side.wait_stream(torch.cuda.current_stream(gpu_device))
+    with torch.cuda.stream(side):
+        other = plan(x)
+    torch.cuda.current_stream(gpu_device).wait_stream(side)
+    assert bits_equal(other, first)
+    side_stream = side.cuda_stream
+    assert (gpu_device.index, side_stream) in projection._scratch  # a workspace of its own
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_linear_concat_writes_each_weight_side_by_side(gpu_device, dtype):
+    """q/k/v in one launch: each column block is its own exactly rounded product,
+    also when a weight's rows end inside a 16-row MFMA tile and for strided
+    inputs/weights."""
+    from kv_cache_repair_amd.kernels import projection
+
+    torch.manual_seed(11)
+    k = 512
+    x = torch.randn(1, 33, k + 64, device=gpu_device).to(dtype)[..., 32:32 + k]  # strided rows
+    backing = (torch.randn(200, k + 8, device=gpu_device) * 0.05).to(dtype)
+    wq, wk, wv = backing[:72, :k], backing[72:72 + 40, 8:8 + k], (torch.randn(24, k, device=gpu_device) * 0.05).to(dtype)
+    y = projection.linear_concat(x, [wq, wk, wv])
+    assert y.shape == (1, 33, 136)
+    for part, w in zip(torch.split(y, [72, 40, 24], dim=-1), (wq, wk, wv)):
+        assert_linear_close(part, x, w)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(16384, 4096), (2048, 1024), (96, 136)])
+def test_silu_gate_linear_is_bitwise_linear_then_silu_mul(gpu_device, dtype, shape):
+    """The gated epilogue equals kvr_linear(gate), kvr_linear(up), kvr_silu_mul bit
+    for bit (same split count), i.e. the eager act_fn(gate_proj(x)) * up_proj(x)
+    rounding chain over the kernel's projections."""
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.kernels import projection
+    from kv_cache_repair_amd.kernels.packed_cache import _silu_mul
+
+    n, k = shape
+    lib = _native.lib()
+    assert lib.kvr_linear_splits(64, n, k) == lib.kvr_linear_splits(64, 2 * n, k)
+    torch.manual_seed(n)
+    x = torch.randn(1, 64, k, device=gpu_device).to(dtype)
+    gate = (torch.randn(n, k, device=gpu_device) * 0.05).to(dtype)
+    up = (torch.randn(n, k, device=gpu_device) * 0.05).to(dtype)
+    fused = projection.silu_gate_linear(x, gate, up)
+    chained = _silu_mul(projection.linear(x, gate), projection.linear(x, up))
+    assert bits_equal(fused, chained)
+    eager = torch.nn.functional.silu(exact_linear(x, gate)) * exact_linear(x, up)
+    dist = ulp_distance(fused, eager)
+    assert (dist <= 2).float().mean().item() >= 0.99
+
+
+def test_projection_plans_reject_what_they_cannot_serve(gpu_device):
+    from kv_cache_repair_amd.kernels import projection
+
+    w = torch.randn(128, 256, device=gpu_device, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        projection.ProjectionPlan([w.float()])
+    with pytest.raises(ValueError):
+        projection.ProjectionPlan([w[:, :255]])  # k not a multiple of 8
+    with pytest.raises(ValueError):
+        projection.ProjectionPlan([w, w[:64]], projection.SILU_GATE)
+    plan = projection.ProjectionPlan([w])
+    with pytest.raises(RuntimeError, match="rows"):
+        plan(torch.randn(65, 256, device=gpu_device, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="drifted"):
+        plan(torch.randn(4, 256, device=gpu_device, dtype=torch.float16))
+
+
 # --------------------------------------------------------------------------- attention
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dim", [64, 128])

@@ -340,8 +340,9 @@ def test_fused_fresh_row_epilogue_is_bit_identical_to_native_rope_and_scatter(gp
     edited = ids.clone()
     edited[0, 70:] = (edited[0, 70:] + 7) % 97
     intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
-    fused, _ = packed_interval_repair(shim, base, edited, intervals, fused_layers=False)
-    plain, _ = packed_interval_repair(shim, base, edited, intervals, fused_epilogue=False, fused_layers=False)
+    fused, _ = packed_interval_repair(shim, base, edited, intervals, fused_layers=False, fused_projections=False)
+    plain, _ = packed_interval_repair(shim, base, edited, intervals, fused_epilogue=False, fused_layers=False,
+                                      fused_projections=False)
     for a, b in zip(fused.layers, plain.layers):
         assert bits_equal(a.keys, b.keys) and bits_equal(a.values, b.values)
     with torch.no_grad():
@@ -368,8 +369,8 @@ def test_fused_layers_match_native_layer_ops(gpu_device, family, dtype):
     edited = ids.clone()
     edited[0, 70:] = (edited[0, 70:] + 7) % 97
     intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
-    fused, _ = packed_interval_repair(shim, base, edited, intervals, fused_layers=True)
-    plain, _ = packed_interval_repair(shim, base, edited, intervals, fused_layers=False)
+    fused, _ = packed_interval_repair(shim, base, edited, intervals, fused_layers=True, fused_projections=False)
+    plain, _ = packed_interval_repair(shim, base, edited, intervals, fused_layers=False, fused_projections=False)
     for a, b in zip(fused.layers, plain.layers):
         for x, y in ((a.keys, b.keys), (a.values, b.values)):
             if dtype == torch.float32:
@@ -380,3 +381,45 @@ def test_fused_layers_match_native_layer_ops(gpu_device, family, dtype):
                 assert ((xf - yf).abs() <= 2 * ulp).float().mean().item() >= 0.99
                 cos = torch.nn.functional.cosine_similarity(xf.reshape(-1, 64), yf.reshape(-1, 64), dim=-1)
                 assert cos.min().item() >= 0.9999
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_projection_plans_match_module_linears(gpu_device, family, dtype):
+    """kvr_linear_multi projections (q/k/v in one launch for Llama, separate for
+    Qwen3's per-head norms; gate/up with the SiLU gate in one) vs the modules'
+    library GEMMs: both round fp32 accumulations once, so the refreshed caches
+    agree to the bf16/fp16 floor: >= 99% of elements within two ulps, per-row
+    cosine >= 0.9999. The plans are cached per layer and follow weight moves."""
+    from kv_cache_repair_amd.kernels import packed_cache as pc
+
+    model = make_model(gpu_device, family, kv_heads=2, head_dim=64, dtype=dtype, layers=3)
+    shim, ids, base = make_request(model, length=140)
+    edited = ids.clone()
+    edited[0, 70:] = (edited[0, 70:] + 7) % 97
+    intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
+    fused, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=True)
+    plain, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=False)
+    eps = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    for a, b in zip(fused.layers, plain.layers):
+        for x, y in ((a.keys, b.keys), (a.values, b.values)):
+            xf, yf = x.float(), y.float()
+            ulp = torch.clamp(yf.abs(), min=2.0 ** -20) * eps
+            assert ((xf - yf).abs() <= 2 * ulp).float().mean().item() >= 0.99
+            cos = torch.nn.functional.cosine_similarity(xf.reshape(-1, 64), yf.reshape(-1, 64), dim=-1)
+            assert cos.min().item() >= 0.9999
+    decoder = shim._base_transformer(model)
+    plans = [pc._layer_plans(layer) for layer in decoder.layers]
+    assert all(p is not None for p in plans)
+    assert all((p.qkv is None) == (family == "qwen3") for p in plans)
+    assert pc._layer_plans(decoder.layers[0]) is plans[0]  # cached
+    again, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=True)
+    assert all(torch.equal(x.keys, y.keys) and torch.equal(x.values, y.values)
+               for x, y in zip(again.layers, fused.layers))  # deterministic
+    with torch.no_grad():  # a weight moved to new storage invalidates that layer's plans
+        layer0 = decoder.layers[0]
+        layer0.mlp.down_proj.weight.data = layer0.mlp.down_proj.weight.data.clone()
+    assert pc._layer_plans(layer0) is not plans[0]
+    moved, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=True)
+    assert all(torch.equal(x.keys, y.keys) for x, y in zip(moved.layers, fused.layers))
+

@@ -24,7 +24,8 @@ def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted([
         "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
         "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
-        "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul"])
+        "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
+        "kvr_linear_workspace_bytes", "kvr_linear_multi"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -75,6 +76,27 @@ def test_entry_points_validate_before_any_launch():
     assert lib.kvr_silu_mul(None, None, None, 8, 5, None) == -2
     assert lib.kvr_silu_mul(None, None, None, -1, 2, None) == -1
     assert lib.kvr_silu_mul(None, None, None, 8, 2, None) == -5
+    assert lib.kvr_linear_splits(65, 4096, 4096) == -3 and lib.kvr_linear_splits(64, 4096, 4095) == -3
+    # K splits: the smallest power of two reaching 256 blocks of 64 weight rows,
+    # at most k / 512, in whole 256-chunks
+    assert lib.kvr_linear_splits(64, 14336, 4096) == 2 and lib.kvr_linear_splits(64, 4096, 14336) == 4
+    assert lib.kvr_linear_splits(64, 28672, 4096) == 1 and lib.kvr_linear_splits(64, 512, 2000) == 3
+    assert lib.kvr_linear_splits(64, 100, 136) == 1 and lib.kvr_linear_splits(1, 1024, 4096) == 8
+    assert lib.kvr_linear_workspace_bytes(64, 14336, 4096) == 224 * 2 * 64 * 64 * 4
+    assert lib.kvr_linear_workspace_bytes(64, 28672, 4096) == 0
+    assert lib.kvr_linear(None, None, None, 64, 4096, 4096, 4096, 4096, 4096, None, 0, 0, None) == -2
+    assert lib.kvr_linear(None, None, None, 64, 4096, 4096, 4095, 4096, 4096, None, 0, 2, None) == -4
+    assert lib.kvr_linear(None, None, None, 64, 4096, 4096, 4096, 4096, 4096, None, 0, 2, None) == -5
+    w3 = (ctypes.c_void_p * 3)(16, 32, 48)
+    rows = (ctypes.c_int32 * 3)(4096, 1024, 1024)
+    ldw = _native.i64_array([4096] * 3)
+    args = (64, 4096, 4096, 6144)
+    assert lib.kvr_linear_multi(16, 4, w3, rows, ldw, 16, *args, 0, None, 0, 2, None) == -1  # > 3 weights
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 2, None, 0, 2, None) == -1  # epilogue
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 1, None, 0, 2, None) == -3  # gate: 2 only
+    assert lib.kvr_linear_multi(16, 2, w3, rows, ldw, 16, *args, 1, None, 0, 2, None) == -3  # unequal rows
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, 64, 4096, 4096, 6143, 0, None, 0, 2, None) == -4
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 0, None, 0, 2, None) == -6  # workspace
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
