@@ -11,13 +11,16 @@ random suffix slots (seed 2).
 One step = one full refresh stage, inputs resident in HBM: shift-cache build
 (prefix copy + RoPE delta rotation of every suffix K row + V copy, all layers)
 -> plan upload -> packed forward through all 32 layers with, per layer, the
-fused fresh-row epilogue (RoPE of the fresh Q/K + K/V scatter, one launch) and
-the packed attention. Prefill, tokenisation and selection are outside
+libkvrepair projection GEMMs (q/k/v in one launch, o, gate/up with the SiLU
+gate, down), the RMSNorms (residual add fused), the fused fresh-row epilogue
+(RoPE of the fresh Q/K + K/V scatter, one launch) and the packed attention.
+Prefill, tokenisation and selection are outside
 the step, as in the reference benchmark (benchmark_refresh.py:3-9); unlike it,
 the rotation is inside.
 
-Printed (one JSON line): stage latency (ms per repair), the per-kernel HIP
-event timings of the timed steps, a roofline object for the dominant kernel,
+Printed (one JSON line): stage latency (ms per repair, K uninstrumented
+steps), the per-kernel HIP event timings of K more identical steps (events
+around every libkvrepair launch), a roofline object for the dominant kernel,
 the rotate-only GB/s, the same stage run the reference way on the same GPU,
 and the reference path timed on the host CPU (cpu_baseline).
 """
@@ -122,7 +125,7 @@ class KernelTimer:
     """Brackets every libkvrepair launch with HIP events on the launching stream."""
 
     NAMES = ("kvr_shift_cache_build", "kvr_rope_scatter_kv", "kvr_indexed_scatter_kv",
-             "kvr_packed_causal_attention", "kvr_rope_delta_rotate")
+             "kvr_packed_causal_attention", "kvr_rope_delta_rotate", "kvr_linear_multi", "kvr_rms_norm")
 
     def __init__(self):
         from kv_cache_repair_amd import _native
@@ -392,14 +395,18 @@ def main(argv=None) -> int:
     del ours
     torch.cuda.synchronize()
 
-    timer = KernelTimer()
-    timer.install()
     step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals)  # noqa: E731
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    timer.active = True
+    # `value`: K uninstrumented steps (the stage is partly host-bound, so per-launch
+    # events would inflate it); then the same K steps again with HIP events around
+    # every libkvrepair launch for the per-kernel timings and the roofline.
     ms = time_steps(step, args.steps, 0)
+    timer = KernelTimer()
+    timer.install()
+    timer.active = True
+    instrumented_ms = time_steps(step, args.steps, 0)
     timer.active = False
     torch.cuda.synchronize()
     kernels = timer.summary(args.steps)
@@ -440,9 +447,19 @@ def main(argv=None) -> int:
     scatter_bytes = 2 * 2 * HKV * len(positions) * DIM * esz
     # fresh-row epilogue: read q, k, v and cos/sin, write rotated q, cache K and V rows
     rope_scatter_bytes = (2 * (HQ + 2 * HKV) + 2) * len(positions) * DIM * esz
+    # projections (q/k/v, o, gate/up, down per layer): every weight byte once, plus x in and y out;
+    # averaged over the step's launches of kvr_linear_multi (four shapes)
+    rows = len(positions)
+    qkv_cols = (HQ + 2 * HKV) * DIM
+    gemm_layer_bytes = esz * (HIDDEN * qkv_cols + HQ * DIM * HIDDEN + 2 * MLP * HIDDEN + MLP * HIDDEN
+                              + rows * (HIDDEN + qkv_cols) + rows * (HQ * DIM + HIDDEN)
+                              + rows * (HIDDEN + MLP) + rows * (MLP + HIDDEN))
+    gemm_launches = kernels.get("kvr_linear_multi", {}).get("launches_per_step", 0.0)
+    gemm_bytes = LAYERS * gemm_layer_bytes / gemm_launches if gemm_launches else 0
     per_kernel = {
         "kvr_shift_cache_build": build_bytes, "kvr_packed_causal_attention": attn_bytes,
-        "kvr_rope_scatter_kv": rope_scatter_bytes, "kvr_indexed_scatter_kv": scatter_bytes}
+        "kvr_rope_scatter_kv": rope_scatter_bytes, "kvr_indexed_scatter_kv": scatter_bytes,
+        "kvr_linear_multi": gemm_bytes}
     for name, b in per_kernel.items():
         if name in kernels:
             kernels[name]["algorithmic_bytes"] = b
@@ -468,7 +485,8 @@ def main(argv=None) -> int:
         "rotate_GBps": rotate_bytes / (rotate["avg_us"] * 1e3),
         "rotate": {"avg_us": rotate["avg_us"], "algorithmic_bytes": rotate_bytes,
                    "frac_of_peak": rotate_bytes / (rotate["avg_us"] * 1e3) / HBM_PEAK_GBPS},
-        "kernels": kernels, "roofline": roofline, "reference_same_gpu": reference, "checks": checks,
+        "kernels": kernels, "instrumented_ms_per_step": instrumented_ms, "roofline": roofline,
+        "reference_same_gpu": reference, "checks": checks,
         "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
     }
     print(json.dumps(line), flush=True)

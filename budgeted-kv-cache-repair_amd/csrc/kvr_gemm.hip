@@ -60,7 +60,10 @@ constexpr int kGranules = kChunk / 8;       // 16-B x granules per row per chunk
 constexpr int kXLoads = kRowsMax * kGranules / kGemmThreads;  // x granules per thread per chunk
 static_assert(kXLoads * kGemmThreads == kRowsMax * kGranules && kGemmThreads % kGranules == 0, "x staging map");
 constexpr int kMinSlice = 512;              // K per split at least (bounds the partial traffic)
-constexpr int kTargetBlocks = 256;          // split until the grid covers every CU once
+#ifndef KVR_GEMM_TARGET_BLOCKS
+#define KVR_GEMM_TARGET_BLOCKS 256
+#endif
+constexpr int kTargetBlocks = KVR_GEMM_TARGET_BLOCKS;  // split until the grid covers every CU once
 constexpr int kRedStride = kTileN + 4;      // fp32 LDS tile of the gated epilogue
 constexpr int kTile = kRowsMax * kTileN;    // fp32 elements of one partial tile
 
@@ -86,8 +89,9 @@ struct GemmArgs {
     const char* w1;
     const char* w2;
     char* y;                        // [M][ldy]
+    const char* res;                // residual [M][ldr] added to y (or null)
     float* partial;                 // [n_tiles][S][64][kTileN] fp32 (S > 1)
-    int64_t ldx, ldy, ldw0, ldw1, ldw2;
+    int64_t ldx, ldy, ldr, ldw0, ldw1, ldw2;
     int32_t end0, end1;             // concatenated row boundaries of w0 | w1 | w2
     int32_t rows;                   // streamed rows in total
     int32_t n_out;                  // output columns (gated: rows / 2)
@@ -96,6 +100,15 @@ struct GemmArgs {
     int32_t slice;                  // K per split (multiple of kStep)
     int32_t splits;                 // S
 };
+
+// Output value of a concatenated projection: the fp32 sum, or with a residual
+// dtype(dtype(sum) + residual) -- `residual + proj(x)` as the eager ops round it.
+template <typename T>
+__device__ inline float with_residual(const GemmArgs& a, float sum, int m, int col) {
+    if (!a.res) return sum;
+    const uint16_t r = reinterpret_cast<const uint16_t*>(a.res)[static_cast<int64_t>(m) * a.ldr + col];
+    return round_through<T>(sum) + elem<T>::to_float(r);
+}
 
 // MFMA roles: A = W (16 streamed rows x 32 k; lane holds w[row lq][k + 8lj ..]),
 // B = x^T (32 k x 16 rows of x; lane holds x[m0 + lq][k + 8lj ..]) from LDS;
@@ -254,7 +267,8 @@ skinny_gemm_kernel(GemmArgs a) {
                 if (m >= a.m) continue;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (c0 + i < a.rows) y[static_cast<int64_t>(m) * a.ldy + c0 + i] = E::from_float(acc[t][i]);
+                    if (c0 + i < a.rows)
+                        y[static_cast<int64_t>(m) * a.ldy + c0 + i] = E::from_float(with_residual<T>(a, acc[t][i], m, c0 + i));
             }
             return;
         }
@@ -321,7 +335,8 @@ __global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(GemmArgs 
             const int col = tile * kTileN + c;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (col + i < a.rows) y[static_cast<int64_t>(m) * a.ldy + col + i] = E::from_float(sum[i]);
+                if (col + i < a.rows)
+                    y[static_cast<int64_t>(m) * a.ldy + col + i] = E::from_float(with_residual<T>(a, sum[i], m, col + i));
         }
     } else {
         for (int e = threadIdx.x; e < 16 * kHalf / 4; e += kReduceThreads) {
@@ -412,11 +427,12 @@ extern "C" int64_t kvr_linear_workspace_bytes(int32_t m, int32_t rows, int32_t k
 
 extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
                                 const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy,
-                                int32_t epilogue, void* workspace, int64_t workspace_bytes, int32_t dtype,
-                                void* stream) {
+                                int32_t epilogue, const void* residual, int64_t ldr, void* workspace,
+                                int64_t workspace_bytes, int32_t dtype, void* stream) {
     if (dtype != KVR_DTYPE_BF16 && dtype != KVR_DTYPE_F16) return KVR_E_UNSUPPORTED_DTYPE;
     if (n_weights < 1 || n_weights > 3 || !w || !rows || !ldw) return KVR_E_INVALID_ARGUMENT;
-    if (epilogue != KVR_LINEAR_CONCAT && epilogue != KVR_LINEAR_SILU_GATE) return KVR_E_INVALID_ARGUMENT;
+    if (epilogue != KVR_LINEAR_CONCAT && epilogue != KVR_LINEAR_SILU_GATE && epilogue != KVR_LINEAR_RESIDUAL)
+        return KVR_E_INVALID_ARGUMENT;
     const bool gated = epilogue == KVR_LINEAR_SILU_GATE;
     if (gated && (n_weights != 2 || rows[0] != rows[1])) return KVR_E_UNSUPPORTED_SHAPE;
     int64_t total = 0;
@@ -429,6 +445,7 @@ extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* co
     const int32_t splits = kvr_linear_splits(m, static_cast<int32_t>(total), k);
     if (splits < 0) return splits;
     if (ldx < k || ldy < n_out || ldx % 8) return KVR_E_BAD_STRIDE;
+    if (epilogue == KVR_LINEAR_RESIDUAL && (!residual || ldr < n_out)) return residual ? KVR_E_BAD_STRIDE : KVR_E_NULL_POINTER;
     for (int i = 0; i < n_weights; ++i)
         if (ldw[i] < k || ldw[i] % 8) return KVR_E_BAD_STRIDE;
     if (!x || !y) return KVR_E_NULL_POINTER;
@@ -454,6 +471,8 @@ extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* co
     a.n_out = n_out;
     a.gated = gated ? 1 : 0;
     a.y = static_cast<char*>(y);
+    a.res = epilogue == KVR_LINEAR_RESIDUAL ? static_cast<const char*>(residual) : nullptr;
+    a.ldr = ldr;
     a.partial = static_cast<float*>(workspace);
     a.ldx = ldx;
     a.ldy = ldy;
@@ -472,6 +491,6 @@ extern "C" int kvr_linear(const void* x, const void* w, void* y, int32_t m, int3
     const void* ws[1] = {w};
     const int32_t rows[1] = {n};
     const int64_t lds[1] = {ldw};
-    return kvr_linear_multi(x, 1, ws, rows, lds, y, m, k, ldx, ldy, KVR_LINEAR_CONCAT, workspace, workspace_bytes,
-                            dtype, stream);
+    return kvr_linear_multi(x, 1, ws, rows, lds, y, m, k, ldx, ldy, KVR_LINEAR_CONCAT, nullptr, 0, workspace,
+                            workspace_bytes, dtype, stream);
 }

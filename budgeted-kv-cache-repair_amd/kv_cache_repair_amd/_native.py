@@ -66,8 +66,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                                ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int32, _vp]
     lib.kvr_linear.restype = ctypes.c_int
     lib.kvr_linear_multi.argtypes = [_vp, ctypes.c_int32, _vpp, _i32p, _i64p, _vp, ctypes.c_int32, ctypes.c_int32,
-                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int64,
-                                     ctypes.c_int32, _vp]
+                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int64, _vp,
+                                     ctypes.c_int64, ctypes.c_int32, _vp]
     lib.kvr_linear_multi.restype = ctypes.c_int
     lib.kvr_attention_schedule.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _i32p, ctypes.c_int64]

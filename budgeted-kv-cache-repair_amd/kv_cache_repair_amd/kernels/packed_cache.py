@@ -251,8 +251,9 @@ def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=
     attention, residual add, post-attention RMSNorm, SiLU-gated MLP, residual
     add. Each RMSNorm is one kvr_rms_norm launch (the first residual add fused
     into the second norm); the MLP is kvr_linear_multi's SiLU-gated gate/up
-    launch plus the down projection when the shell carries projection plans,
-    else the module's linear layers around one kvr_silu_mul launch.
+    launch plus the down projection with the second residual add in its
+    epilogue when the shell carries projection plans, else the module's linear
+    layers around one kvr_silu_mul launch.
     """
     normed = _rms_norm(self.input_layernorm, hidden_states)
     attended, _ = self.self_attn(hidden_states=normed, attention_mask=attention_mask, position_ids=position_ids,
@@ -261,9 +262,9 @@ def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=
     normed, residual = _rms_norm(self.post_attention_layernorm, attended, residual=hidden_states)
     mlp = self.mlp
     plans = getattr(self, "_kvr_plans", None)
-    if plans is not None:
-        out = plans.down(plans.gate_up(normed))
-    elif isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
+    if plans is not None:  # gate/up with the SiLU gate, then down with the residual add
+        return plans.down(plans.gate_up(normed), residual=residual)
+    if isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
         out = mlp.down_proj(_silu_mul(mlp.gate_proj(normed), mlp.up_proj(normed)))
     else:
         out = mlp(normed)

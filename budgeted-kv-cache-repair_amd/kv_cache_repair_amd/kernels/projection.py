@@ -8,6 +8,7 @@ weights (fixed for the life of a model) to the C entry point:
   * one weight:               y = x w^T                  (o_proj, down_proj)
   * concatenated weights:     y = x [w0; w1; w2]^T       (q/k/v into one output)
   * SiLU-gated pair:          y = act(x gate^T) * (x up^T)  (the MLP front half)
+  * with a residual:          y = residual + x w^T          (down_proj + the layer's residual add)
 
 Same results as torch.nn.functional.linear up to fp32 summation order (the
 kernel accumulates in fp32 and rounds once); deterministic run to run. Plans
@@ -27,6 +28,7 @@ from .. import _native
 MAX_ROWS = 64
 CONCAT = 0
 SILU_GATE = 1
+RESIDUAL = 2
 _SUPPORTED = (torch.float16, torch.bfloat16)
 
 _scratch_lock = threading.Lock()
@@ -110,8 +112,11 @@ class ProjectionPlan:
             self._workspace[m] = need
         return need
 
-    def __call__(self, x: torch.Tensor, stream: int | None = None) -> torch.Tensor:
-        """y[..., n_out] for x[..., k] (rows of x contiguous, at most MAX_ROWS of them)."""
+    def __call__(self, x: torch.Tensor, stream: int | None = None, residual: torch.Tensor | None = None
+                 ) -> torch.Tensor:
+        """y[..., n_out] for x[..., k] (rows of x contiguous, at most MAX_ROWS of them);
+        with ``residual`` (same shape as y, rows contiguous) y = residual + x w^T,
+        rounded as the eager add rounds it."""
         if x.dtype != self.dtype or x.device != self.device or x.shape[-1] != self.k or x.stride(-1) != 1:
             raise RuntimeError("projection input geometry/dtype/device drifted")
         m = x.numel() // self.k
@@ -124,9 +129,16 @@ class ProjectionPlan:
         need = self.workspace_bytes(m)
         workspace = _scratch_for(self.device, stream).reserve(need).data_ptr() if need else None
         y = torch.empty((*x.shape[:-1], self.n_out), dtype=self.dtype, device=self.device)
+        epilogue, res, ldr = self.epilogue, None, 0
+        if residual is not None:
+            if self.epilogue != CONCAT or residual.shape != y.shape or residual.dtype != self.dtype \
+                    or residual.device != self.device or residual.stride(-1) != 1:
+                raise RuntimeError("projection residual geometry/dtype/device drifted")
+            res2d = residual.reshape(m, self.n_out)
+            epilogue, res, ldr = RESIDUAL, res2d.data_ptr(), int(res2d.stride(0))
         status = _native.lib().kvr_linear_multi(
             rows2d.data_ptr(), self._count, self._w, self._rows, self._ldw, y.data_ptr(), m, self.k, ldx,
-            self.n_out, self.epilogue, workspace, need, self._code, ctypes.c_void_p(stream))
+            self.n_out, epilogue, res, ldr, workspace, need, self._code, ctypes.c_void_p(stream))
         _native.check(status, "kvr_linear_multi")
         return y
 

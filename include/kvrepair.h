@@ -44,6 +44,7 @@ enum kvr_dtype {
 enum kvr_linear_epilogue {
     KVR_LINEAR_CONCAT = 0,     /* y[:, off_i + r] = x . w_i[r]; off_i = rows of the weights before i */
     KVR_LINEAR_SILU_GATE = 1,  /* y[:, r] = silu(x . w_0[r]) * (x . w_1[r]), eager rounding */
+    KVR_LINEAR_RESIDUAL = 2,   /* as CONCAT, then y = dtype(dtype(y) + residual) (the layer's residual add) */
 };
 
 enum kvr_status {
@@ -201,7 +202,10 @@ int kvr_linear(const void* x, const void* w, void* y, int32_t m, int32_t n, int3
                int64_t ldy, void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream);
 
 /* Up to three weights in one launch. KVR_LINEAR_CONCAT: outputs side by side
- * (the q/k/v projections of one layer into [M][nq + nk + nv]);
+ * (the q/k/v projections of one layer into [M][nq + nk + nv]); KVR_LINEAR_RESIDUAL:
+ * the same plus `residual` ([M][ldr], may alias y with ldr == ldy) as
+ * `residual + down_proj(x)` rounds it (modeling_llama.py:328); `residual`/`ldr`
+ * are ignored by the other epilogues;
  * KVR_LINEAR_SILU_GATE: two weights of equal rows (gate_proj, up_proj), y =
  * dtype(dtype(silu(dtype(x gate^T))) * dtype(x up^T)) -- the MLP's
  * act_fn(gate_proj(x)) * up_proj(x) (modeling_llama.py:174) with the
@@ -209,7 +213,8 @@ int kvr_linear(const void* x, const void* w, void* y, int32_t m, int32_t n, int3
  * same split count followed by kvr_silu_mul. */
 int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
                      const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy, int32_t epilogue,
-                     void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream);
+                     const void* residual, int64_t ldr, void* workspace, int64_t workspace_bytes, int32_t dtype,
+                     void* stream);
 
 /*
  * Host-side work schedule for kvr_packed_causal_attention (no device access).

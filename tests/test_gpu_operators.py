@@ -371,6 +371,24 @@ def test_silu_gate_linear_is_bitwise_linear_then_silu_mul(gpu_device, dtype, sha
     assert (dist <= 2).float().mean().item() >= 0.99
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(4096, 14336), (100, 136)])
+def test_linear_residual_epilogue_is_bitwise_linear_then_add(gpu_device, dtype, shape):
+    """down_proj + the layer's residual add in one launch equals kvr_linear then
+    the eager `residual + out` bit for bit (split and unsplit K)."""
+    from kv_cache_repair_amd.kernels import projection
+
+    n, k = shape
+    torch.manual_seed(k)
+    x = torch.randn(1, 64, k, device=gpu_device).to(dtype)
+    w = (torch.randn(n, k, device=gpu_device) * 0.02).to(dtype)
+    residual = (torch.randn(1, 64, n, device=gpu_device) * 4).to(dtype)
+    plan = projection.ProjectionPlan([w])
+    assert bits_equal(plan(x, residual=residual), residual + plan(x))
+    with pytest.raises(RuntimeError, match="residual"):
+        plan(x, residual=residual[..., :-1])
+
+
 def test_projection_plans_reject_what_they_cannot_serve(gpu_device):
     from kv_cache_repair_amd.kernels import projection
 

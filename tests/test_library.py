@@ -91,12 +91,14 @@ def test_entry_points_validate_before_any_launch():
     rows = (ctypes.c_int32 * 3)(4096, 1024, 1024)
     ldw = _native.i64_array([4096] * 3)
     args = (64, 4096, 4096, 6144)
-    assert lib.kvr_linear_multi(16, 4, w3, rows, ldw, 16, *args, 0, None, 0, 2, None) == -1  # > 3 weights
-    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 2, None, 0, 2, None) == -1  # epilogue
-    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 1, None, 0, 2, None) == -3  # gate: 2 only
-    assert lib.kvr_linear_multi(16, 2, w3, rows, ldw, 16, *args, 1, None, 0, 2, None) == -3  # unequal rows
-    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, 64, 4096, 4096, 6143, 0, None, 0, 2, None) == -4
-    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 0, None, 0, 2, None) == -6  # workspace
+    assert lib.kvr_linear_multi(16, 4, w3, rows, ldw, 16, *args, 0, None, 0, None, 0, 2, None) == -1  # > 3 weights
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 3, None, 0, None, 0, 2, None) == -1  # epilogue
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 1, None, 0, None, 0, 2, None) == -3  # gate: 2 only
+    assert lib.kvr_linear_multi(16, 2, w3, rows, ldw, 16, *args, 1, None, 0, None, 0, 2, None) == -3  # unequal rows
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, 64, 4096, 4096, 6143, 0, None, 0, None, 0, 2, None) == -4
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 0, None, 0, None, 0, 2, None) == -6  # workspace
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 2, None, 0, None, 0, 2, None) == -5  # residual
+    assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 2, 16, 6000, None, 0, 2, None) == -4  # ldr
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
