@@ -19,8 +19,9 @@ the step, as in the reference benchmark (benchmark_refresh.py:3-9); unlike it,
 the rotation is inside.
 
 Printed (one JSON line): stage latency (ms per repair, K uninstrumented
-steps), the per-kernel HIP event timings of K more identical steps (events
-around every libkvrepair launch), a roofline object for the dominant kernel,
+steps), the per-kernel HIP event timings of K more steps that dispatch the
+same kernels one by one from Python (events around every libkvrepair
+launch), a roofline object for the dominant kernel,
 the rotate-only GB/s, the same stage run the reference way on the same GPU,
 and the reference path timed on the host CPU (cpu_baseline).
 """
@@ -112,12 +113,12 @@ def make_request(device, layers=LAYERS):
 
 
 # ----------------------------------------------------------------------------- our stage
-def hip_stage(shim, old, old_ids, new_ids, intervals):
+def hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=None):
     from kv_cache_repair_amd.cache import build_halo_cache
     from kv_cache_repair_amd.kernels.packed_cache import packed_refresh_owned_
 
     cache, _ = build_halo_cache(shim, old, old_ids, new_ids, 0)
-    packed_refresh_owned_(shim, cache, new_ids, intervals)
+    packed_refresh_owned_(shim, cache, new_ids, intervals, native_layers=native_layers)
     return cache
 
 
@@ -399,14 +400,19 @@ def main(argv=None) -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # `value`: K uninstrumented steps (the stage is partly host-bound, so per-launch
-    # events would inflate it); then the same K steps again with HIP events around
-    # every libkvrepair launch for the per-kernel timings and the roofline.
+    # `value`: K uninstrumented steps (each decoder layer is one native call that
+    # enqueues its kernels from C). Then K more steps with every layer's kernels
+    # dispatched one by one from Python (native_layers=False: the same kernels
+    # with the same arguments, bit-identical output) and HIP events around each
+    # libkvrepair launch, for the per-kernel timings and the roofline.
     ms = time_steps(step, args.steps, 0)
+    dispatched = lambda: hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=False)  # noqa: E731
+    dispatched()
+    torch.cuda.synchronize()
     timer = KernelTimer()
     timer.install()
     timer.active = True
-    instrumented_ms = time_steps(step, args.steps, 0)
+    instrumented_ms = time_steps(dispatched, args.steps, 0)
     timer.active = False
     torch.cuda.synchronize()
     kernels = timer.summary(args.steps)

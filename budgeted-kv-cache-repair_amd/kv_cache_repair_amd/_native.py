@@ -32,6 +32,29 @@ class NativeError(RuntimeError):
     """A kvrepair C entry point returned a negative status."""
 
 
+class LayerDesc(ctypes.Structure):
+    """Mirror of kvr_layer_desc (include/kvrepair.h)."""
+
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "input_norm", "post_norm", "q_norm", "k_norm", "w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down")] + \
+        [(name, ctypes.c_int64) for name in ("ld_q", "ld_k", "ld_v", "ld_o", "ld_gate", "ld_up", "ld_down")] + \
+        [(name, ctypes.c_float) for name in ("eps_input", "eps_post", "eps_q", "eps_k")] + \
+        [("cache_k", ctypes.c_void_p), ("cache_v", ctypes.c_void_p), ("cache_strides", ctypes.c_int64 * 6)]
+
+
+class RefreshDesc(ctypes.Structure):
+    """Mirror of kvr_refresh_desc (include/kvrepair.h)."""
+
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "rows", "hidden", "q_heads", "kv_heads", "head_dim", "intermediate")] + [
+        ("n_keys", ctypes.c_int64), ("scale", ctypes.c_float), ("dtype", ctypes.c_int32),
+        ("positions", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+        ("cs_strides", ctypes.c_int64 * 4), ("schedule", ctypes.c_void_p), ("schedule_len", ctypes.c_int64),
+        ("host_schedule", ctypes.c_void_p), ("attn_workspace", ctypes.c_void_p),
+        ("attn_workspace_bytes", ctypes.c_int64), ("gemm_workspace", ctypes.c_void_p),
+        ("gemm_workspace_bytes", ctypes.c_int64), ("scratch", ctypes.c_void_p), ("scratch_bytes", ctypes.c_int64)]
+
+
 def _declare(lib: ctypes.CDLL) -> None:
     lib.kvr_abi_version.argtypes = []
     lib.kvr_abi_version.restype = ctypes.c_int
@@ -69,6 +92,16 @@ def _declare(lib: ctypes.CDLL) -> None:
                                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int64, _vp,
                                      ctypes.c_int64, ctypes.c_int32, _vp]
     lib.kvr_linear_multi.restype = ctypes.c_int
+    _desc_p = ctypes.POINTER(LayerDesc)
+    _refresh_p = ctypes.POINTER(RefreshDesc)
+    lib.kvr_decoder_scratch_bytes.argtypes = [_refresh_p]
+    lib.kvr_decoder_scratch_bytes.restype = ctypes.c_int64
+    lib.kvr_decoder_gemm_workspace_bytes.argtypes = [_refresh_p]
+    lib.kvr_decoder_gemm_workspace_bytes.restype = ctypes.c_int64
+    lib.kvr_decoder_layer.argtypes = [_desc_p, _refresh_p, _vp, _vp]
+    lib.kvr_decoder_layer.restype = ctypes.c_int
+    lib.kvr_decoder_desc_sizes.argtypes = [_i64p]
+    lib.kvr_decoder_desc_sizes.restype = None
     lib.kvr_attention_schedule.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _i32p, ctypes.c_int64]
     lib.kvr_attention_schedule.restype = ctypes.c_int64
@@ -98,6 +131,10 @@ def lib() -> ctypes.CDLL:
             version = handle.kvr_abi_version()
             if version != ABI_VERSION:
                 raise NativeError(f"libkvrepair ABI {version} != expected {ABI_VERSION}; rebuild the library")
+            sizes = (ctypes.c_int64 * 2)()
+            handle.kvr_decoder_desc_sizes(sizes)
+            if tuple(sizes) != (ctypes.sizeof(LayerDesc), ctypes.sizeof(RefreshDesc)):
+                raise NativeError(f"libkvrepair descriptor sizes {tuple(sizes)} do not match the bindings; rebuild")
             _lib = handle
     return _lib
 

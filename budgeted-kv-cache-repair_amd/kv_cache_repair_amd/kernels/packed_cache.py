@@ -50,6 +50,7 @@ class _PackedContext:
     backend: str
     device_plan: Any = None
     launcher: Any = None
+    native: Any = None
 
 
 @dataclass
@@ -201,6 +202,7 @@ class _LayerPlans:
     down: Any
     q_cols: int
     k_cols: int
+    desc: Any = None  # kvr_layer_desc template (no cache pointers) for kvr_decoder_layer, or None
 
 
 _PLAN_CACHE: "weakref.WeakKeyDictionary[Any, _LayerPlans]" = weakref.WeakKeyDictionary()
@@ -224,7 +226,11 @@ def _layer_plans(layer) -> _LayerPlans | None:
     weights = [m.weight for m in modules]
     if len({(w.dtype, w.device) for w in weights}) != 1 or weights[4].shape != weights[5].shape:
         return None
-    pointers = tuple(int(w.data_ptr()) for w in weights)
+    norms = [layer.input_layernorm, layer.post_attention_layernorm]
+    if getattr(attention, "q_norm", None) is not None:
+        norms += [attention.q_norm, attention.k_norm]
+    pointers = tuple(int(w.data_ptr()) for w in weights) + tuple(
+        int(n.weight.data_ptr()) if isinstance(getattr(n, "weight", None), torch.Tensor) else 0 for n in norms)
     with _PLAN_LOCK:
         cached = _PLAN_CACHE.get(layer)
         if cached is not None and cached.pointers == pointers:
@@ -236,10 +242,37 @@ def _layer_plans(layer) -> _LayerPlans | None:
         pointers=pointers, qkv=None if separate else plan([q, k, v]), q=plan([q]) if separate else None,
         k=plan([k]) if separate else None, v=plan([v]) if separate else None, o=plan([o]),
         gate_up=plan([gate, up], _projection.SILU_GATE), down=plan([down]), q_cols=int(q.shape[0]),
-        k_cols=int(k.shape[0]))
+        k_cols=int(k.shape[0]), desc=_layer_desc(layer, weights, norms))
     with _PLAN_LOCK:
         _PLAN_CACHE[layer] = plans
     return plans
+
+
+def _layer_desc(layer, weights, norms):
+    """kvr_layer_desc of ``layer`` without cache pointers, or None when a norm is
+    not a plain weight-times-normalised RMSNorm of the projections' dtype."""
+    dtype, device = weights[0].dtype, weights[0].device
+    hidden = int(weights[3].shape[0])
+    head_dim = int(getattr(layer.self_attn, "head_dim", 0))
+    for i, norm in enumerate(norms):
+        w = getattr(norm, "weight", None)
+        size = hidden if i < 2 else head_dim
+        if not isinstance(w, torch.Tensor) or w.dtype != dtype or w.device != device or tuple(w.shape) != (size,) \
+                or not w.is_contiguous() or not isinstance(getattr(norm, "variance_epsilon", None), float):
+            return None
+    q, k, v, o, gate, up, down = weights
+    desc = _native.LayerDesc()
+    desc.input_norm, desc.post_norm = norms[0].weight.data_ptr(), norms[1].weight.data_ptr()
+    desc.q_norm = norms[2].weight.data_ptr() if len(norms) > 2 else None
+    desc.k_norm = norms[3].weight.data_ptr() if len(norms) > 2 else None
+    desc.w_q, desc.w_k, desc.w_v, desc.w_o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    desc.w_gate, desc.w_up, desc.w_down = gate.data_ptr(), up.data_ptr(), down.data_ptr()
+    desc.ld_q, desc.ld_k, desc.ld_v, desc.ld_o = q.stride(0), k.stride(0), v.stride(0), o.stride(0)
+    desc.ld_gate, desc.ld_up, desc.ld_down = gate.stride(0), up.stride(0), down.stride(0)
+    desc.eps_input, desc.eps_post = norms[0].variance_epsilon, norms[1].variance_epsilon
+    if len(norms) > 2:
+        desc.eps_q, desc.eps_k = norms[2].variance_epsilon, norms[3].variance_epsilon
+    return desc
 
 
 def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
@@ -269,6 +302,89 @@ def _fused_layer_forward(self, hidden_states, attention_mask=None, position_ids=
     else:
         out = mlp(normed)
     return residual + out
+
+
+class _NativeForward:
+    """kvr_refresh_desc of one refresh and the device buffers it points into
+    (scratch slab for the layer intermediates, projection workspace)."""
+
+    def __init__(self, launcher: _Launcher, hidden: int, intermediate: int, scale: float):
+        d = _native.RefreshDesc()
+        d.rows, d.hidden, d.intermediate = launcher.n_sel, hidden, intermediate
+        d.q_heads, d.kv_heads, d.head_dim = launcher.q_heads, launcher.kv_heads, launcher.head_dim
+        d.n_keys, d.scale, d.dtype = launcher.n_keys, scale, launcher.dtype_code
+        d.positions = launcher.positions_ptr
+        d.schedule = launcher.device_schedule.data_ptr()
+        d.schedule_len = len(launcher.host_schedule)
+        d.host_schedule = ctypes.cast(launcher.host_schedule, ctypes.c_void_p)
+        if launcher.workspace is not None:
+            d.attn_workspace, d.attn_workspace_bytes = launcher.workspace.data_ptr(), launcher.workspace_bytes
+        lib = _native.lib()
+        scratch = int(lib.kvr_decoder_scratch_bytes(ctypes.byref(d)))
+        _native.check(scratch, "kvr_decoder_scratch_bytes")
+        gemm = int(lib.kvr_decoder_gemm_workspace_bytes(ctypes.byref(d)))
+        _native.check(gemm, "kvr_decoder_gemm_workspace_bytes")
+        self.scratch = torch.empty(scratch, dtype=torch.uint8, device=launcher.device)
+        self.gemm = torch.empty(gemm, dtype=torch.uint8, device=launcher.device) if gemm else None
+        d.scratch, d.scratch_bytes = self.scratch.data_ptr(), scratch
+        if self.gemm is not None:
+            d.gemm_workspace, d.gemm_workspace_bytes = self.gemm.data_ptr(), gemm
+        self.desc = d
+        self.tables = None
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream(launcher.device).cuda_stream)
+
+    def bind_tables(self, position_embeddings) -> None:
+        """Point the descriptor at the forward's rotary tables (shared by all layers)."""
+        if position_embeddings is None:
+            raise RuntimeError("native packed layer requires the model's rotary embeddings")
+        cos, sin = position_embeddings
+        if self.tables is not None and self.tables[0] is cos and self.tables[1] is sin:
+            return
+        d = self.desc
+        for table in (cos, sin):
+            if table.shape[-2:] != (d.rows, d.head_dim) or table.numel() != d.rows * d.head_dim \
+                    or _native.DTYPE_CODES.get(table.dtype) != d.dtype:
+                raise RuntimeError("packed native rotary embedding geometry/dtype drifted")
+        d.cos, d.sin = cos.data_ptr(), sin.data_ptr()
+        d.cs_strides[:] = (cos.stride(-2), cos.stride(-1), sin.stride(-2), sin.stride(-1))
+        self.tables = (cos, sin)
+
+
+def _native_layer_forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
+                          use_cache=False, position_embeddings=None, sur_packed_context=None, **kwargs):
+    """Decoder layer of a packed shell as ONE kvr_decoder_layer call.
+
+    The same kernels, arguments and order as _fused_layer_forward with
+    projection plans plus _fused_attention_forward (bit-identical output), but
+    enqueued from C: input RMSNorm, q/k/v projection (+ Qwen3 q/k norms), RoPE of
+    the fresh rows + K/V scatter into this layer's cache, packed attention, o
+    projection, residual + post-attention RMSNorm, SiLU-gated gate/up, down +
+    residual. ``hidden_states`` ([1, B, hidden], contiguous) is updated in place.
+    """
+    context = sur_packed_context
+    if not isinstance(context, _PackedContext) or context.native is None:
+        raise RuntimeError("packed attention requires explicit per-call request context")
+    if attention_mask is not None:
+        raise RuntimeError("native dense mask construction must be bypassed for packed attention")
+    if not isinstance(past_key_values, Cache):
+        raise RuntimeError("packed fused epilogue requires the packed cache layers")
+    layer = past_key_values.layers[self.self_attn.layer_idx]
+    if not isinstance(layer, _PackedLayer) or layer.updated:
+        raise RuntimeError("native packed forward updated one layer more than once")
+    native = context.native
+    native.bind_tables(position_embeddings)
+    d = native.desc
+    if hidden_states.shape != (1, d.rows, d.hidden) or not hidden_states.is_contiguous() \
+            or _native.DTYPE_CODES.get(hidden_states.dtype) != d.dtype:
+        raise RuntimeError("packed native hidden-state geometry/dtype drifted")
+    desc = self._kvr_layer_desc
+    if desc.cache_k != layer.keys.data_ptr() or desc.cache_v != layer.values.data_ptr():
+        raise RuntimeError("packed native cache layer drifted")
+    status = _native.lib().kvr_decoder_layer(ctypes.byref(desc), ctypes.byref(d), hidden_states.data_ptr(),
+                                             native.stream)
+    _native.check(status, "kvr_decoder_layer")
+    layer.updated = True
+    return hidden_states
 
 
 def _fused_norm_forward(self, hidden_states):
@@ -336,13 +452,15 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     return (plans.o(attended) if plans is not None else self.o_proj(attended)), None
 
 
-def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True, plans=None):
+def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True, plans=None, layer_descs=None):
     """Shallow module shells sharing parameters, with a private config naming the
     packed attention; the caller's modules and config are never modified. With
     ``fused_epilogue`` the attention shells run _fused_attention_forward; with
     ``fused_layers`` the layer and final-norm shells run their fused forwards.
     ``plans`` (one _LayerPlans or None per layer) routes the shells'
-    projections through kvr_linear_multi."""
+    projections through kvr_linear_multi; ``layer_descs`` (one kvr_layer_desc
+    per layer, cache pointers filled) runs each layer shell as one
+    kvr_decoder_layer call."""
     _register_attention()
     config = copy.deepcopy(base.config)
     config._attn_implementation = _ATTENTION_NAME
@@ -363,7 +481,10 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
             attention.forward = types.MethodType(_fused_attention_forward, attention)
             attention._kvr_fused_norms = fused_layers
             attention._kvr_plans = layer_plans
-        if fused_layers:
+        if layer_descs is not None:
+            layer.forward = types.MethodType(_native_layer_forward, layer)
+            layer._kvr_layer_desc = layer_descs[len(layers)]
+        elif fused_layers:
             layer.forward = types.MethodType(_fused_layer_forward, layer)
             layer._kvr_plans = layer_plans
         layer._modules["self_attn"] = attention
@@ -551,18 +672,53 @@ def _projection_plans_for(base, fused_projections, dtype: torch.dtype, selected:
     return [_layer_plans(layer) for layer in base.layers]
 
 
+def _native_layers_for(native_layers, base, plans, fused_epilogue: bool, fused_layers: bool):
+    """Whether every layer runs as one kvr_decoder_layer call. Default (None): yes
+    when the projection plans, fused epilogue and fused layer ops are all in use
+    and every layer has a native descriptor and the same attention scale."""
+    possible = (plans is not None and fused_epilogue and fused_layers
+                and all(p is not None and p.desc is not None for p in plans)
+                and len({float(layer.self_attn.scaling) for layer in base.layers}) == 1)
+    if native_layers is None:
+        return possible
+    if native_layers and not possible:
+        raise ValueError("native_layers=True needs fp16/bf16 plain-linear Llama/Qwen3 layers, <= 64 selected rows, "
+                         "and the fused epilogue, layer ops and projections")
+    return bool(native_layers)
+
+
+def _native_layer_descs(plans, output, layer_count):
+    """Per-refresh copies of the layers' descriptors with this cache's pointers."""
+    descs = []
+    for i in range(layer_count):
+        keys, values = layer_kv(output, i)
+        desc = _native.LayerDesc.from_buffer_copy(plans[i].desc)
+        desc.cache_k, desc.cache_v = keys.data_ptr(), values.data_ptr()
+        desc.cache_strides[:] = (*_native.strides3(keys), *_native.strides3(values))
+        descs.append(desc)
+    return descs
+
+
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
                   attention_backend: str, writeback_backend: str, fused_epilogue: bool = True,
-                  fused_layers: bool | None = None, fused_projections: bool | None = None) -> None:
+                  fused_layers: bool | None = None, fused_projections: bool | None = None,
+                  native_layers: bool | None = None) -> None:
     """Run the packed forward, scattering into the caller-owned ``output`` cache."""
     base = shim._base_transformer(shim.generator)
     device_plan = host_plan.to(edited_ids_t.device)
     positions = device_plan.positions
     key0 = layer_kv(output, 0)[0]
-    context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan,
-                             _launcher(device_plan, base.config, key0))
+    launcher = _launcher(device_plan, base.config, key0)
+    context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan, launcher)
     plans = _projection_plans_for(base, fused_projections, key0.dtype, device_plan.selected_count)
-    native_view = _make_native_view(base, fused_epilogue, _fused_layers_for(fused_layers, key0.dtype), plans)
+    fused_layers = _fused_layers_for(fused_layers, key0.dtype)
+    descs = None
+    if _native_layers_for(native_layers, base, plans, fused_epilogue, fused_layers):
+        first = base.layers[0]
+        context.native = _NativeForward(launcher, int(first.mlp.down_proj.weight.shape[0]),
+                                        int(first.mlp.gate_proj.weight.shape[0]), float(first.self_attn.scaling))
+        descs = _native_layer_descs(plans, output, layer_count)
+    native_view = _make_native_view(base, fused_epilogue, fused_layers, plans, descs)
     layers = [_PackedLayer(*layer_kv(output, i), context, writeback_backend) for i in range(layer_count)]
     cache = Cache(layers=layers)
     result = native_view(input_ids=edited_ids_t.index_select(1, positions), position_ids=positions.unsqueeze(0),
@@ -575,8 +731,8 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
 def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
                            intervals: Sequence[tuple[int, int]], *, attention_backend: str = "hip",
                            writeback_backend: str = "hip", plan: Any = None, fused_epilogue: bool = True,
-                           fused_layers: bool | None = None,
-                           fused_projections: bool | None = None) -> tuple[Any, dict[str, Any]]:
+                           fused_layers: bool | None = None, fused_projections: bool | None = None,
+                           native_layers: bool | None = None) -> tuple[Any, dict[str, Any]]:
     """Recompute sorted selected rows in one native layer-major forward.
 
     Same signature, validation order, receipt and ownership contract as the
@@ -596,6 +752,10 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     one; fp32 accumulation rounded once, like the library GEMM up to summation
     order); the default (None) uses them for fp16/bf16 caches with at most 64
     selected rows, where the modules' GEMMs are weight-streaming bound.
+    ``native_layers`` runs each decoder layer as one kvr_decoder_layer call
+    (the same kernels in the same order, bit-identical to the Python-dispatched
+    fused path); the default (None) does so whenever the three fusions above
+    are all active.
     """
     _check_backends(attention_backend, writeback_backend)
     _check_ids(edited_ids_t)
@@ -615,7 +775,7 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
 
     output = clone_cache(base_cache)
     _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend,
-                  bool(fused_epilogue), fused_layers, fused_projections)
+                  bool(fused_epilogue), fused_layers, fused_projections, native_layers)
     return output, receipt
 
 
@@ -623,7 +783,7 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
 def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tensor,
                           intervals: Sequence[tuple[int, int]], *, plan: Any = None,
                           fused_epilogue: bool = True, fused_layers: bool | None = None,
-                          fused_projections: bool | None = None) -> dict[str, Any]:
+                          fused_projections: bool | None = None, native_layers: bool | None = None) -> dict[str, Any]:
     """Packed refresh that scatters IN PLACE into a cache the caller owns.
 
     For a cache the caller has just built and nobody else references (the
@@ -646,5 +806,5 @@ def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tenso
     _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
     _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue),
-                  fused_layers, fused_projections)
+                  fused_layers, fused_projections, native_layers)
     return receipt

@@ -217,6 +217,70 @@ int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, con
                      void* stream);
 
 /*
+ * One decoder layer of the packed refresh, enqueued by a single call.
+ *
+ * The packed executor's layer (transformers 5.15.0 modeling_llama.py:301-330 /
+ * modeling_qwen3.py:287-316 routed through the packed plugin points of
+ * packed_cache.py:85-200 in the reference) as one host call that enqueues its
+ * kernels back to back: input RMSNorm -> q/k/v projection (one launch; three for
+ * Qwen3, whose per-head q/k RMSNorms follow) -> RoPE of the fresh rows + K/V
+ * scatter into this layer's cache -> packed causal attention -> o projection ->
+ * residual add + post-attention RMSNorm -> SiLU-gated gate/up projection ->
+ * down projection + residual add. Same kernels and arithmetic as the separate
+ * entry points, so the result is bit-identical to calling them in that order.
+ * `hidden` ([rows][hidden], row-major) is read and overwritten in place with
+ * the layer's output. No reference counterpart of its own: it replaces the
+ * per-op Python dispatch of the executor's module shells.
+ */
+typedef struct kvr_layer_desc {
+    const void* input_norm;   /* [hidden] */
+    const void* post_norm;    /* [hidden] */
+    const void* q_norm;       /* [head_dim] per-head RMSNorm weight (Qwen3) or NULL */
+    const void* k_norm;       /* [head_dim] or NULL; both or neither */
+    const void* w_q;          /* [q_heads * head_dim][ld_q] */
+    const void* w_k;          /* [kv_heads * head_dim][ld_k] */
+    const void* w_v;
+    const void* w_o;          /* [hidden][ld_o] */
+    const void* w_gate;       /* [intermediate][ld_gate] */
+    const void* w_up;
+    const void* w_down;       /* [hidden][ld_down] */
+    int64_t ld_q, ld_k, ld_v, ld_o, ld_gate, ld_up, ld_down;
+    float eps_input, eps_post, eps_q, eps_k;
+    void* cache_k;            /* this layer's [1, kv_heads, n_keys, head_dim] K and V */
+    void* cache_v;
+    int64_t cache_strides[6]; /* K {head, row, dim}, V {head, row, dim} in elements */
+} kvr_layer_desc;
+
+typedef struct kvr_refresh_desc {
+    int32_t rows;             /* selected rows (<= 64) */
+    int32_t hidden, q_heads, kv_heads, head_dim, intermediate;
+    int64_t n_keys;
+    float scale;              /* attention scale */
+    int32_t dtype;            /* KVR_DTYPE_BF16 or KVR_DTYPE_F16 */
+    const int64_t* positions; /* device, sorted */
+    const void* cos;          /* [rows][head_dim] rotary tables at the positions */
+    const void* sin;
+    int64_t cs_strides[4];    /* cos {row, dim}, sin {row, dim} */
+    const int32_t* schedule;  /* kvr_attention_schedule output: device copy, length, host copy */
+    int64_t schedule_len;
+    const int32_t* host_schedule;
+    void* attn_workspace;     /* kvr_attention_workspace_bytes */
+    int64_t attn_workspace_bytes;
+    void* gemm_workspace;     /* max kvr_linear_workspace_bytes over the layer's projections */
+    int64_t gemm_workspace_bytes;
+    void* scratch;            /* kvr_decoder_scratch_bytes, 256-byte aligned */
+    int64_t scratch_bytes;
+} kvr_refresh_desc;
+
+/* Scratch bytes kvr_decoder_layer needs for `d` (negative status if `d` is unsupported). */
+int64_t kvr_decoder_scratch_bytes(const kvr_refresh_desc* d);
+/* GEMM workspace bytes kvr_decoder_layer needs for `d`. */
+int64_t kvr_decoder_gemm_workspace_bytes(const kvr_refresh_desc* d);
+int kvr_decoder_layer(const kvr_layer_desc* layer, const kvr_refresh_desc* d, void* hidden, void* stream);
+/* sizeof(kvr_layer_desc), sizeof(kvr_refresh_desc): lets bindings check their struct mirrors. */
+void kvr_decoder_desc_sizes(int64_t sizes[2]);
+
+/*
  * Host-side work schedule for kvr_packed_causal_attention (no device access).
  * Splits the selected rows into row groups and each group's causal key range
  * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`

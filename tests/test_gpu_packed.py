@@ -423,3 +423,30 @@ def test_projection_plans_match_module_linears(gpu_device, family, dtype):
     moved, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=True)
     assert all(torch.equal(x.keys, y.keys) for x, y in zip(moved.layers, fused.layers))
 
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_native_layer_call_is_bit_identical_to_dispatched_fused_layers(gpu_device, family, dtype):
+    """kvr_decoder_layer enqueues the same kernels with the same arguments as the
+    Python-dispatched fused shells, so the refreshed caches are bit-identical;
+    it is the default whenever the fusions are active, and refuses requests
+    it cannot serve instead of falling back silently."""
+    from kv_cache_repair_amd.kernels import packed_cache as pc
+
+    model = make_model(gpu_device, family, kv_heads=2, head_dim=64, dtype=dtype, layers=3)
+    shim, ids, base = make_request(model, length=140)
+    edited = ids.clone()
+    edited[0, 70:] = (edited[0, 70:] + 7) % 97
+    intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
+    native, _ = pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True)
+    dispatched, _ = pc.packed_interval_repair(shim, base, edited, intervals, native_layers=False)
+    default, _ = pc.packed_interval_repair(shim, base, edited, intervals)
+    for a, b, c in zip(native.layers, dispatched.layers, default.layers):
+        for x, y, z in ((a.keys, b.keys, c.keys), (a.values, b.values, c.values)):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+            assert torch.equal(x.view(torch.int16), z.view(torch.int16))
+    with pytest.raises(ValueError, match="native_layers"):
+        pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True, fused_projections=False)
+    with pytest.raises(ValueError, match="native_layers"):  # more rows than one projection launch serves
+        pc.packed_interval_repair(shim, base, edited, [(0, 65)], native_layers=True)

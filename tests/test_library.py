@@ -25,7 +25,8 @@ def test_header_declares_the_entry_points():
         "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
         "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
         "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
-        "kvr_linear_workspace_bytes", "kvr_linear_multi"])
+        "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
+        "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_desc_sizes"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -182,3 +183,28 @@ def test_workspace_is_zero_when_every_tile_fits_one_chunk():
     s = schedule(list(range(0, 8000, 100)), 8000, 4, 2, 64, chunk=256)
     buf = (ctypes.c_int32 * len(s))(*s)
     assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 64 * 66 * 4
+
+
+def test_decoder_layer_descriptors_validate_before_any_launch():
+    import ctypes as C
+
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    sizes = (C.c_int64 * 2)()
+    lib.kvr_decoder_desc_sizes(sizes)
+    assert tuple(sizes) == (C.sizeof(_native.LayerDesc), C.sizeof(_native.RefreshDesc))
+    d = _native.RefreshDesc(rows=64, hidden=4096, q_heads=32, kv_heads=8, head_dim=128, intermediate=14336,
+                            n_keys=7680, scale=128 ** -0.5, dtype=2)
+    # normed, q|k|v, q/k norms, rotated q, attention out, o, residual sum, MLP activation: 64 rows each
+    expect = 64 * 2 * (4096 + 6144 + 4096 + 1024 + 4096 + 4096 + 4096 + 4096 + 14336)
+    assert lib.kvr_decoder_scratch_bytes(C.byref(d)) == expect
+    assert lib.kvr_decoder_gemm_workspace_bytes(C.byref(d)) == max(
+        lib.kvr_linear_workspace_bytes(64, r, k) for r, k in
+        ((6144, 4096), (4096, 4096), (1024, 4096), (28672, 4096), (4096, 14336)))
+    for field, value, status in (("rows", 65, -3), ("dtype", 0, -2), ("q_heads", 30, -3), ("scale", 0.0, -1)):
+        bad = _native.RefreshDesc.from_buffer_copy(d)
+        setattr(bad, field, value)
+        assert lib.kvr_decoder_scratch_bytes(C.byref(bad)) == status, field
+    layer = _native.LayerDesc()
+    assert lib.kvr_decoder_layer(C.byref(layer), C.byref(d), None, None) == -5  # nothing bound
