@@ -14,9 +14,12 @@
 //   act    = silu(normed W_gate^T) * (normed W_up^T)            kvr_linear_multi (gated)
 //   hidden = hidden2 + act W_down^T                             kvr_linear_multi (residual)
 //
-// Every step is the same entry point the Python shells call, with the same
+// Every step is the same kernel the Python shells launch, with the same
 // arguments, so the layer output is bit-identical to the step-by-step path;
-// what disappears is ~10 Python-level dispatches per layer.
+// what disappears is ~10 Python-level dispatches per layer and three split-K
+// reduce launches, whose sums are read straight from the partials by the next
+// kernel (RoPE + scatter, residual + post-attention norm, residual + the next
+// layer's input norm), with the reduce kernel's summation order and rounding.
 #include "kvr_internal.h"
 
 namespace kvr {
@@ -137,21 +140,25 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
         if (st < 0) return st; \
     } while (0)
 
-    // input RMSNorm
+    // input RMSNorm (already in `normed` when the previous layer fused it into its down projection)
     const int64_t rows_h[4] = {h, h, h, h};
-    KVR_TRY(kvr_rms_norm(hidden, nullptr, nullptr, normed, L->input_norm, m, h, rows_h, L->eps_input, dt, stream));
+    if (!L->input_normed)
+        KVR_TRY(kvr_rms_norm(hidden, nullptr, nullptr, normed, L->input_norm, m, h, rows_h, L->eps_input, dt, stream));
+    const PartialSums gemm_partials{static_cast<const float*>(gws), 0};
+    const bool norm_partials = rms_norm_partials_ok(h, dt);
 
     // q/k/v projections (+ Qwen3's per-head norms)
     const char* qp;
     const char* kp;
     const char* vp;
     int64_t q_ld, k_ld, v_ld;
+    int32_t qkv_splits = 1;
     if (!qk_norm) {
         const void* w[3] = {L->w_q, L->w_k, L->w_v};
         const int32_t rows[3] = {qd, kd, kd};
         const int64_t ldw[3] = {L->ld_q, L->ld_k, L->ld_v};
-        KVR_TRY(kvr_linear_multi(normed, 3, w, rows, ldw, qkv, m, h, h, qd + 2 * kd, KVR_LINEAR_CONCAT, nullptr, 0,
-                                 gws, gwb, dt, stream));
+        KVR_TRY(linear_multi(normed, 3, w, rows, ldw, qkv, m, h, h, qd + 2 * kd, KVR_LINEAR_CONCAT, nullptr, 0, gws,
+                             gwb, dt, stream, /*reduce=*/false, &qkv_splits));
         qp = qkv;
         kp = qkv + static_cast<int64_t>(qd) * 2;
         vp = qkv + static_cast<int64_t>(qd + kd) * 2;
@@ -183,8 +190,16 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
     const int64_t* cv = L->cache_strides + 3;
     const int64_t rs[18] = {dim, q_ld, 1, dim, qd, 1, dim, k_ld, 1, dim, v_ld, 1,
                             ck[0], ck[1], ck[2], cv[0], cv[1], cv[2]};
-    KVR_TRY(kvr_rope_scatter_kv(qp, q_rot, kp, vp, L->cache_k, L->cache_v, d->cos, d->sin, d->positions, m,
-                                d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, dt, stream));
+    if (qkv_splits > 1) {  // q/k/v straight from the projection's partials
+        const int64_t part_col[3] = {0, qd, qd + kd};
+        PartialSums p = gemm_partials;
+        p.splits = qkv_splits;
+        KVR_TRY(rope_scatter_partials(p, part_col, q_rot, L->cache_k, L->cache_v, d->cos, d->sin, d->positions, m,
+                                      d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, dt, stream));
+    } else {
+        KVR_TRY(kvr_rope_scatter_kv(qp, q_rot, kp, vp, L->cache_k, L->cache_v, d->cos, d->sin, d->positions, m,
+                                    d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, dt, stream));
+    }
 
     // packed causal attention over the whole cache; output in [rows][q_heads * dim]
     const int64_t as[12] = {dim, qd, 1, ck[0], ck[1], ck[2], cv[0], cv[1], cv[2], dim, qd, 1};
@@ -192,9 +207,24 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
                                         d->kv_heads, d->n_keys, dim, d->scale, as, d->schedule, d->schedule_len,
                                         d->host_schedule, d->attn_workspace, d->attn_workspace_bytes, dt, stream));
 
-    // o projection, residual add + post-attention RMSNorm
-    KVR_TRY(kvr_linear(attn, L->w_o, o_out, m, h, qd, qd, L->ld_o, h, gws, gwb, dt, stream));
-    KVR_TRY(kvr_rms_norm(o_out, hidden, hidden2, normed, L->post_norm, m, h, rows_h, L->eps_post, dt, stream));
+    // o projection, residual add + post-attention RMSNorm (from the partials when split)
+    {
+        const void* w[1] = {L->w_o};
+        const int32_t rows[1] = {h};
+        const int64_t ldw[1] = {L->ld_o};
+        int32_t splits = 1;
+        KVR_TRY(linear_multi(attn, 1, w, rows, ldw, o_out, m, qd, qd, h, KVR_LINEAR_CONCAT, nullptr, 0, gws, gwb, dt,
+                             stream, /*reduce=*/!norm_partials, &splits));
+        if (norm_partials && splits > 1) {
+            PartialSums p = gemm_partials;
+            p.splits = splits;
+            KVR_TRY(rms_norm_partials(p, hidden, hidden2, normed, L->post_norm, m, h, rows_h, L->eps_post, dt,
+                                      stream));
+        } else {
+            KVR_TRY(kvr_rms_norm(o_out, hidden, hidden2, normed, L->post_norm, m, h, rows_h, L->eps_post, dt,
+                                 stream));
+        }
+    }
 
     // MLP: SiLU-gated gate/up, then down with the residual add, written over `hidden`
     const void* gw[2] = {L->w_gate, L->w_up};
@@ -205,9 +235,44 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
     const void* dw[1] = {L->w_down};
     const int32_t dr[1] = {h};
     const int64_t dl[1] = {L->ld_down};
-    KVR_TRY(kvr_linear_multi(act, 1, dw, dr, dl, hidden, m, in, in, h, KVR_LINEAR_RESIDUAL, hidden2, h, gws, gwb, dt,
-                             stream));
+    if (!L->next_norm) {
+        KVR_TRY(kvr_linear_multi(act, 1, dw, dr, dl, hidden, m, in, in, h, KVR_LINEAR_RESIDUAL, hidden2, h, gws, gwb,
+                                 dt, stream));
+    } else {  // ... and the next layer's input norm into `normed`
+        int32_t splits = 1;
+        if (norm_partials) {
+            KVR_TRY(linear_multi(act, 1, dw, dr, dl, o_out, m, in, in, h, KVR_LINEAR_CONCAT, nullptr, 0, gws, gwb, dt,
+                                 stream, /*reduce=*/false, &splits));
+        }
+        if (norm_partials && splits > 1) {
+            PartialSums p = gemm_partials;
+            p.splits = splits;
+            KVR_TRY(rms_norm_partials(p, hidden2, hidden, normed, L->next_norm, m, h, rows_h, L->eps_next, dt,
+                                      stream));
+        } else {
+            if (!norm_partials)
+                KVR_TRY(kvr_linear_multi(act, 1, dw, dr, dl, hidden, m, in, in, h, KVR_LINEAR_RESIDUAL, hidden2, h,
+                                         gws, gwb, dt, stream));
+            else  // one split: the projection was written to o_out
+                KVR_TRY(kvr_rms_norm(o_out, hidden2, hidden, normed, L->next_norm, m, h, rows_h, L->eps_next, dt,
+                                     stream));
+            if (!norm_partials)
+                KVR_TRY(kvr_rms_norm(hidden, nullptr, nullptr, normed, L->next_norm, m, h, rows_h, L->eps_next, dt,
+                                     stream));
+        }
+    }
 #undef KVR_TRY
+    return KVR_OK;
+}
+
+extern "C" int kvr_decoder_forward(const kvr_layer_desc* layers, int32_t n_layers, const kvr_refresh_desc* d,
+                                   void* hidden, void* stream) {
+    if (n_layers < 0) return KVR_E_INVALID_ARGUMENT;
+    if (n_layers > 0 && !layers) return KVR_E_NULL_POINTER;
+    for (int32_t i = 0; i < n_layers; ++i) {
+        const int st = kvr_decoder_layer(layers + i, d, hidden, stream);
+        if (st < 0) return st;
+    }
     return KVR_OK;
 }
 

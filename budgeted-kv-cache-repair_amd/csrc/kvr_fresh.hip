@@ -36,6 +36,8 @@ struct FreshArgs {
     int32_t n_q_heads;
     int32_t n_kv_heads;
     int32_t head_dim;
+    PartialSums src;      // src.base != nullptr: q / fresh K / fresh V come from split-K partial sums
+    int64_t part_col[3];  // their first column in the concatenated projection
 };
 
 // One rotated pair with distinct cos/sin for the two halves (the rotary
@@ -92,20 +94,38 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
     const int64_t lo_off = static_cast<int64_t>(c) * EPV;
     const int64_t hi_off = lo_off + half;
 
-    const char* src;
+    const char* src = nullptr;
     char* dst;
     if (part == 0) {
-        src = a.q + (h * a.qs[0] + r * a.qs[1]) * E::size;
+        if (!a.src.base) src = a.q + (h * a.qs[0] + r * a.qs[1]) * E::size;
         dst = a.q_out + (h * a.qos[0] + r * a.qos[1]) * E::size;
     } else {
         const int kv = part - 1;
         const int64_t pos = a.positions[r];
         if (pos < 0 || pos >= a.n_keys) return;
-        src = a.fresh[kv] + (h * a.fs[kv][0] + r * a.fs[kv][1]) * E::size;
+        if (!a.src.base) src = a.fresh[kv] + (h * a.fs[kv][0] + r * a.fs[kv][1]) * E::size;
         dst = a.out[kv] + (h * a.os[kv][0] + pos * a.os[kv][1]) * E::size;
     }
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(src + lo_off * E::size);
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(src + hi_off * E::size);
+    u32x4 lo, hi;
+    if constexpr (EPV == 8) {
+        if (a.src.base) {  // the projection's output, rounded as its reduce kernel rounds it
+            const int64_t col = a.part_col[part] + h * a.head_dim;
+            float sums[8];
+            bits b[EPV];
+            partial_sum8(a.src, r, col + lo_off, sums);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sums[e]);
+            __builtin_memcpy(&lo, b, 16);
+            partial_sum8(a.src, r, col + hi_off, sums);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sums[e]);
+            __builtin_memcpy(&hi, b, 16);
+        }
+    }
+    if (src) {
+        lo = *reinterpret_cast<const u32x4*>(src + lo_off * E::size);
+        hi = *reinterpret_cast<const u32x4*>(src + hi_off * E::size);
+    }
     if (part == 2) {  // values: bit copy
         *reinterpret_cast<u32x4*>(dst + lo_off * E::size) = lo;
         *reinterpret_cast<u32x4*>(dst + hi_off * E::size) = hi;
@@ -153,11 +173,11 @@ __global__ void __launch_bounds__(kThreads) fresh_scalar_kernel(FreshArgs a) {
     int part;
     int64_t h, r;
     decode_row(a, g, part, h, r);
-    const bits* src;
+    const bits* src = nullptr;
     bits* dst;
-    int64_t sd, dd;
+    int64_t sd = 1, dd;
     if (part == 0) {
-        src = reinterpret_cast<const bits*>(a.q) + h * a.qs[0] + r * a.qs[1];
+        if (!a.src.base) src = reinterpret_cast<const bits*>(a.q) + h * a.qs[0] + r * a.qs[1];
         dst = reinterpret_cast<bits*>(a.q_out) + h * a.qos[0] + r * a.qos[1];
         sd = a.qs[2];
         dd = a.qos[2];
@@ -165,12 +185,20 @@ __global__ void __launch_bounds__(kThreads) fresh_scalar_kernel(FreshArgs a) {
         const int kv = part - 1;
         const int64_t pos = a.positions[r];
         if (pos < 0 || pos >= a.n_keys) return;
-        src = reinterpret_cast<const bits*>(a.fresh[kv]) + h * a.fs[kv][0] + r * a.fs[kv][1];
+        if (!a.src.base) src = reinterpret_cast<const bits*>(a.fresh[kv]) + h * a.fs[kv][0] + r * a.fs[kv][1];
         dst = reinterpret_cast<bits*>(a.out[kv]) + h * a.os[kv][0] + pos * a.os[kv][1];
         sd = a.fs[kv][2];
         dd = a.os[kv][2];
     }
-    const bits lo = src[i * sd], hi = src[(i + half) * sd];
+    bits lo, hi;
+    if (src) {
+        lo = src[i * sd];
+        hi = src[(i + half) * sd];
+    } else {  // the projection's output, rounded as its reduce kernel rounds it
+        const int64_t col = a.part_col[part] + h * a.head_dim;
+        lo = E::from_float(partial_sum1(a.src, r, col + i));
+        hi = E::from_float(partial_sum1(a.src, r, col + i + half));
+    }
     if (part == 2) {
         dst[i * dd] = lo;
         dst[(i + half) * dd] = hi;
@@ -207,11 +235,14 @@ int launch(const FreshArgs& a, bool vec, int tpr_log2, hipStream_t s) {
 }  // namespace
 }  // namespace kvr
 
-extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh_k, const void* fresh_v, void* out_k,
-                                   void* out_v, const void* cos, const void* sin, const int64_t* positions,
-                                   int64_t n_sel, int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys,
-                                   int32_t head_dim, const int64_t strides[18], const int64_t cs_strides[4],
-                                   int32_t dtype, void* stream) {
+namespace kvr {
+namespace {
+
+int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const void* fresh_v, void* out_k, void* out_v,
+                      const void* cos, const void* sin, const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
+                      int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, const int64_t strides[18],
+                      const int64_t cs_strides[4], int32_t dtype, void* stream, const PartialSums* partial,
+                      const int64_t* part_col) {
     using namespace kvr;
     const int esize = dtype_size(dtype);
     if (esize == 0) return KVR_E_UNSUPPORTED_DTYPE;
@@ -223,8 +254,13 @@ extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh
     for (int i = 0; i < 4; ++i)
         if (cs_strides[i] < 0 || (i % 2 == 1 && cs_strides[i] == 0)) return KVR_E_BAD_STRIDE;
     if (n_sel == 0) return KVR_OK;
-    if (!q || !q_out || !fresh_k || !fresh_v || !out_k || !out_v || !cos || !sin || !positions)
+    if (partial) {
+        if (!partial->base || partial->splits < 1 || !part_col) return KVR_E_NULL_POINTER;
+        if (dtype_size(dtype) != 2 || n_sel > kPartialTileRows) return KVR_E_UNSUPPORTED_SHAPE;
+    } else if (!q || !fresh_k || !fresh_v) {
         return KVR_E_NULL_POINTER;
+    }
+    if (!q_out || !out_k || !out_v || !cos || !sin || !positions) return KVR_E_NULL_POINTER;
 
     FreshArgs a;
     a.q = static_cast<const char*>(q);
@@ -253,6 +289,8 @@ extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh
     a.n_q_heads = n_q_heads;
     a.n_kv_heads = n_kv_heads;
     a.head_dim = head_dim;
+    a.src = partial ? *partial : PartialSums{};
+    for (int i = 0; i < 3; ++i) a.part_col[i] = part_col ? part_col[i] : 0;
 
     // Vector path: each half splits into a power-of-two number of 16-byte chunks.
     const int64_t half_bytes = static_cast<int64_t>(head_dim / 2) * esize;
@@ -278,4 +316,25 @@ extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh
         case KVR_DTYPE_F16: return launch<f16_t>(a, vec, tpr_log2, s);
         default: return launch<bf16_t>(a, vec, tpr_log2, s);
     }
+}
+
+}  // namespace
+
+int rope_scatter_partials(const PartialSums& src, const int64_t part_col[3], void* q_out, void* out_k, void* out_v,
+                          const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,
+                          int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
+                          const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream) {
+    return rope_scatter_impl(nullptr, q_out, nullptr, nullptr, out_k, out_v, cos, sin, positions, n_sel, n_q_heads,
+                             n_kv_heads, n_keys, head_dim, strides, cs_strides, dtype, stream, &src, part_col);
+}
+
+}  // namespace kvr
+
+extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh_k, const void* fresh_v, void* out_k,
+                                   void* out_v, const void* cos, const void* sin, const int64_t* positions,
+                                   int64_t n_sel, int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys,
+                                   int32_t head_dim, const int64_t strides[18], const int64_t cs_strides[4],
+                                   int32_t dtype, void* stream) {
+    return kvr::rope_scatter_impl(q, q_out, fresh_k, fresh_v, out_k, out_v, cos, sin, positions, n_sel, n_q_heads,
+                                  n_kv_heads, n_keys, head_dim, strides, cs_strides, dtype, stream, nullptr, nullptr);
 }

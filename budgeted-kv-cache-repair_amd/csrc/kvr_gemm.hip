@@ -366,23 +366,23 @@ bool allow_lds(F fn, size_t bytes) {
 }
 
 template <typename T, int MT>
-int launch_mt(const GemmArgs& a, hipStream_t s) {
+int launch_mt(const GemmArgs& a, hipStream_t s, bool reduce) {
     static const bool ok = allow_lds(skinny_gemm_kernel<T, MT>, kLdsBytes);
     if (!ok) return KVR_E_LAUNCH_FAILED;
     const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, kTileN)), static_cast<unsigned>(a.splits));
     skinny_gemm_kernel<T, MT><<<grid, kGemmThreads, kLdsBytes, s>>>(a);
-    if (a.splits > 1)
+    if (a.splits > 1 && reduce)
         splitk_reduce_kernel<T><<<dim3(grid.x, static_cast<unsigned>(MT)), kReduceThreads, 0, s>>>(a);
     return launch_status();
 }
 
 template <typename T>
-int launch(const GemmArgs& a, hipStream_t s) {
+int launch(const GemmArgs& a, hipStream_t s, bool reduce) {
     switch ((a.m + 15) / 16) {
-        case 1: return launch_mt<T, 1>(a, s);
-        case 2: return launch_mt<T, 2>(a, s);
-        case 3: return launch_mt<T, 3>(a, s);
-        default: return launch_mt<T, 4>(a, s);
+        case 1: return launch_mt<T, 1>(a, s, reduce);
+        case 2: return launch_mt<T, 2>(a, s, reduce);
+        case 3: return launch_mt<T, 3>(a, s, reduce);
+        default: return launch_mt<T, 4>(a, s, reduce);
     }
 }
 
@@ -425,10 +425,16 @@ extern "C" int64_t kvr_linear_workspace_bytes(int32_t m, int32_t rows, int32_t k
     return ceil_div(rows, kTileN) * splits * static_cast<int64_t>(kRowsMax) * kTileN * 4;
 }
 
-extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
-                                const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy,
-                                int32_t epilogue, const void* residual, int64_t ldr, void* workspace,
-                                int64_t workspace_bytes, int32_t dtype, void* stream) {
+namespace kvr {
+
+// kvr_linear_multi with an option to stop before the split-K reduction: with
+// reduce == false and more than one split, y is left unwritten and the fp32
+// partials [ceil(rows / 64)][splits][64][64] stay in `workspace` for a fused
+// consumer (*splits_out = splits; 1 means y was written directly).
+int linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows, const int64_t* ldw,
+                 void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy, int32_t epilogue, const void* residual,
+                 int64_t ldr, void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream, bool reduce,
+                 int32_t* splits_out) {
     if (dtype != KVR_DTYPE_BF16 && dtype != KVR_DTYPE_F16) return KVR_E_UNSUPPORTED_DTYPE;
     if (n_weights < 1 || n_weights > 3 || !w || !rows || !ldw) return KVR_E_INVALID_ARGUMENT;
     if (epilogue != KVR_LINEAR_CONCAT && epilogue != KVR_LINEAR_SILU_GATE && epilogue != KVR_LINEAR_RESIDUAL)
@@ -481,8 +487,20 @@ extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* co
     const Split sp = plan_split(static_cast<int32_t>(total), k);
     a.splits = sp.splits;
     a.slice = sp.slice;
+    if (!reduce && (gated || a.res)) return KVR_E_INVALID_ARGUMENT;  // partial consumers take plain sums
+    if (splits_out) *splits_out = sp.splits;
     hipStream_t s = as_stream(stream);
-    return dtype == KVR_DTYPE_BF16 ? launch<bf16_t>(a, s) : launch<f16_t>(a, s);
+    return dtype == KVR_DTYPE_BF16 ? launch<bf16_t>(a, s, reduce) : launch<f16_t>(a, s, reduce);
+}
+
+}  // namespace kvr
+
+extern "C" int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
+                                const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy,
+                                int32_t epilogue, const void* residual, int64_t ldr, void* workspace,
+                                int64_t workspace_bytes, int32_t dtype, void* stream) {
+    return linear_multi(x, n_weights, w, rows, ldw, y, m, k, ldx, ldy, epilogue, residual, ldr, workspace,
+                        workspace_bytes, dtype, stream, true, nullptr);
 }
 
 extern "C" int kvr_linear(const void* x, const void* w, void* y, int32_t m, int32_t n, int32_t k, int64_t ldx,

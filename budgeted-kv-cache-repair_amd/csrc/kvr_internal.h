@@ -67,6 +67,93 @@ __device__ inline float silu_gate(float g, float u) {
     return act * u;
 }
 
+// Split-K partial tiles left by linear_multi(..., reduce = false): fp32
+// [ceil(cols / 64)][splits][64 rows][64 cols]; element (row, col) of the
+// projection is the sum over s of tile(col / 64)[s][row][col % 64], added in
+// split order and rounded to the dtype -- exactly what the reduce kernel writes.
+struct PartialSums {
+    const float* base = nullptr;  // nullptr: read the dtype tensor instead
+    int32_t splits = 0;
+};
+constexpr int kPartialTileCols = 64;
+constexpr int kPartialTileRows = 64;
+
+int linear_multi(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows, const int64_t* ldw,
+                 void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy, int32_t epilogue, const void* residual,
+                 int64_t ldr, void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream, bool reduce,
+                 int32_t* splits_out);
+
+// Eight consecutive columns [col, col + 8) of `row` (col % 8 == 0) summed over
+// the splits in order, as fp32 (not yet rounded). The loads of up to
+// kPartialBatch splits are issued before the adds, so a few splits cost one
+// memory round trip, not one per split.
+constexpr int kPartialBatch = 8;
+
+__device__ inline void partial_sum8(const PartialSums& p, int64_t row, int64_t col, float out[8]) {
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    const int64_t tile = col / kPartialTileCols;
+    const float* at = p.base + (tile * p.splits * kPartialTileRows + row) * kPartialTileCols + col % kPartialTileCols;
+    const int64_t step = static_cast<int64_t>(kPartialTileRows) * kPartialTileCols;
+    f32x4_t lo = *reinterpret_cast<const f32x4_t*>(at);
+    f32x4_t hi = *reinterpret_cast<const f32x4_t*>(at + 4);
+    for (int s0 = 1; s0 < p.splits; s0 += kPartialBatch) {
+        f32x4_t l[kPartialBatch], h[kPartialBatch];
+#pragma unroll
+        for (int b = 0; b < kPartialBatch; ++b) {
+            if (s0 + b < p.splits) {
+                l[b] = *reinterpret_cast<const f32x4_t*>(at + (s0 + b) * step);
+                h[b] = *reinterpret_cast<const f32x4_t*>(at + (s0 + b) * step + 4);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kPartialBatch; ++b) {
+            if (s0 + b < p.splits) {
+                lo += l[b];
+                hi += h[b];
+            }
+        }
+    }
+    for (int e = 0; e < 4; ++e) {
+        out[e] = lo[e];
+        out[4 + e] = hi[e];
+    }
+}
+
+// One column of `row` summed over the splits in order (fp32, not yet rounded).
+__device__ inline float partial_sum1(const PartialSums& p, int64_t row, int64_t col) {
+    const int64_t tile = col / kPartialTileCols;
+    const float* at = p.base + (tile * p.splits * kPartialTileRows + row) * kPartialTileCols + col % kPartialTileCols;
+    const int64_t step = static_cast<int64_t>(kPartialTileRows) * kPartialTileCols;
+    float sum = at[0];
+    for (int s0 = 1; s0 < p.splits; s0 += kPartialBatch) {
+        float v[kPartialBatch];
+#pragma unroll
+        for (int b = 0; b < kPartialBatch; ++b)
+            if (s0 + b < p.splits) v[b] = at[(s0 + b) * step];
+#pragma unroll
+        for (int b = 0; b < kPartialBatch; ++b)
+            if (s0 + b < p.splits) sum += v[b];
+    }
+    return sum;
+}
+
+// kvr_rms_norm with x given as split-K partial sums (rounded to the dtype as the
+// reduce kernel rounds them). Only the vector path; rms_norm_partials_ok says
+// whether it applies to `hidden` columns of `dtype`.
+bool rms_norm_partials_ok(int32_t hidden, int32_t dtype);
+int rms_norm_partials(const PartialSums& x, const void* residual, void* residual_out, void* out, const void* weight,
+                      int64_t rows, int32_t hidden, const int64_t row_strides[4], float eps, int32_t dtype,
+                      void* stream);
+
+// kvr_rope_scatter_kv with q, fresh K and fresh V given as split-K partial sums
+// of one concatenated projection (columns part_col[0] + h*head_dim + i for
+// query head h, part_col[1] + ... for K, part_col[2] + ... for V). The q /
+// fresh-K / fresh-V strides of `strides` are ignored.
+int rope_scatter_partials(const PartialSums& src, const int64_t part_col[3], void* q_out, void* out_k, void* out_v,
+                          const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,
+                          int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
+                          const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -33,6 +33,7 @@ struct NormArgs {
     int64_t x_stride, r_stride, ro_stride, o_stride;  // row strides (elements); dims are unit-stride
     int32_t hidden;
     float eps;
+    PartialSums px;        // px.base != nullptr: x comes from split-K partial sums (vector path only)
 };
 
 template <typename T>
@@ -98,7 +99,7 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, 
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (kNormThreads >> tpr_log2) + (threadIdx.x >> tpr_log2);
     const bool live = row < a.rows;
     const int nvec = a.hidden / V;
-    const char* x = a.x + row * a.x_stride * E::size;
+    const char* x = a.x ? a.x + row * a.x_stride * E::size : nullptr;
     const char* res = a.residual ? a.residual + row * a.r_stride * E::size : nullptr;
     char* res_out = a.residual ? a.residual_out + row * a.ro_stride * E::size : nullptr;
     char* out = a.out + row * a.o_stride * E::size;
@@ -109,9 +110,21 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, 
     for (int k = 0; k < NV; ++k) {
         const int j = t + k * tpr;
         if (!live || j >= nvec) continue;
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(j) * 16);
         bits xb[V];
-        __builtin_memcpy(xb, &xv, 16);
+        bool from_partials = false;
+        if constexpr (V == 8) {
+            if (a.px.base) {  // the projection's output element, rounded as its reduce kernel rounds it
+                float sums[8];
+                partial_sum8(a.px, row, static_cast<int64_t>(j) * 8, sums);
+#pragma unroll
+                for (int e = 0; e < V; ++e) xb[e] = E::from_float(sums[e]);
+                from_partials = true;
+            }
+        }
+        if (!from_partials) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(j) * 16);
+            __builtin_memcpy(xb, &xv, 16);
+        }
         if (res) {
             const u32x4 rv = *reinterpret_cast<const u32x4*>(res + static_cast<int64_t>(j) * 16);
             bits rb[V], sb[V];
@@ -195,7 +208,7 @@ __global__ void __launch_bounds__(kEltThreads) silu_mul_vec_kernel(const char* g
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <typename T>
-int launch_norm(const NormArgs& a, hipStream_t s) {
+int launch_norm(const NormArgs& a, hipStream_t s, bool require_vec = false) {
     constexpr int V = 16 / elem<T>::size;
     const int64_t nvec = a.hidden / V;
     bool vec = a.hidden % V == 0 && a.x_stride % V == 0 && a.o_stride % V == 0 && aligned16(a.x) &&
@@ -217,6 +230,7 @@ int launch_norm(const NormArgs& a, hipStream_t s) {
         }
         return launch_status();
     }
+    if (require_vec) return KVR_E_UNSUPPORTED_SHAPE;
     const int64_t blocks = ceil_div(a.rows, kNormThreads / 64);
     rms_norm_kernel<T><<<static_cast<unsigned>(blocks), kNormThreads, 0, s>>>(a);
     return launch_status();
@@ -264,6 +278,7 @@ extern "C" int kvr_rms_norm(const void* x, const void* residual, void* residual_
     a.o_stride = row_strides[3];
     a.hidden = hidden;
     a.eps = eps;
+    a.px = PartialSums{};
     hipStream_t s = as_stream(stream);
     switch (dtype) {
         case KVR_DTYPE_F32: return launch_norm<f32_t>(a, s);
@@ -271,6 +286,39 @@ extern "C" int kvr_rms_norm(const void* x, const void* residual, void* residual_
         default: return launch_norm<bf16_t>(a, s);
     }
 }
+
+namespace kvr {
+
+bool rms_norm_partials_ok(int32_t hidden, int32_t dtype) {
+    return (dtype == KVR_DTYPE_BF16 || dtype == KVR_DTYPE_F16) && hidden > 0 && hidden % 8 == 0 &&
+           hidden / 8 <= 256 * kMaxVec;
+}
+
+int rms_norm_partials(const PartialSums& x, const void* residual, void* residual_out, void* out, const void* weight,
+                      int64_t rows, int32_t hidden, const int64_t row_strides[4], float eps, int32_t dtype,
+                      void* stream) {
+    if (!rms_norm_partials_ok(hidden, dtype)) return KVR_E_UNSUPPORTED_SHAPE;
+    if (!x.base || x.splits < 1 || !out || !weight || (residual && !residual_out)) return KVR_E_NULL_POINTER;
+    if (rows <= 0 || rows > kPartialTileRows) return KVR_E_UNSUPPORTED_SHAPE;
+    NormArgs a;
+    a.x = nullptr;
+    a.residual = static_cast<const char*>(residual);
+    a.residual_out = static_cast<char*>(residual_out);
+    a.out = static_cast<char*>(out);
+    a.weight = static_cast<const char*>(weight);
+    a.rows = rows;
+    a.x_stride = hidden;
+    a.r_stride = row_strides[1];
+    a.ro_stride = row_strides[2];
+    a.o_stride = row_strides[3];
+    a.hidden = hidden;
+    a.eps = eps;
+    a.px = x;
+    hipStream_t s = as_stream(stream);
+    return dtype == KVR_DTYPE_F16 ? launch_norm<f16_t>(a, s, true) : launch_norm<bf16_t>(a, s, true);
+}
+
+}  // namespace kvr
 
 extern "C" int kvr_silu_mul(const void* gate, const void* up, void* out, int64_t n, int32_t dtype, void* stream) {
     using namespace kvr;

@@ -39,6 +39,7 @@ class LayerDesc(ctypes.Structure):
         "input_norm", "post_norm", "q_norm", "k_norm", "w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down")] + \
         [(name, ctypes.c_int64) for name in ("ld_q", "ld_k", "ld_v", "ld_o", "ld_gate", "ld_up", "ld_down")] + \
         [(name, ctypes.c_float) for name in ("eps_input", "eps_post", "eps_q", "eps_k")] + \
+        [("next_norm", ctypes.c_void_p), ("eps_next", ctypes.c_float), ("input_normed", ctypes.c_int32)] + \
         [("cache_k", ctypes.c_void_p), ("cache_v", ctypes.c_void_p), ("cache_strides", ctypes.c_int64 * 6)]
 
 
@@ -100,6 +101,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.kvr_decoder_gemm_workspace_bytes.restype = ctypes.c_int64
     lib.kvr_decoder_layer.argtypes = [_desc_p, _refresh_p, _vp, _vp]
     lib.kvr_decoder_layer.restype = ctypes.c_int
+    lib.kvr_decoder_forward.argtypes = [_desc_p, ctypes.c_int32, _refresh_p, _vp, _vp]
+    lib.kvr_decoder_forward.restype = ctypes.c_int
     lib.kvr_decoder_desc_sizes.argtypes = [_i64p]
     lib.kvr_decoder_desc_sizes.restype = None
     lib.kvr_attention_schedule.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,

@@ -103,12 +103,20 @@ class IndexedPlan:
         # inference mode so every launch can reject in-place mutation with a
         # host-side check instead of a device read.
         with torch.cuda.device(device), torch.inference_mode(False):
-            positions = torch.tensor(self.positions, device=device, dtype=torch.int64)
-            full = torch.tensor(self.full_prefix_tiles, device=device, dtype=torch.int64)
-            total = torch.tensor(self.total_tiles, device=device, dtype=torch.int64)
+            positions = _upload(torch.tensor(self.positions, dtype=torch.int64), device)
+            full = _upload(torch.tensor(self.full_prefix_tiles, dtype=torch.int64), device)
+            total = _upload(torch.tensor(self.total_tiles, dtype=torch.int64), device)
         tensors = (positions, full, total)
         seal = (id(self), tuple(id(t) for t in tensors), tuple(t._version for t in tensors))
         return DeviceIndexedPlan(self, positions, full, total, seal)
+
+
+def _upload(host: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Copy a small host tensor to ``device`` on the current stream without
+    blocking the host: staged through pinned memory (whose block the caching
+    host allocator keeps until the copy has run), so the refresh's kernels can
+    be enqueued while earlier work is still running."""
+    return host.pin_memory().to(device, non_blocking=True)
 
 
 @dataclass(frozen=True)
@@ -158,7 +166,7 @@ class DeviceIndexedPlan:
         host = (ctypes.c_int32 * int(need))()
         _native.check(int(lib.kvr_attention_schedule(*args, host, int(need))), "kvr_attention_schedule")
         with torch.cuda.device(self.device), torch.inference_mode(False):
-            dev = torch.tensor(list(host), dtype=torch.int32, device=self.device)
+            dev = _upload(torch.frombuffer(host, dtype=torch.int32), self.device)
         self._schedules[key] = (host, dev, dev._version)
         return host, dev
 

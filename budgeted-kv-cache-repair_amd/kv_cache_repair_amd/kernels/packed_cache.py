@@ -50,7 +50,6 @@ class _PackedContext:
     backend: str
     device_plan: Any = None
     launcher: Any = None
-    native: Any = None
 
 
 @dataclass
@@ -214,32 +213,53 @@ def _plain_linear(module) -> bool:
             and _projection.supported_weight(module.weight))
 
 
+def _layer_modules(layer):
+    """(projection modules, norm modules) of a Llama/Qwen3 decoder layer, read
+    through the `_modules` dicts (plain dict lookups: this runs per layer and
+    per refresh)."""
+    attention, mlp = layer._modules["self_attn"], layer._modules["mlp"]
+    am, mm = attention._modules, mlp._modules
+    projections = (am["q_proj"], am["k_proj"], am["v_proj"], am["o_proj"], mm["gate_proj"], mm["up_proj"],
+                   mm["down_proj"])
+    norms = [layer._modules["input_layernorm"], layer._modules["post_attention_layernorm"]]
+    if am.get("q_norm") is not None:
+        norms += [am["q_norm"], am["k_norm"]]
+    return projections, norms
+
+
+def _plans_key(projections, norms) -> tuple:
+    """Identity of everything a layer's plans point at: module objects, weight
+    tensors and their storage, and the projections' (absent) biases."""
+    key = []
+    for m in (*projections, *norms):
+        params = m.__dict__["_parameters"]
+        w = params.get("weight")
+        key += (id(m), id(w), w.data_ptr() if isinstance(w, torch.Tensor) else 0, params.get("bias") is None)
+    return tuple(key)
+
+
 def _layer_plans(layer) -> _LayerPlans | None:
     """Plans for ``layer`` (one of the caller's decoder layers), cached per layer
-    and rebuilt when a weight's storage moves; None when any projection has a
-    bias, is not a plain fp16/bf16 nn.Linear, or the MLP activation is not SiLU."""
-    attention, mlp = layer.self_attn, layer.mlp
-    modules = (attention.q_proj, attention.k_proj, attention.v_proj, attention.o_proj, mlp.gate_proj,
-               mlp.up_proj, mlp.down_proj)
-    if not all(_plain_linear(m) for m in modules) or not isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
-        return None
-    weights = [m.weight for m in modules]
-    if len({(w.dtype, w.device) for w in weights}) != 1 or weights[4].shape != weights[5].shape:
-        return None
-    norms = [layer.input_layernorm, layer.post_attention_layernorm]
-    if getattr(attention, "q_norm", None) is not None:
-        norms += [attention.q_norm, attention.k_norm]
-    pointers = tuple(int(w.data_ptr()) for w in weights) + tuple(
-        int(n.weight.data_ptr()) if isinstance(getattr(n, "weight", None), torch.Tensor) else 0 for n in norms)
+    and rebuilt when a module, weight or weight storage changes; None when any
+    projection has a bias, is not a plain fp16/bf16 nn.Linear, or the MLP
+    activation is not SiLU."""
+    projections, norms = _layer_modules(layer)
+    key = _plans_key(projections, norms)
     with _PLAN_LOCK:
         cached = _PLAN_CACHE.get(layer)
-        if cached is not None and cached.pointers == pointers:
-            return cached
+    if cached is not None and cached.pointers == key:
+        return cached
+    mlp = layer._modules["mlp"]
+    if not all(_plain_linear(m) for m in projections) or not isinstance(mlp.act_fn, _SILU_ACTIVATIONS):
+        return None
+    weights = [m.weight for m in projections]
+    if len({(w.dtype, w.device) for w in weights}) != 1 or weights[4].shape != weights[5].shape:
+        return None
     q, k, v, o, gate, up, down = weights
     plan = _projection.ProjectionPlan
-    separate = getattr(attention, "q_norm", None) is not None
+    separate = len(norms) > 2
     plans = _LayerPlans(
-        pointers=pointers, qkv=None if separate else plan([q, k, v]), q=plan([q]) if separate else None,
+        pointers=key, qkv=None if separate else plan([q, k, v]), q=plan([q]) if separate else None,
         k=plan([k]) if separate else None, v=plan([v]) if separate else None, o=plan([o]),
         gate_up=plan([gate, up], _projection.SILU_GATE), down=plan([down]), q_cols=int(q.shape[0]),
         k_cols=int(k.shape[0]), desc=_layer_desc(layer, weights, norms))
@@ -350,43 +370,6 @@ class _NativeForward:
         self.tables = (cos, sin)
 
 
-def _native_layer_forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
-                          use_cache=False, position_embeddings=None, sur_packed_context=None, **kwargs):
-    """Decoder layer of a packed shell as ONE kvr_decoder_layer call.
-
-    The same kernels, arguments and order as _fused_layer_forward with
-    projection plans plus _fused_attention_forward (bit-identical output), but
-    enqueued from C: input RMSNorm, q/k/v projection (+ Qwen3 q/k norms), RoPE of
-    the fresh rows + K/V scatter into this layer's cache, packed attention, o
-    projection, residual + post-attention RMSNorm, SiLU-gated gate/up, down +
-    residual. ``hidden_states`` ([1, B, hidden], contiguous) is updated in place.
-    """
-    context = sur_packed_context
-    if not isinstance(context, _PackedContext) or context.native is None:
-        raise RuntimeError("packed attention requires explicit per-call request context")
-    if attention_mask is not None:
-        raise RuntimeError("native dense mask construction must be bypassed for packed attention")
-    if not isinstance(past_key_values, Cache):
-        raise RuntimeError("packed fused epilogue requires the packed cache layers")
-    layer = past_key_values.layers[self.self_attn.layer_idx]
-    if not isinstance(layer, _PackedLayer) or layer.updated:
-        raise RuntimeError("native packed forward updated one layer more than once")
-    native = context.native
-    native.bind_tables(position_embeddings)
-    d = native.desc
-    if hidden_states.shape != (1, d.rows, d.hidden) or not hidden_states.is_contiguous() \
-            or _native.DTYPE_CODES.get(hidden_states.dtype) != d.dtype:
-        raise RuntimeError("packed native hidden-state geometry/dtype drifted")
-    desc = self._kvr_layer_desc
-    if desc.cache_k != layer.keys.data_ptr() or desc.cache_v != layer.values.data_ptr():
-        raise RuntimeError("packed native cache layer drifted")
-    status = _native.lib().kvr_decoder_layer(ctypes.byref(desc), ctypes.byref(d), hidden_states.data_ptr(),
-                                             native.stream)
-    _native.check(status, "kvr_decoder_layer")
-    layer.updated = True
-    return hidden_states
-
-
 def _fused_norm_forward(self, hidden_states):
     return _rms_norm(self, hidden_states)
 
@@ -452,15 +435,13 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     return (plans.o(attended) if plans is not None else self.o_proj(attended)), None
 
 
-def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True, plans=None, layer_descs=None):
+def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = True, plans=None):
     """Shallow module shells sharing parameters, with a private config naming the
     packed attention; the caller's modules and config are never modified. With
     ``fused_epilogue`` the attention shells run _fused_attention_forward; with
     ``fused_layers`` the layer and final-norm shells run their fused forwards.
     ``plans`` (one _LayerPlans or None per layer) routes the shells'
-    projections through kvr_linear_multi; ``layer_descs`` (one kvr_layer_desc
-    per layer, cache pointers filled) runs each layer shell as one
-    kvr_decoder_layer call."""
+    projections through kvr_linear_multi."""
     _register_attention()
     config = copy.deepcopy(base.config)
     config._attn_implementation = _ATTENTION_NAME
@@ -481,10 +462,7 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
             attention.forward = types.MethodType(_fused_attention_forward, attention)
             attention._kvr_fused_norms = fused_layers
             attention._kvr_plans = layer_plans
-        if layer_descs is not None:
-            layer.forward = types.MethodType(_native_layer_forward, layer)
-            layer._kvr_layer_desc = layer_descs[len(layers)]
-        elif fused_layers:
+        if fused_layers:
             layer.forward = types.MethodType(_fused_layer_forward, layer)
             layer._kvr_plans = layer_plans
         layer._modules["self_attn"] = attention
@@ -510,15 +488,21 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     if (type(model), type(base)) not in {(LlamaForCausalLM, LlamaModel), (Qwen3ForCausalLM, Qwen3Model)}:
         raise ValueError("packed executor requires exact native dense Llama or Qwen3 classes")
     device = edited_ids.device
-    # One walk over the module tree gathers every per-module condition below.
-    base_ids = {id(module) for module in base.modules()}
+    # One walk over the module tree (through the `_modules` dicts: a module
+    # reached twice is checked twice, which changes no outcome) gathers every
+    # per-module condition below.
     training = hooked = overridden = off_device = False
-    for module in model.modules():
-        in_base = id(module) in base_ids
-        training |= in_base and module.training
-        hooked |= getattr(module, "_hf_hook", None) is not None
-        overridden |= in_base and "forward" in module.__dict__
-        off_device |= any(p is not None and p.device != device for p in module._parameters.values())
+    stack = [(model, False)]
+    while stack:
+        module, in_base = stack.pop()
+        in_base = in_base or module is base
+        attrs = module.__dict__
+        training |= in_base and attrs["training"]
+        hooked |= attrs.get("_hf_hook") is not None
+        overridden |= in_base and "forward" in attrs
+        for p in attrs["_parameters"].values():
+            off_device |= p is not None and p.device != device
+        stack.extend((child, in_base) for child in attrs["_modules"].values() if child is not None)
     if model.training or base.training or training:
         raise ValueError("packed executor requires eval mode on all decoder modules")
     config = model.config
@@ -688,15 +672,44 @@ def _native_layers_for(native_layers, base, plans, fused_epilogue: bool, fused_l
 
 
 def _native_layer_descs(plans, output, layer_count):
-    """Per-refresh copies of the layers' descriptors with this cache's pointers."""
-    descs = []
+    """Per-refresh array of the layers' descriptors with this cache's pointers;
+    each layer but the last computes the next layer's input norm in its down
+    projection's reduction, and the next layer skips it."""
+    descs = (_native.LayerDesc * layer_count)()
     for i in range(layer_count):
         keys, values = layer_kv(output, i)
-        desc = _native.LayerDesc.from_buffer_copy(plans[i].desc)
+        descs[i] = plans[i].desc
+        desc = descs[i]
         desc.cache_k, desc.cache_v = keys.data_ptr(), values.data_ptr()
         desc.cache_strides[:] = (*_native.strides3(keys), *_native.strides3(values))
-        descs.append(desc)
+        if i + 1 < layer_count:
+            desc.next_norm, desc.eps_next = plans[i + 1].desc.input_norm, plans[i + 1].desc.eps_input
+        desc.input_normed = 1 if i > 0 else 0
     return descs
+
+
+def _native_refresh(base, launcher: _Launcher, plans, output, layer_count: int, edited_ids_t, positions) -> None:
+    """The packed forward as ONE kvr_decoder_forward call over all layers.
+
+    The model's own embedding and rotary modules make the selected rows' input
+    hidden states and cos/sin tables (as LlamaModel/Qwen3Model.forward does,
+    transformers 5.15.0 modeling_llama.py:377-398); then every decoder layer
+    runs as kvr_decoder_layer -- the same kernels with the same arguments as the
+    Python-dispatched fused shells, so the cache is bit-identical. The final
+    norm is skipped: the refresh consumes only the K/V the layers scatter.
+    """
+    first = base.layers[0]
+    native = _NativeForward(launcher, int(first.mlp.down_proj.weight.shape[0]),
+                            int(first.mlp.gate_proj.weight.shape[0]), float(first.self_attn.scaling))
+    descs = _native_layer_descs(plans, output, layer_count)
+    hidden = base.embed_tokens(edited_ids_t.index_select(1, positions)).contiguous()
+    native.bind_tables(base.rotary_emb(hidden, positions.unsqueeze(0)))
+    d = native.desc
+    if hidden.shape != (1, d.rows, d.hidden) or _native.DTYPE_CODES.get(hidden.dtype) != d.dtype:
+        raise RuntimeError("packed native hidden-state geometry/dtype drifted")
+    status = _native.lib().kvr_decoder_forward(descs, layer_count, ctypes.byref(d), hidden.data_ptr(),
+                                               native.stream)
+    _native.check(status, "kvr_decoder_forward")
 
 
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
@@ -709,16 +722,13 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
     positions = device_plan.positions
     key0 = layer_kv(output, 0)[0]
     launcher = _launcher(device_plan, base.config, key0)
-    context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan, launcher)
     plans = _projection_plans_for(base, fused_projections, key0.dtype, device_plan.selected_count)
     fused_layers = _fused_layers_for(fused_layers, key0.dtype)
-    descs = None
     if _native_layers_for(native_layers, base, plans, fused_epilogue, fused_layers):
-        first = base.layers[0]
-        context.native = _NativeForward(launcher, int(first.mlp.down_proj.weight.shape[0]),
-                                        int(first.mlp.gate_proj.weight.shape[0]), float(first.self_attn.scaling))
-        descs = _native_layer_descs(plans, output, layer_count)
-    native_view = _make_native_view(base, fused_epilogue, fused_layers, plans, descs)
+        _native_refresh(base, launcher, plans, output, layer_count, edited_ids_t, positions)
+        return
+    context = _PackedContext(positions, host_plan.logical_length, attention_backend, device_plan, launcher)
+    native_view = _make_native_view(base, fused_epilogue, fused_layers, plans)
     layers = [_PackedLayer(*layer_kv(output, i), context, writeback_backend) for i in range(layer_count)]
     cache = Cache(layers=layers)
     result = native_view(input_ids=edited_ids_t.index_select(1, positions), position_ids=positions.unsqueeze(0),
@@ -752,10 +762,10 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     one; fp32 accumulation rounded once, like the library GEMM up to summation
     order); the default (None) uses them for fp16/bf16 caches with at most 64
     selected rows, where the modules' GEMMs are weight-streaming bound.
-    ``native_layers`` runs each decoder layer as one kvr_decoder_layer call
-    (the same kernels in the same order, bit-identical to the Python-dispatched
-    fused path); the default (None) does so whenever the three fusions above
-    are all active.
+    ``native_layers`` runs the whole packed forward as one kvr_decoder_forward
+    call after the model's embedding and rotary modules (the same kernels with
+    the same arguments, bit-identical to the Python-dispatched fused shells);
+    the default (None) does so whenever the three fusions above are active.
     """
     _check_backends(attention_backend, writeback_backend)
     _check_ids(edited_ids_t)

@@ -231,6 +231,13 @@ int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, con
  * `hidden` ([rows][hidden], row-major) is read and overwritten in place with
  * the layer's output. No reference counterpart of its own: it replaces the
  * per-op Python dispatch of the executor's module shells.
+ *
+ * Split-K projections whose consumer can read the fp32 partials directly skip
+ * their reduce launch: the q/k/v sums feed the RoPE + scatter kernel, the o
+ * sums the residual add + post-attention norm, the down sums the residual add
+ * + the next layer's input norm (`next_norm`; the next call then sets
+ * `input_normed`). Those consumers round the sums exactly as the reduce kernel
+ * does, so the output stays bit-identical to the separate entry points.
  */
 typedef struct kvr_layer_desc {
     const void* input_norm;   /* [hidden] */
@@ -246,6 +253,9 @@ typedef struct kvr_layer_desc {
     const void* w_down;       /* [hidden][ld_down] */
     int64_t ld_q, ld_k, ld_v, ld_o, ld_gate, ld_up, ld_down;
     float eps_input, eps_post, eps_q, eps_k;
+    const void* next_norm;    /* [hidden] input RMSNorm weight of the next layer, or NULL: computed here, */
+    float eps_next;           /* fused into the down projection's reduce (its output replaces `hidden`'s */
+    int32_t input_normed;     /* norm); nonzero: the previous call already normalised `hidden` this way */
     void* cache_k;            /* this layer's [1, kv_heads, n_keys, head_dim] K and V */
     void* cache_v;
     int64_t cache_strides[6]; /* K {head, row, dim}, V {head, row, dim} in elements */
@@ -277,6 +287,9 @@ int64_t kvr_decoder_scratch_bytes(const kvr_refresh_desc* d);
 /* GEMM workspace bytes kvr_decoder_layer needs for `d`. */
 int64_t kvr_decoder_gemm_workspace_bytes(const kvr_refresh_desc* d);
 int kvr_decoder_layer(const kvr_layer_desc* layer, const kvr_refresh_desc* d, void* hidden, void* stream);
+/* kvr_decoder_layer over layers[0 .. n_layers) in order (the packed forward's layer loop). */
+int kvr_decoder_forward(const kvr_layer_desc* layers, int32_t n_layers, const kvr_refresh_desc* d, void* hidden,
+                        void* stream);
 /* sizeof(kvr_layer_desc), sizeof(kvr_refresh_desc): lets bindings check their struct mirrors. */
 void kvr_decoder_desc_sizes(int64_t sizes[2]);
 

@@ -26,7 +26,7 @@ def test_header_declares_the_entry_points():
         "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
         "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
         "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
-        "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_desc_sizes"])
+        "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -208,3 +208,6 @@ def test_decoder_layer_descriptors_validate_before_any_launch():
         assert lib.kvr_decoder_scratch_bytes(C.byref(bad)) == status, field
     layer = _native.LayerDesc()
     assert lib.kvr_decoder_layer(C.byref(layer), C.byref(d), None, None) == -5  # nothing bound
+    assert lib.kvr_decoder_forward(None, 0, C.byref(d), None, None) == 0
+    assert lib.kvr_decoder_forward(None, 2, C.byref(d), None, None) == -5
+    assert lib.kvr_decoder_forward(C.byref(layer), -1, C.byref(d), None, None) == -1
