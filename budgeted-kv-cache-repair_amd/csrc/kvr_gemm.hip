@@ -39,12 +39,10 @@ namespace {
 #ifndef KVR_GEMM_RING_CHUNKS
 #define KVR_GEMM_RING_CHUNKS 1
 #endif
-#ifndef KVR_GEMM_BURST
-#define KVR_GEMM_BURST 0
-#endif
 
 constexpr int kWaves = KVR_GEMM_WAVES;      // waves per block, 16 streamed weight rows each
-constexpr int kGemmThreads = 64 * kWaves;
+constexpr int kComputeThreads = 64 * kWaves;
+constexpr int kGemmThreads = kComputeThreads;
 constexpr int kTileN = 16 * kWaves;         // streamed weight rows per block
 constexpr int kHalf = kTileN / 2;           // gated: output columns per block
 constexpr int kRowsMax = 64;                // M <= 64 (four 16-row MFMA tiles)
@@ -57,8 +55,8 @@ constexpr int kRingChunks = KVR_GEMM_RING_CHUNKS;  // W ring depth in chunks
 constexpr int kRing = kRingChunks * kChunkSteps;   // W fragments in flight per lane (k-steps)
 static_assert(kRingChunks == 1 || kRingChunks == 2, "chunk buffers alternate with the ring");
 constexpr int kGranules = kChunk / 8;       // 16-B x granules per row per chunk
-constexpr int kXLoads = kRowsMax * kGranules / kGemmThreads;  // x granules per thread per chunk
-static_assert(kXLoads * kGemmThreads == kRowsMax * kGranules && kGemmThreads % kGranules == 0, "x staging map");
+constexpr int kXLoads = kRowsMax * kGranules / kComputeThreads;  // x granules per thread per chunk
+static_assert(kXLoads * kComputeThreads == kRowsMax * kGranules && kComputeThreads % kGranules == 0, "x staging map");
 constexpr int kMinSlice = 512;              // K per split at least (bounds the partial traffic)
 #ifndef KVR_GEMM_TARGET_BLOCKS
 #define KVR_GEMM_TARGET_BLOCKS 256
@@ -120,7 +118,7 @@ __device__ inline float with_residual(const GemmArgs& a, float sum, int m, int c
 // same rows of up. The fp32 tile (column c = 16w + 4lj + i) thus holds gate
 // in columns [0, kHalf) and up in [kHalf, kTileN) in gated mode.
 template <typename T, int MT>
-__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))  // two blocks per CU
 skinny_gemm_kernel(GemmArgs a) {
     using G = gemm_t<T>;
     using E = elem<T>;
@@ -189,7 +187,7 @@ skinny_gemm_kernel(GemmArgs a) {
         const int kk = min(c * kChunk + xcol, klast);
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
-            const int r = (kGemmThreads / kGranules) * i + xrow;
+            const int r = (kComputeThreads / kGranules) * i + xrow;
             xr[i] = *reinterpret_cast<const u32x4*>(xbase + (static_cast<int64_t>(r < a.m ? r : 0) * a.ldx + kk) * 2);
         }
     };
@@ -197,7 +195,7 @@ skinny_gemm_kernel(GemmArgs a) {
         const bool k_ok = c * kChunk + xcol < klen;  // klen is a multiple of 8
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
-            const int r = (kGemmThreads / kGranules) * i + xrow;
+            const int r = (kComputeThreads / kGranules) * i + xrow;
             const u32x4 zero = {0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(buf + r * kXStride + xcol) = (k_ok && r < a.m) ? xr[i] : zero;
         }
@@ -240,17 +238,9 @@ skinny_gemm_kernel(GemmArgs a) {
                     bf[t] = *reinterpret_cast<const u32x4*>(cur + (16 * t + lq) * kXStride + d * kStep + 8 * lj);
 #pragma unroll
                 for (int t = 0; t < MT; ++t) acc[t] = G::mma(af, __builtin_bit_cast(v8, bf[t]), acc[t]);
-#if !KVR_GEMM_BURST
                 wf[slot] = load_w(cc * kChunkSteps + d + kRing);
                 __builtin_amdgcn_sched_barrier(0);
-#endif
             }
-#if KVR_GEMM_BURST
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int d = 0; d < kChunkSteps; ++d) wf[r * kChunkSteps + d] = load_w(cc * kChunkSteps + d + kRing);
-            __builtin_amdgcn_sched_barrier(0);
-#endif
             store_x(cc + 1, xs + ((cc + 1) & 1) * kXBuf);
             __syncthreads();
         }
@@ -277,7 +267,7 @@ skinny_gemm_kernel(GemmArgs a) {
         for (int t = 0; t < MT; ++t)
             *reinterpret_cast<f32x4*>(red + (16 * t + lq) * kRedStride + 16 * wave + 4 * lj) = acc[t];
         __syncthreads();
-        for (int e = tid; e < 16 * MT * kHalf; e += kGemmThreads) {
+        for (int e = tid; e < 16 * MT * kHalf; e += kComputeThreads) {
             const int m = e / kHalf;
             const int c = e % kHalf;
             const int col = tile * kHalf + c;
