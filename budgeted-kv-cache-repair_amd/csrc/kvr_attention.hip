@@ -40,7 +40,13 @@ constexpr int kTilesPerGroup = 4;
 constexpr int kGroupRows = kRowTile * kTilesPerGroup;
 constexpr int kSub = 64;                   // keys per LDS sub-tile
 constexpr int kMaxChunksPerGroup = 1024;   // merge weights fit in LDS
-constexpr int kTargetBlocks = 256;         // one block per CU (MI355X: 256 CUs)
+#ifndef KVR_ATTN_TARGET_BLOCKS
+#define KVR_ATTN_TARGET_BLOCKS 256
+#endif
+#ifndef KVR_ATTN_MAX_QT
+#define KVR_ATTN_MAX_QT 4
+#endif
+constexpr int kTargetBlocks = KVR_ATTN_TARGET_BLOCKS;  // one block per CU (MI355X: 256 CUs)
 constexpr float kLazyLog2 = 8.f;           // lazy-rescale headroom (log2 units): p <= 256
 
 enum Header {
@@ -691,8 +697,8 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
 // Host helpers
 // ---------------------------------------------------------------------------
 int pick_qt(int group) {
-    if (group % 4 == 0) return 4;
-    if (group % 2 == 0) return 2;
+    if (group % 4 == 0 && KVR_ATTN_MAX_QT >= 4) return 4;
+    if (group % 2 == 0 && KVR_ATTN_MAX_QT >= 2) return 2;
     return 1;
 }
 

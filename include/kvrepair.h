@@ -294,6 +294,20 @@ int kvr_decoder_forward(const kvr_layer_desc* layers, int32_t n_layers, const kv
 void kvr_decoder_desc_sizes(int64_t sizes[2]);
 
 /*
+ * Interval writeback of the interval executors: rows [in_start, in_start + width)
+ * of in_k / in_v overwrite rows [out_start, out_start + width) of out_k / out_v,
+ * all [batch][heads][tokens][head_dim] with element strides
+ * strides[16] = out_k {b,h,t,d}, out_v {...}, in_k {...}, in_v {...} (all
+ * positive). A bit copy, K and V in one launch; outputs must not overlap each
+ * other or the inputs (the caller proves it). Replaces copy_kv_interval_
+ * (src/kv_cache_repair/kernels/writeback.py:18-60, in_start = out_start) and
+ * scatter_fresh_kv (_writeback_triton.py:44-59, in_start = 0).
+ */
+int kvr_copy_kv_interval(void* out_k, void* out_v, const void* in_k, const void* in_v, int32_t batch,
+                         int32_t heads, int64_t width, int32_t head_dim, int64_t out_start, int64_t in_start,
+                         const int64_t strides[16], int32_t dtype, void* stream);
+
+/*
  * Host-side work schedule for kvr_packed_causal_attention (no device access).
  * Splits the selected rows into row groups and each group's causal key range
  * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`

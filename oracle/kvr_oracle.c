@@ -217,6 +217,29 @@ void orc_index_copy(int dtype, void* out, const int64_t* out_stride, int64_t n_k
 }
 
 /*
+ * Interval writeback of the interval executors (kernels/writeback.py:18-60,
+ * _writeback_triton.py:7-41): rows [in_start, in_start + width) of `src`
+ * overwrite rows [out_start, out_start + width) of `out`, both
+ * [batch][heads][tokens][head_dim] with element strides {b, h, t, d}. Raw
+ * element bits are copied. One tensor per call (K and V are two calls).
+ */
+void orc_copy_interval(int dtype, void* out, const int64_t* out_stride, const void* src, const int64_t* src_stride,
+                       int64_t batch, int64_t heads, int64_t width, int32_t head_dim, int64_t out_start,
+                       int64_t in_start) {
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h)
+            for (int64_t p = 0; p < width; ++p)
+                for (int32_t d = 0; d < head_dim; ++d)
+                    copy_elem(src,
+                              b * src_stride[0] + h * src_stride[1] + (in_start + p) * src_stride[2] +
+                                  d * src_stride[3],
+                              out,
+                              b * out_stride[0] + h * out_stride[1] + (out_start + p) * out_stride[2] +
+                                  d * out_stride[3],
+                              dtype);
+}
+
+/*
  * Dense fp64 absolute-causal GQA attention, the reference's independent oracle
  * (tests/test_indexed_attention.py:106-116): K/V repeated per query group,
  * scores = q . k * scale, keys j > positions[r] masked, softmax, @ V.

@@ -44,6 +44,8 @@ def lib() -> ctypes.CDLL:
         L.orc_rope_rotate.restype = ctypes.c_int
         L.orc_index_copy.argtypes = [ctypes.c_int, _vp, _i64p, ctypes.c_int64, _vp, _i64p, _i64p, ctypes.c_int64,
                                      ctypes.c_int64, ctypes.c_int32]
+        L.orc_copy_interval.argtypes = [ctypes.c_int, _vp, _i64p, _vp, _i64p, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64]
         L.orc_attention_f64.argtypes = [ctypes.c_int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64p, ctypes.c_int64,
                                         ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                         ctypes.c_double, _f64p]
@@ -122,6 +124,27 @@ def index_copy(out: np.ndarray, fresh: np.ndarray, positions, dtype: int) -> np.
     rs, fs = _strides(result), _strides(fresh)
     lib().orc_index_copy(dtype, _ptr(result), _ptr(rs, _i64p), result.shape[1], _ptr(fresh), _ptr(fs, _i64p),
                          _ptr(pos, _i64p), pos.shape[0], result.shape[0], result.shape[2])
+    return result
+
+
+def copy_interval(out: np.ndarray, src: np.ndarray, out_start: int, in_start: int, width: int,
+                  dtype: int) -> np.ndarray:
+    """Return a copy of ``out`` [batch, heads, tokens, D] whose rows
+    [out_start, out_start + width) are rows [in_start, ...) of ``src``
+    (kernels/writeback.py:18-60; _writeback_triton.py:44-59 with in_start 0)."""
+    expect = np.float32 if dtype == F32 else np.uint16
+    for a in (out, src):
+        if a.ndim != 4 or a.dtype != expect:
+            raise ValueError("oracle copy_interval needs 4-D arrays of the dtype's storage type")
+    if out.shape[0] != src.shape[0] or out.shape[1] != src.shape[1] or out.shape[3] != src.shape[3]:
+        raise ValueError("oracle copy_interval batch/heads/head_dim differ")
+    if not (0 <= out_start and out_start + width <= out.shape[2] and 0 <= in_start
+            and in_start + width <= src.shape[2]):
+        raise ValueError("oracle copy_interval rows out of range")
+    result = np.array(out, copy=True)
+    lib().orc_copy_interval(dtype, _ptr(result), _ptr(_strides(result), _i64p), _ptr(src),
+                            _ptr(_strides(src), _i64p), out.shape[0], out.shape[1], width, out.shape[3], out_start,
+                            in_start)
     return result
 
 

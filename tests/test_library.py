@@ -26,7 +26,8 @@ def test_header_declares_the_entry_points():
         "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
         "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
         "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
-        "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes"])
+        "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
+        "kvr_copy_kv_interval"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -100,6 +101,20 @@ def test_entry_points_validate_before_any_launch():
     assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 0, None, 0, None, 0, 2, None) == -6  # workspace
     assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 2, None, 0, None, 0, 2, None) == -5  # residual
     assert lib.kvr_linear_multi(16, 3, w3, rows, ldw, 16, *args, 2, 16, 6000, None, 0, 2, None) == -4  # ldr
+
+
+def test_interval_copy_validates_before_any_launch():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    s16 = _native.i64_array([1] * 16)
+    assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 3, 8, 0, 0, s16, 7, None) == -2  # dtype
+    assert lib.kvr_copy_kv_interval(None, None, None, None, 0, 2, 3, 8, 0, 0, s16, 2, None) == -1  # batch
+    assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 3, 8, -1, 0, s16, 2, None) == -1  # start
+    assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 3, 8, 0, 0, _native.i64_array([0] * 16), 2,
+                                    None) == -4
+    assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 0, 8, 0, 0, s16, 2, None) == 0  # empty: no-op
+    assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 3, 8, 0, 0, s16, 2, None) == -5
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):

@@ -220,6 +220,52 @@ def test_scatter_skips_out_of_range_positions():
     assert got[0, 2].tolist() == [1.0] * 8 and got.sum() == 8
 
 
+# --------------------------------------------------------------------------- interval writeback
+@pytest.mark.parametrize("shape,start,end", [((1, 8, 37, 16), 3, 4), ((2, 3, 71, 37), 5, 22),
+                                             ((2, 5, 33, 7), 0, 33), ((1, 1, 9, 13), 0, 0)])
+def test_copy_interval_matches_slice_assignment_on_strided_views(shape, start, end):
+    # shapes and bounds of the reference's tests/test_writeback.py:34-40; torch slice copy is the checker
+    torch.manual_seed(701 + end)
+    b, h, t, d = shape
+    out_backing = torch.randn(b, h, 2 * t + 3, 2 * d + 5)
+    out_view = out_backing[:, :, 1:1 + 2 * t:2, 2:2 + 2 * d:2]            # "holes"
+    src = torch.randn(b, max(1, end), h, d).permute(0, 2, 1, 3)          # token-major
+    expect = out_view.clone()
+    expect[:, :, start:end] = src[:, :, start:end]
+    got = orc.copy_interval(out_view.numpy(), src.numpy(), start, start, end - start, orc.F32)
+    assert np.array_equal(got, expect.numpy())
+    fresh = torch.randn(b, h, end - start + 2, d)                        # scatter_fresh_kv: rows [0, W)
+    expect = out_view.clone()
+    expect[:, :, start:end] = fresh[:, :, :end - start]
+    got = orc.copy_interval(out_view.numpy(), fresh.numpy(), start, 0, end - start, orc.F32)
+    assert np.array_equal(got, expect.numpy())
+
+
+@pytest.mark.parametrize("dtype,payload", [
+    (torch.float16, [0, -32768, 31744, -1024, 32257, 1]),   # reference tests/test_writeback.py:102-103
+    (torch.bfloat16, [0, -32768, 32640, -128, 32705, 1]),
+])
+def test_copy_interval_keeps_payload_bits(dtype, payload):
+    raw = np.array(payload, np.int16).view(np.uint16).reshape(1, 1, 2, 3)
+    out = np.zeros((1, 1, 4, 3), np.uint16)
+    got = orc.copy_interval(out, raw, 0, 0, 2, CODE[dtype])
+    assert np.array_equal(got[:, :, :2], raw) and not got[:, :, 2:].any()
+
+
+def test_copy_interval_rejects_rows_out_of_range():
+    with pytest.raises(ValueError, match="range"):
+        orc.copy_interval(np.zeros((1, 1, 4, 3), np.float32), np.zeros((1, 1, 2, 3), np.float32), 3, 0, 2, orc.F32)
+
+
+def test_writeback_rejects_cpu_tensors_before_any_device_work():
+    # reference tests/test_writeback.py:62-65: no silent CPU fallback
+    from kv_cache_repair_amd.kernels.writeback import copy_kv_interval_
+
+    tensors = [torch.zeros((1, 1, 3, 4)) for _ in range(4)]
+    with pytest.raises(ValueError, match="CUDA"):
+        copy_kv_interval_(*tensors, 0, 1)
+
+
 # --------------------------------------------------------------------------- attention
 def test_attention_query_at_zero_returns_value_zero():
     # reference tests/test_indexed_attention.py:251-259
