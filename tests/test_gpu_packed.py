@@ -327,6 +327,74 @@ def test_bf16_8b_layer_geometry_refresh_matches_reference(gpu_device):
                                                  ref.layer_kv(control, i)[c][:, :, 928:992])
 
 
+def _large_geometry_stage(gpu_device, family, total, delete_at, delete_span, intervals, seed, layers=2):
+    """BASELINE c4 / c5 edits on `layers` decoder layers of the 8B geometry (random
+    weights, K/V ~ N(0,1)): HIP stage, reference stage and its fp32 control."""
+    from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM
+
+    from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache
+    from kv_cache_repair_amd.kernels.packed_cache import packed_refresh_owned_
+
+    torch.manual_seed(seed)
+    common = dict(vocab_size=1024, hidden_size=4096, num_hidden_layers=layers, num_attention_heads=32,
+                  num_key_value_heads=8, head_dim=128, max_position_embeddings=total)
+    if family == "qwen3":
+        cfg = Qwen3Config(intermediate_size=12288, rope_theta=1000000.0, layer_types=["full_attention"] * layers,
+                          **common)
+        ctor = Qwen3ForCausalLM
+    else:
+        cfg = LlamaConfig(intermediate_size=14336, rope_theta=500000.0, **common)
+        ctor = LlamaForCausalLM
+    with torch.device(gpu_device):
+        model = ctor(cfg).to(torch.bfloat16).eval()
+    gen = torch.Generator(device=gpu_device).manual_seed(seed)
+    old = ref.cache_from_tensors([(torch.randn(1, 8, total, 128, device=gpu_device, generator=gen).to(torch.bfloat16),
+                                   torch.randn(1, 8, total, 128, device=gpu_device, generator=gen).to(torch.bfloat16))
+                                  for _ in range(layers)])
+    old_ids = torch.randint(0, 1024, (1, total), device=gpu_device, generator=gen)
+    old_ids[0, delete_at] = (old_ids[0, delete_at + delete_span] + 1) % 1024  # prefix stops at the edit
+    new_ids = torch.cat((old_ids[:, :delete_at], old_ids[:, delete_at + delete_span:]), dim=1)
+    shim = OperatorShim(model)
+    ours, meta = build_halo_cache(shim, old, old_ids, new_ids, 0)
+    receipt = packed_refresh_owned_(shim, ours, new_ids, intervals)
+    expect = ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)
+    control_model = copy.deepcopy(model).float()
+    control_old = ref.cache_from_tensors([(l.keys.float(), l.values.float()) for l in old.layers])
+    control = ref.reference_refresh_stage(control_model, control_old, old_ids, new_ids, intervals)
+    assert meta["position_shift"] == -delete_span
+    assert receipt["recomputed_tokens"] == sum(e - b for b, e in intervals)
+    selected = [p for b, e in intervals for p in range(b, e)]
+    keep = torch.ones(new_ids.shape[1], dtype=torch.bool, device=gpu_device)
+    keep[selected] = False
+    for i in range(layers):
+        for c in (0, 1):
+            a, e = ref.layer_kv(ours, i)[c], ref.layer_kv(expect, i)[c]
+            assert bits_equal(a[:, :, keep], e[:, :, keep])  # rotated/copied rows: bit-exact
+            assert_north_star_close(a[:, :, selected], e[:, :, selected], ref.layer_kv(control, i)[c][:, :, selected])
+            assert_within_native_precision_floor(a[:, :, selected], e[:, :, selected],
+                                                 ref.layer_kv(control, i)[c][:, :, selected])
+
+
+def test_c4_qwen3_geometry_32k_cache_5_percent_budget(gpu_device):
+    """BASELINE config 4 on two layers: Qwen3-8B geometry (per-head q/k norm,
+    theta 1e6), 32768-token cache, delete 1024 @4096, 1383 rows in 32 random
+    intervals (seed 3) -- more rows than one projection launch, so the layers
+    run through the dispatched fused shells and the modules' GEMMs."""
+    import random
+
+    slots = sorted(random.Random(3).sample(range(27648 // 88), 32))
+    intervals = [(4096 + 88 * s, 4096 + 88 * s + (44 if i < 7 else 43)) for i, s in enumerate(slots)]
+    _large_geometry_stage(gpu_device, "qwen3", 32768, 4096, 1024, intervals, seed=3)
+
+
+def test_c5_full_refresh_geometry(gpu_device):
+    """BASELINE config 5 on two layers: 8B Llama geometry, 16384-token cache,
+    delete 256 @1024, every one of the 15104 suffix rows refreshed (the packed
+    attention becomes a dense causal prefill tile; the scatter rewrites the
+    whole suffix)."""
+    _large_geometry_stage(gpu_device, "llama", 16384, 1024, 256, [(1024, 16128)], seed=4)
+
+
 @pytest.mark.parametrize("family", ["llama", "qwen3"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_fused_fresh_row_epilogue_is_bit_identical_to_native_rope_and_scatter(gpu_device, family, dtype):
