@@ -272,9 +272,10 @@ def reference_stage(model, old, old_ids, new_ids, intervals):
 
 
 # ----------------------------------------------------------------------------- HBM traffic (rocprofv3 PMC)
-TRAFFIC_SUMMARY = ROOT / "profiles" / "attention_c3_hbm_traffic.md"
+TRAFFIC_SUMMARIES = (ROOT / "profiles" / "attention_c3_hbm_traffic.md",
+                     ROOT / "profiles" / "projection_gemm_c3_hbm_traffic.md")
 KERNEL_SOURCES = {"kvr_packed_causal_attention": "kvr_attention.hip", "kvr_shift_cache_build": "kvr_rotate.hip",
-                  "kvr_indexed_scatter_kv": "kvr_scatter.hip"}
+                  "kvr_indexed_scatter_kv": "kvr_scatter.hip", "kvr_linear_multi": "kvr_gemm.hip"}
 
 
 def source_digest(name: str) -> str:
@@ -285,20 +286,21 @@ def source_digest(name: str) -> str:
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counts), or None when the
-    summary is absent or was measured on another version of the kernel source."""
-    if kernel not in KERNEL_SOURCES or not TRAFFIC_SUMMARY.exists():
+    """HBM bytes per launch of ``kernel`` from a committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counts), or None when no
+    summary covers it or it was measured on another version of the kernel source."""
+    if kernel not in KERNEL_SOURCES:
         return None
-    fields = {}
-    for line in TRAFFIC_SUMMARY.read_text().splitlines():
-        if line.startswith("traffic:"):
-            for item in line[len("traffic:"):].split():
-                key, _, value = item.partition("=")
-                fields[key] = value
-    if fields.get("kernel") != kernel or fields.get("source_sha256") != source_digest(KERNEL_SOURCES[kernel]):
-        return None
-    return int(fields["bytes_per_launch"])
+    for summary in TRAFFIC_SUMMARIES:
+        if not summary.exists():
+            continue
+        for line in summary.read_text().splitlines():
+            if not line.startswith("traffic:"):
+                continue
+            fields = dict(item.partition("=")[::2] for item in line[len("traffic:"):].split())
+            if fields.get("kernel") == kernel and fields.get("source_sha256") == source_digest(KERNEL_SOURCES[kernel]):
+                return int(fields["bytes_per_launch"])
+    return None
 
 
 # ----------------------------------------------------------------------------- CPU baseline
