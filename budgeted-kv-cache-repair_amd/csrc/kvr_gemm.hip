@@ -16,10 +16,14 @@
 // Work split: block = 4 waves x 16 streamed weight rows (64 rows) x one K
 // slice. The slice is walked in chunks of 256: x[:, chunk] is staged in one of
 // two LDS buffers (the next chunk's global loads are in flight while the
-// current one is multiplied) and shared by the 4 waves; W streams straight
-// into MFMA registers through a ring of 8 fragments per lane (one chunk
-// ahead). Split-K slices (S > 1) write fp32 partial tiles to a workspace and a
-// second launch sums them in slice order, so results are deterministic.
+// current one is multiplied) and shared by the 4 waves; W streams into
+// registers through a ring of 8 loads per lane (one chunk ahead), each load
+// instruction covering whole 128-B lines of 8 rows (one memory request per
+// line: 16-row x 64-B loads in the MFMA layout reach ~25% less bandwidth),
+// and every pair of loads is transposed to MFMA A fragments through a small
+// per-wave LDS tile. Split-K slices (S > 1) write fp32 partial tiles to a
+// workspace and a second launch sums them in slice order, so results are
+// deterministic.
 #include "kvr_internal.h"
 
 #include <string.h>
@@ -32,9 +36,6 @@ namespace {
 #endif
 #ifndef KVR_GEMM_CHUNK_STEPS
 #define KVR_GEMM_CHUNK_STEPS 8
-#endif
-#ifndef KVR_GEMM_NT
-#define KVR_GEMM_NT 1
 #endif
 #ifndef KVR_GEMM_RING_CHUNKS
 #define KVR_GEMM_RING_CHUNKS 1
@@ -52,8 +53,13 @@ constexpr int kChunk = kChunkSteps * kStep; // K per chunk
 constexpr int kXStride = kChunk + 8;        // LDS row stride (elements): 16 B pad, conflict-free B reads
 constexpr int kXBuf = kRowsMax * kXStride;  // one chunk buffer (elements)
 constexpr int kRingChunks = KVR_GEMM_RING_CHUNKS;  // W ring depth in chunks
-constexpr int kRing = kRingChunks * kChunkSteps;   // W fragments in flight per lane (k-steps)
+#ifndef KVR_GEMM_RING
+#define KVR_GEMM_RING (KVR_GEMM_RING_CHUNKS * KVR_GEMM_CHUNK_STEPS)
+#endif
+constexpr int kRing = KVR_GEMM_RING;               // W fragments in flight per lane (k-steps)
 static_assert(kRingChunks == 1 || kRingChunks == 2, "chunk buffers alternate with the ring");
+static_assert((kRingChunks * kChunkSteps) % kRing == 0, "ring slots repeat within the unrolled chunks");
+static_assert(kRing % 2 == 0 && kChunkSteps % 2 == 0, "whole-line loads come in pairs");
 constexpr int kGranules = kChunk / 8;       // 16-B x granules per row per chunk
 constexpr int kXLoads = kRowsMax * kGranules / kComputeThreads;  // x granules per thread per chunk
 static_assert(kXLoads * kComputeThreads == kRowsMax * kGranules && kComputeThreads % kGranules == 0, "x staging map");
@@ -136,47 +142,57 @@ skinny_gemm_kernel(GemmArgs a) {
     const int k0 = split * a.slice;
     const int klen = (a.k - k0 < a.slice) ? a.k - k0 : a.slice;  // > 0, multiple of 8
 
-    // ---- this lane's streamed weight row ----
-    const char* wb;
-    int64_t ldw;
-    int local;
-    bool row_ok;
-    if (a.gated) {
-        const bool up = wave >= kWaves / 2;
-        local = tile * kHalf + 16 * (up ? wave - kWaves / 2 : wave) + lq;
-        row_ok = local < a.n_out;
-        wb = up ? a.w1 : a.w0;
-        ldw = up ? a.ldw1 : a.ldw0;
-    } else {
-        const int g = tile * kTileN + 16 * wave + lq;
-        row_ok = g < a.rows;
-        if (g < a.end0) {
-            wb = a.w0; ldw = a.ldw0; local = g;
-        } else if (g < a.end1) {
-            wb = a.w1; ldw = a.ldw1; local = g - a.end0;
+    // ---- this lane's streamed weight rows ----
+    // Pointer to k0 of row `rw` (0..15) of the wave's 16 streamed rows; rows
+    // past the end read row 0 (their outputs are never written).
+    auto row_ptr = [&](int rw) __attribute__((always_inline)) -> const char* {
+        const char* wb;
+        int64_t ldw;
+        int local;
+        bool row_ok;
+        if (a.gated) {
+            const bool up = wave >= kWaves / 2;
+            local = tile * kHalf + 16 * (up ? wave - kWaves / 2 : wave) + rw;
+            row_ok = local < a.n_out;
+            wb = up ? a.w1 : a.w0;
+            ldw = up ? a.ldw1 : a.ldw0;
         } else {
-            wb = a.w2; ldw = a.ldw2; local = g - a.end1;
+            const int g = tile * kTileN + 16 * wave + rw;
+            row_ok = g < a.rows;
+            if (g < a.end0) {
+                wb = a.w0; ldw = a.ldw0; local = g;
+            } else if (g < a.end1) {
+                wb = a.w1; ldw = a.ldw1; local = g - a.end0;
+            } else {
+                wb = a.w2; ldw = a.ldw2; local = g - a.end1;
+            }
         }
-    }
-    if (!row_ok) local = 0;
+        if (!row_ok) local = 0;
+        return wb + (static_cast<int64_t>(local) * ldw + k0) * 2;
+    };
 
-    // ---- W ring: the fragment of k-step s lives in wf[s % kRing] ----
-    // Loads are unconditional, so the wait before each MFMA covers only the
-    // fragment it consumes: rows past the end read row 0 (their outputs are
-    // never written) and k offsets past the slice are clamped to its last 8
+    // ---- W ring: the load of k-step s lives in wf[s % kRing] ----
+    // Loads are unconditional, so the wait before each use covers only the
+    // load it consumes; k offsets past the slice are clamped to its last 8
     // elements (in bounds; they meet the zeroed tail of the staged x, so they
     // contribute 0 * w = 0 for finite w).
-    const char* wrow = wb + (static_cast<int64_t>(local) * ldw + k0) * 2;
+    //
+    // Whole-line loads: one instruction covers 8 rows x 128 B (lane L reads
+    // piece L & 7 of row 8h + (L >> 3), h = s & 1, k block s >> 1), every
+    // 128-B line in a single request. Each pair of loads (16 rows x 64 k) is
+    // transposed to the two MFMA A fragments of k-steps 2u, 2u + 1 through a
+    // 2 KB per-wave LDS tile (pieces XOR-swizzled by row: conflict-free).
     const int klast = klen - 8;
     u32x4 wf[kRing];
-    auto load_w = [&](int s) __attribute__((always_inline)) -> u32x4 {
-        const int kk = min(s * kStep + 8 * lj, klast);
-#if KVR_GEMM_NT
-        return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + kk * 2));
-#else
-        return *reinterpret_cast<const u32x4*>(wrow + kk * 2);
-#endif
+    const char* wrow[2] = {row_ptr(lane >> 3), row_ptr(8 + (lane >> 3))};
+    auto load_w = [&](int s, int h) __attribute__((always_inline)) -> u32x4 {
+        const int kk = min((s >> 1) * 64 + 8 * (lane & 7), klast);
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + kk * 2));
     };
+    char* wtile = reinterpret_cast<char*>(xs + 2 * kXBuf) + wave * 2048;
+    char* const wput = wtile + (lane >> 3) * 128 + (((lane & 7) ^ (lane >> 3)) * 16);
+    const char* const wget0 = wtile + (lq >> 3) * 1024 + (lq & 7) * 128 + (((0 + lj) ^ (lq & 7)) * 16);
+    const char* const wget1 = wtile + (lq >> 3) * 1024 + (lq & 7) * 128 + (((4 + lj) ^ (lq & 7)) * 16);
 
     // ---- x chunks: thread t stages granules (row (threads / G) i + t / G, 8 (t % G)) ----
     const int xrow = tid / kGranules;
@@ -204,7 +220,7 @@ skinny_gemm_kernel(GemmArgs a) {
     const int chunks = (klen + kChunk - 1) / kChunk;
     load_x(0);
 #pragma unroll
-    for (int d = 0; d < kRing; ++d) wf[d] = load_w(d);
+    for (int d = 0; d < kRing; ++d) wf[d] = load_w(d, d & 1);
     store_x(0, xs);
     __syncthreads();
 
@@ -212,10 +228,10 @@ skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Chunk c: issue chunk c + 1's x loads, multiply chunk c (refilling each W
-    // slot with the fragment kRing steps ahead right after its MFMAs, so the
-    // load reuses the slot's registers), then store chunk c + 1 into the other
-    // buffer. The loop advances kRingChunks chunks at a time so every ring slot
+    // Chunk c: issue chunk c + 1's x loads, multiply chunk c pair by pair
+    // (copy the pair's two loads into the transpose tile, refill their slots
+    // with the loads kRing steps ahead, read back the two A fragments, run the
+    // MFMAs), then store chunk c + 1 into the other buffer. The loop advances kRingChunks chunks at a time so every ring slot
     // index is static; a chunk past the last one multiplies an all-zero x
     // buffer (store_x zeroes k >= klen) and adds nothing. Past the slice the
     // loads repeat in-bounds addresses into the idle buffer or unread slots.
@@ -229,16 +245,24 @@ skinny_gemm_kernel(GemmArgs a) {
             load_x(cc + 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int d = 0; d < kChunkSteps; ++d) {
-                const int slot = r * kChunkSteps + d;
-                const v8 af = __builtin_bit_cast(v8, wf[slot]);
-                u32x4 bf[MT];
+            for (int d = 0; d < kChunkSteps; d += 2) {
+                const int slot = (r * kChunkSteps + d) % kRing;
+                *reinterpret_cast<u32x4*>(wput) = wf[slot];
+                *reinterpret_cast<u32x4*>(wput + 1024) = wf[slot + 1];
+                wf[slot] = load_w(cc * kChunkSteps + d + kRing, 0);
+                wf[slot + 1] = load_w(cc * kChunkSteps + d + 1 + kRing, 1);
+                const v8 af0 = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(wget0));
+                const v8 af1 = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(wget1));
+                u32x4 bf0[MT], bf1[MT];
 #pragma unroll
-                for (int t = 0; t < MT; ++t)
-                    bf[t] = *reinterpret_cast<const u32x4*>(cur + (16 * t + lq) * kXStride + d * kStep + 8 * lj);
+                for (int t = 0; t < MT; ++t) {
+                    bf0[t] = *reinterpret_cast<const u32x4*>(cur + (16 * t + lq) * kXStride + d * kStep + 8 * lj);
+                    bf1[t] = *reinterpret_cast<const u32x4*>(cur + (16 * t + lq) * kXStride + (d + 1) * kStep + 8 * lj);
+                }
 #pragma unroll
-                for (int t = 0; t < MT; ++t) acc[t] = G::mma(af, __builtin_bit_cast(v8, bf[t]), acc[t]);
-                wf[slot] = load_w(cc * kChunkSteps + d + kRing);
+                for (int t = 0; t < MT; ++t) acc[t] = G::mma(af0, __builtin_bit_cast(v8, bf0[t]), acc[t]);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) acc[t] = G::mma(af1, __builtin_bit_cast(v8, bf1[t]), acc[t]);
                 __builtin_amdgcn_sched_barrier(0);
             }
             store_x(cc + 1, xs + ((cc + 1) & 1) * kXBuf);
@@ -345,7 +369,8 @@ __global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(GemmArgs 
     }
 }
 
-constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2;  // two x chunk buffers
+// two x chunk buffers + the per-wave W transpose tiles
+constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + kWaves * 2048;
 static_assert(kLdsBytes >= static_cast<size_t>(kRowsMax) * kRedStride * 4, "gated epilogue tile fits");
 
 template <typename F>
