@@ -76,6 +76,14 @@ def _shift_rows(old_k, old_v, new_k, new_v, *, prefix_rows, old_tail_start, new_
 
 def _check_uniform(pairs, what: str):
     first = pairs[0][0]
+    # Fast path: every tensor has the first one's exact shape, strides, dtype and
+    # GPU (what build_halo_cache and the executors produce) and that layout
+    # passes the checks below; anything else takes the per-tensor checks.
+    sig = (first.shape, first.stride(), first.dtype, first.get_device())
+    if (first.ndim == 4 and first.shape[0] == 1 and sig[3] >= 0 and all(s > 0 for s in sig[1])
+            and all((t.shape, t.stride(), t.dtype, t.get_device()) == sig for pair in pairs for t in pair)):
+        _require_device(first, what)
+        return
     for key, value in pairs:
         for t in (key, value):
             if t.ndim != 4 or t.shape[0] != 1 or t.shape[1] != first.shape[1] or t.shape[3] != first.shape[3]:
@@ -203,7 +211,8 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     inv_freq, scaling, rotary_dim = _rotary(generator, k0.device)
     # one allocation for every layer's K and V; each layer gets contiguous [1, Hkv, N, D] views
     slab = torch.empty((len(old), 2, 1, k0.shape[1], n_new, k0.shape[3]), dtype=k0.dtype, device=k0.device)
-    new = [(slab[i, 0], slab[i, 1]) for i in range(len(old))]
+    views = slab.view(2 * len(old), 1, k0.shape[1], n_new, k0.shape[3]).unbind(0)
+    new = list(zip(views[0::2], views[1::2]))
     if recompute_end == align["prefix"]:
         # No recomputed rows: prefix copy + shifted tail in one launch.
         if n_new:

@@ -26,6 +26,19 @@ def _validate_cache(cache: Any, logical_length: int) -> int:
     layer_count = len(layers)
     if layer_count == 0:
         raise ValueError("base_cache must contain at least one K/V layer")
+    # Fast path: every layer's K and V share one shape, dtype and GPU that
+    # satisfy the per-layer checks below; otherwise those checks name the layer.
+    try:
+        tensors = [t for entry in layers for t in (entry.keys, entry.values)]
+    except AttributeError:
+        tensors = None
+    if tensors and all(isinstance(t, torch.Tensor) for t in tensors):
+        first = tensors[0]
+        sig = (first.shape, first.dtype, first.get_device())
+        if (first.ndim == 4 and sig[2] >= 0 and first.shape[0] == 1 and first.shape[2] == logical_length
+                and first.shape[1] > 0 and first.shape[3] > 0 and first.is_floating_point()
+                and all((t.shape, t.dtype, t.get_device()) == sig for t in tensors)):
+            return layer_count
     expected_shape = expected_dtype = None
     for layer in range(layer_count):
         try:

@@ -231,10 +231,11 @@ def _plans_key(projections, norms) -> tuple:
     """Identity of everything a layer's plans point at: module objects, weight
     tensors and their storage, and the projections' (absent) biases."""
     key = []
+    add = key.extend
     for m in (*projections, *norms):
         params = m.__dict__["_parameters"]
         w = params.get("weight")
-        key += (id(m), id(w), w.data_ptr() if isinstance(w, torch.Tensor) else 0, params.get("bias") is None)
+        add((id(m), id(w), w.data_ptr() if w is not None else 0, params.get("bias") is None))
     return tuple(key)
 
 
@@ -490,19 +491,22 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     device = edited_ids.device
     # One walk over the module tree (through the `_modules` dicts: a module
     # reached twice is checked twice, which changes no outcome) gathers every
-    # per-module condition below.
+    # per-module condition below. Parameters are compared by device index
+    # (get_device(): -1 off the GPUs), the request device being a GPU.
+    index = device.index if device.type == "cuda" else -2
     training = hooked = overridden = off_device = False
     stack = [(model, False)]
+    pop, extend = stack.pop, stack.extend
     while stack:
-        module, in_base = stack.pop()
+        module, in_base = pop()
         in_base = in_base or module is base
         attrs = module.__dict__
         training |= in_base and attrs["training"]
         hooked |= attrs.get("_hf_hook") is not None
         overridden |= in_base and "forward" in attrs
         for p in attrs["_parameters"].values():
-            off_device |= p is not None and p.device != device
-        stack.extend((child, in_base) for child in attrs["_modules"].values() if child is not None)
+            off_device |= p is not None and p.get_device() != index
+        extend((child, in_base) for child in attrs["_modules"].values() if child is not None)
     if model.training or base.training or training:
         raise ValueError("packed executor requires eval mode on all decoder modules")
     config = model.config
@@ -688,12 +692,45 @@ def _native_layer_descs(plans, output, layer_count):
     return descs
 
 
+def _native_inputs(base, d, edited_ids_t, positions):
+    """(hidden, cos, sin) of the selected rows from ONE kvr_refresh_inputs launch:
+    the embedding rows and the rotary tables the model's own modules would
+    produce (a plain nn.Embedding and the default-RoPE rotary module, whose
+    fp32 operations the kernel repeats: bit-identical tables). None when the
+    modules are not of that plain form; the caller then runs them."""
+    embed, rotary = base.embed_tokens, base.rotary_emb
+    weight = embed.__dict__["_parameters"].get("weight")
+    inv_freq = rotary.__dict__["_buffers"].get("inv_freq")
+    if (type(embed) is not torch.nn.Embedding or embed.max_norm is not None or weight is None
+            or _native.DTYPE_CODES.get(weight.dtype) != d.dtype or weight.ndim != 2 or weight.stride(1) != 1
+            or int(weight.shape[1]) != d.hidden or inv_freq is None or 2 * inv_freq.numel() != d.head_dim
+            or type(rotary).__name__ not in ("LlamaRotaryEmbedding", "Qwen3RotaryEmbedding")):
+        return None
+    inv_freq = inv_freq.to(device=weight.device, dtype=torch.float32).contiguous()
+    n, hidden_size, head_dim = int(d.rows), int(d.hidden), int(d.head_dim)
+    buf = torch.empty(n * (hidden_size + 2 * head_dim), dtype=weight.dtype, device=weight.device)
+    hidden = buf[:n * hidden_size].view(1, n, hidden_size)
+    cos = buf[n * hidden_size:n * (hidden_size + head_dim)].view(1, n, head_dim)
+    sin = buf[n * (hidden_size + head_dim):].view(1, n, head_dim)
+    ids = edited_ids_t[0]
+    if ids.stride(0) != 1:
+        ids = ids.contiguous()
+    status = _native.lib().kvr_refresh_inputs(
+        ids.data_ptr(), 1 if ids.dtype == torch.int32 else 0, int(ids.shape[0]), positions.data_ptr(), n,
+        weight.data_ptr(), int(weight.shape[0]), int(weight.stride(0)), hidden_size, hidden.data_ptr(), hidden_size,
+        inv_freq.data_ptr(), head_dim, float(getattr(rotary, "attention_scaling", 1.0)), cos.data_ptr(),
+        sin.data_ptr(), d.dtype, _native.stream_handle(weight.device))
+    _native.check(status, "kvr_refresh_inputs")
+    return hidden, cos, sin
+
+
 def _native_refresh(base, launcher: _Launcher, plans, output, layer_count: int, edited_ids_t, positions) -> None:
     """The packed forward as ONE kvr_decoder_forward call over all layers.
 
-    The model's own embedding and rotary modules make the selected rows' input
-    hidden states and cos/sin tables (as LlamaModel/Qwen3Model.forward does,
-    transformers 5.15.0 modeling_llama.py:377-398); then every decoder layer
+    One kvr_refresh_inputs launch makes the selected rows' input hidden states
+    and cos/sin tables (what the model's embedding and rotary modules compute in
+    LlamaModel/Qwen3Model.forward, transformers 5.15.0 modeling_llama.py:377-398,
+    bit for bit; other module forms run the modules); then every decoder layer
     runs as kvr_decoder_layer -- the same kernels with the same arguments as the
     Python-dispatched fused shells, so the cache is bit-identical. The final
     norm is skipped: the refresh consumes only the K/V the layers scatter.
@@ -702,8 +739,13 @@ def _native_refresh(base, launcher: _Launcher, plans, output, layer_count: int, 
     native = _NativeForward(launcher, int(first.mlp.down_proj.weight.shape[0]),
                             int(first.mlp.gate_proj.weight.shape[0]), float(first.self_attn.scaling))
     descs = _native_layer_descs(plans, output, layer_count)
-    hidden = base.embed_tokens(edited_ids_t.index_select(1, positions)).contiguous()
-    native.bind_tables(base.rotary_emb(hidden, positions.unsqueeze(0)))
+    inputs = _native_inputs(base, native.desc, edited_ids_t, positions)
+    if inputs is None:
+        hidden = base.embed_tokens(edited_ids_t.index_select(1, positions)).contiguous()
+        native.bind_tables(base.rotary_emb(hidden, positions.unsqueeze(0)))
+    else:
+        hidden, cos, sin = inputs
+        native.bind_tables((cos, sin))
     d = native.desc
     if hidden.shape != (1, d.rows, d.hidden) or _native.DTYPE_CODES.get(hidden.dtype) != d.dtype:
         raise RuntimeError("packed native hidden-state geometry/dtype drifted")

@@ -125,6 +125,30 @@ int kvr_indexed_scatter_kv(void* out_k, void* out_v, const void* fresh_k, const 
                            int32_t head_dim, const int64_t strides[12], int32_t dtype, void* stream);
 
 /*
+ * Input rows of the packed forward in ONE launch: the embedding lookup and the
+ * rotary tables that LlamaModel/Qwen3Model.forward computes before its first
+ * decoder layer (transformers 5.15.0 models/llama/modeling_llama.py:377-398;
+ * default RoPE, LlamaRotaryEmbedding.forward :113-127), for the selected rows:
+ *   hidden[r, :] = embed[ids[positions[r]], :]                        (bit copy)
+ *   cos[r, d]    = dtype(cosf(float(positions[r]) * inv_freq[d % (D/2)]) * scaling)
+ *   sin[r, d]    = dtype(sinf(float(positions[r]) * inv_freq[d % (D/2)]) * scaling)
+ * r < n_sel, D = head_dim (even); fp32 product, cos/sin and scaling, one
+ * rounding to `dtype`: the rotary module's own operations, bit-identical to its
+ * tables on this device. The reference obtains these from the model's modules
+ * inside its packed forward (src/kv_cache_repair/kernels/packed_cache.py:
+ * 225-298); this entry has no counterpart of its own. ids: n_ids token ids,
+ * int32 when ids_are_int32 else int64; positions: n_sel int64 indices into ids.
+ * embed: [vocab][ld_embed], hidden: [n_sel][ld_hidden], cos/sin: contiguous
+ * [n_sel][head_dim]; inv_freq: head_dim / 2 fp32 values. A position outside
+ * [0, n_ids) or a token id outside [0, vocab) writes a quiet-NaN hidden row
+ * (nothing is read out of bounds). n_sel == 0 enqueues nothing.
+ */
+int kvr_refresh_inputs(const void* ids, int32_t ids_are_int32, int64_t n_ids, const int64_t* positions,
+                       int64_t n_sel, const void* embed, int64_t vocab, int64_t ld_embed, int32_t hidden_size,
+                       void* hidden, int64_t ld_hidden, const float* inv_freq, int32_t head_dim, float scaling,
+                       void* cos, void* sin, int32_t dtype, void* stream);
+
+/*
  * Fresh-row epilogue of one packed layer in ONE launch (RoPE at absolute
  * positions fused with the indexed K/V scatter):
  *   q_out[0, h, r, :]            = rope(q[0, h, r, :], cos[r], sin[r])        h < n_q_heads

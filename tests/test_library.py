@@ -27,7 +27,7 @@ def test_header_declares_the_entry_points():
         "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
         "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
-        "kvr_copy_kv_interval"])
+        "kvr_copy_kv_interval", "kvr_refresh_inputs"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -115,6 +115,21 @@ def test_interval_copy_validates_before_any_launch():
                                     None) == -4
     assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 0, 8, 0, 0, s16, 2, None) == 0  # empty: no-op
     assert lib.kvr_copy_kv_interval(None, None, None, None, 1, 2, 3, 8, 0, 0, s16, 2, None) == -5
+
+
+def test_refresh_inputs_validates_before_any_launch():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    call = lib.kvr_refresh_inputs
+    # ids, int32?, n_ids, positions, n_sel, embed, vocab, ld_embed, hidden, out, ld_out, inv_freq, D, scaling, cos, sin
+    assert call(None, 0, 8, None, 4, None, 100, 64, 64, None, 64, None, 128, 1.0, None, None, 7, None) == -2  # dtype
+    assert call(None, 0, 8, None, 4, None, 100, 64, 64, None, 64, None, 127, 1.0, None, None, 2, None) == -1  # odd D
+    assert call(None, 0, 8, None, -1, None, 100, 64, 64, None, 64, None, 128, 1.0, None, None, 2, None) == -1
+    assert call(None, 0, 8, None, 4, None, 0, 64, 64, None, 64, None, 128, 1.0, None, None, 2, None) == -1  # vocab
+    assert call(None, 0, 8, None, 4, None, 100, 32, 64, None, 64, None, 128, 1.0, None, None, 2, None) == -4  # ld
+    assert call(None, 0, 8, None, 0, None, 100, 64, 64, None, 64, None, 128, 1.0, None, None, 2, None) == 0  # empty
+    assert call(None, 0, 8, None, 4, None, 100, 64, 64, None, 64, None, 128, 1.0, None, None, 2, None) == -5
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
