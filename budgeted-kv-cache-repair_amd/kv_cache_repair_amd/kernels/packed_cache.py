@@ -489,24 +489,29 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     if (type(model), type(base)) not in {(LlamaForCausalLM, LlamaModel), (Qwen3ForCausalLM, Qwen3Model)}:
         raise ValueError("packed executor requires exact native dense Llama or Qwen3 classes")
     device = edited_ids.device
-    # One walk over the module tree (through the `_modules` dicts: a module
-    # reached twice is checked twice, which changes no outcome) gathers every
-    # per-module condition below. Parameters are compared by device index
-    # (get_device(): -1 off the GPUs), the request device being a GPU.
+    # Module-tree conditions, gathered from the modules' __dict__s in two flat
+    # walks through the `_modules` dicts: the decoder (`base`) subtree, whose
+    # modules must all be in eval mode with no per-instance forward, and the
+    # rest of the model; no module anywhere may carry a dispatch hook or a
+    # parameter off the request device (compared by index: get_device() is -1
+    # off the GPUs, and the request device is a GPU when it matters below).
     index = device.index if device.type == "cuda" else -2
-    training = hooked = overridden = off_device = False
-    stack = [(model, False)]
-    pop, extend = stack.pop, stack.extend
-    while stack:
-        module, in_base = pop()
-        in_base = in_base or module is base
-        attrs = module.__dict__
-        training |= in_base and attrs["training"]
-        hooked |= attrs.get("_hf_hook") is not None
-        overridden |= in_base and "forward" in attrs
-        for p in attrs["_parameters"].values():
-            off_device |= p is not None and p.get_device() != index
-        extend((child, in_base) for child in attrs["_modules"].values() if child is not None)
+    inner, outer = [], []
+    for root, found in ((base, inner), (model, outer)):
+        stack = [root]
+        pop, push, add = stack.pop, stack.extend, found.append
+        while stack:
+            module = pop()
+            if module is None or (found is outer and module is base):
+                continue
+            attrs = module.__dict__
+            add(attrs)
+            push(attrs["_modules"].values())
+    training = True in [attrs["training"] for attrs in inner]
+    overridden = True in ["forward" in attrs for attrs in inner]
+    hooked = True in [attrs.get("_hf_hook") is not None for attrs in inner + outer]
+    off_device = True in [p is not None and p.get_device() != index
+                          for attrs in inner + outer for p in attrs["_parameters"].values()]
     if model.training or base.training or training:
         raise ValueError("packed executor requires eval mode on all decoder modules")
     config = model.config
