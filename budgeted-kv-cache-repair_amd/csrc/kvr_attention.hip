@@ -6,8 +6,10 @@
 // and indexed_causal_attention (indexed_attention.py:207-241).
 //
 // Work decomposition (host schedule, kvr_attention_schedule):
-//   selected rows are cut into groups of 64 (four tiles of 16 rows); group g
-//   needs keys [0, pos[last row of g] + 1). That key range is cut into chunks
+//   selected rows are cut into groups of 64 (four tiles of 16 rows) -- or, when
+//   so few rows would fill under half the grid, into 16-row groups for the
+//   split-key tile kernel below; group g needs keys
+//   [0, pos[last row of g] + 1). That key range is cut into chunks
 //   whose boundaries are multiples of 64 keys, sized so every chunk carries
 //   about the same cost (64-key sub-tiles weighted by how many of the group's
 //   row tiles still attend to them) and the whole grid is about one block per
@@ -26,18 +28,20 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 namespace kvr {
 namespace {
 
 constexpr int32_t kMagic = 0x4B565253;  // "KVRS"
-constexpr int32_t kVersion = 3;
-constexpr int kHeader = 16;
+constexpr int32_t kVersion = 4;
+constexpr int kHeader = 17;
 constexpr int kWorkInts = 4;               // (group, chunk, key_begin, key_end)
 constexpr int kRowTile = 16;               // rows per MFMA tile
 constexpr int kTilesPerGroup = 4;
-constexpr int kGroupRows = kRowTile * kTilesPerGroup;
+constexpr int kGroupRows = kRowTile * kTilesPerGroup;  // rows per group of the wide kernels
+constexpr int kTileGroupRows = kRowTile;               // rows per group of the split-key tile kernel
 constexpr int kSub = 64;                   // keys per LDS sub-tile
 constexpr int kMaxChunksPerGroup = 1024;   // merge weights fit in LDS
 #ifndef KVR_ATTN_TARGET_BLOCKS
@@ -65,7 +69,8 @@ enum Header {
     H_NMULTI,
     H_NKEYS,
     H_DTYPE,
-    H_MAXCHUNKS
+    H_MAXCHUNKS,
+    H_GROUP_ROWS
 };
 enum Kind { KIND_GENERIC = 0, KIND_MFMA = 1 };
 
@@ -81,8 +86,8 @@ struct AttnArgs {
     int64_t qs[3], ks[3], vs[3], os[3];  // {head,row,dim} element strides
     const int64_t* positions;
     const int32_t* sched;  // device schedule
-    float* ws_ml;          // [Hq][n_work][64] (m, l)
-    float* ws_o;           // [Hq][n_work][64][D]
+    float* ws_ml;          // [Hq][n_work][group_rows] (m, l)
+    float* ws_o;           // [Hq][n_work][group_rows][D]
     int64_t n_sel;
     int64_t n_keys;
     int32_t n_q_heads;
@@ -91,6 +96,7 @@ struct AttnArgs {
     int32_t n_head_groups;
     int32_t n_groups;
     int32_t n_work;
+    int32_t group_rows;  // rows per group: kGroupRows, or kTileGroupRows (tile kernel)
     int32_t head_dim;
     int32_t out_vec;  // output rows take 8-byte stores (unit dim stride, aligned)
     float scale_log2;  // scale * log2(e)
@@ -476,6 +482,232 @@ attn_mfma_kernel(AttnArgs a) {
 }
 
 // ===========================================================================
+// Split-key tile kernel (bf16 / fp16, head_dim 64 or 128) for schedules of
+// 16-row groups (few selected rows). Block = (KV head, head group, one 16-row
+// group, chunk); wave w serves query head w % QT over the keys of every other
+// 64-key sub-tile (key half w / QT): each iteration stages two sub-tiles (128
+// keys, double-buffered) and the two waves of a head attend one each. At the
+// end the second wave of each head hands its (m, l, O) to the first through
+// LDS, which combines them (rescaling both to the larger reference max) and
+// writes the output or the chunk's partial. With a quarter of the rows of the
+// wide kernel per block, a group needs a quarter of the chunks for the same
+// grid, so the partials (and the merge's reads) shrink 4x; the K/V of a chunk
+// is read by up to four groups, all on the XCD of its KV head (grid x).
+// ===========================================================================
+template <typename T, int D, int QT>
+__global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
+    using C = MfmaCfg<D, QT>;
+    using W = MfmaWave<T, D, QT>;
+    using v8 = typename W::v8;
+    constexpr int NT = C::threads;
+    extern __shared__ __align__(16) char smem[];
+    uint16_t* lds = reinterpret_cast<uint16_t*>(smem);  // [stage 2][sub-tile 2][buf_elems]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lq = lane & 15;
+    const int lj = lane >> 4;
+    const int hq = wave % QT;
+    const int kh = wave / QT;  // key half: sub-tiles 2i + kh
+
+    const int work = blockIdx.y;
+    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int grp = wk[0];
+    const int32_t key_begin = wk[2];
+    const int32_t key_end = wk[3];
+    const int n_chunks = group_table(a.sched)[2 * grp + 1];
+    const int kv_head = blockIdx.x / a.n_head_groups;
+    const int hg = blockIdx.x - kv_head * a.n_head_groups;
+    const int q_head = kv_head * a.group + hg * QT + hq;
+    const int64_t row0 = static_cast<int64_t>(grp) * kTileGroupRows;
+
+    const int32_t ks1 = static_cast<int32_t>(a.ks[1]);
+    const int32_t vs1 = static_cast<int32_t>(a.vs[1]);
+    const char* kbase = a.k + (static_cast<int64_t>(kv_head) * a.ks[0] + static_cast<int64_t>(key_begin) * a.ks[1]) * 2;
+    const char* vbase = a.v + (static_cast<int64_t>(kv_head) * a.vs[0] + static_cast<int64_t>(key_begin) * a.vs[1]) * 2;
+    const int32_t n_keys_chunk = key_end - key_begin;
+    const int n_sub = (n_keys_chunk + kSub - 1) / kSub;
+    const int n_it = (n_sub + 1) / 2;
+
+    u32x4 kr[2][C::kp], vr0[2][C::vp], vr1[2][C::vp];
+    // Global -> registers: sub-tiles 2i and 2i + 1 (zero beyond the chunk end).
+    auto load = [&](int i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int s = 2 * i + j;
+            const int32_t left = n_keys_chunk - kSub * s;
+            const char* kb = kbase + static_cast<int64_t>(kSub) * s * a.ks[1] * 2;
+            const char* vb = vbase + static_cast<int64_t>(kSub) * s * a.vs[1] * 2;
+#pragma unroll
+            for (int p = 0; p < C::kp; ++p) {
+                const int idx = tid + p * NT;
+                kr[j][p] = u32x4{0u, 0u, 0u, 0u};
+                if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
+                    const int kk = idx / C::c8;
+                    const int c8 = idx - kk * C::c8;
+                    if (kk < left) kr[j][p] = *reinterpret_cast<const u32x4*>(kb + (kk * ks1 + 8 * c8) * 2);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < C::vp; ++p) {
+                const int idx = tid + p * NT;
+                vr0[j][p] = u32x4{0u, 0u, 0u, 0u};
+                vr1[j][p] = u32x4{0u, 0u, 0u, 0u};
+                if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
+                    const int pr = idx & 31;
+                    const int c8 = idx >> 5;
+                    const int kk = 2 * pr;
+                    if (kk < left) vr0[j][p] = *reinterpret_cast<const u32x4*>(vb + (kk * vs1 + 8 * c8) * 2);
+                    if (kk + 1 < left) vr1[j][p] = *reinterpret_cast<const u32x4*>(vb + ((kk + 1) * vs1 + 8 * c8) * 2);
+                }
+            }
+        }
+    };
+    // Registers -> LDS stage: per sub-tile K as is, V transposed (key pairs packed per dim).
+    auto store = [&](uint16_t* stage) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint16_t* Ks = stage + j * C::buf_elems;
+            uint16_t* Vt = Ks + C::k_elems;
+#pragma unroll
+            for (int p = 0; p < C::kp; ++p) {
+                const int idx = tid + p * NT;
+                if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
+                    const int kk = idx / C::c8;
+                    const int c8 = idx - kk * C::c8;
+                    *reinterpret_cast<u32x4*>(Ks + kk * C::kstr + 8 * c8) = kr[j][p];
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < C::vp; ++p) {
+                const int idx = tid + p * NT;
+                if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
+                    const int pr = idx & 31;
+                    const int c8 = idx >> 5;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t x0 = vr0[j][p][q], x1 = vr1[j][p][q];
+                        uint16_t* col = Vt + (8 * c8 + 2 * q) * C::vstr + 2 * pr;
+                        *reinterpret_cast<uint32_t*>(col) = (x0 & 0xffffu) | (x1 << 16);
+                        *reinterpret_cast<uint32_t*>(col + C::vstr) = (x0 >> 16) | (x1 & 0xffff0000u);
+                    }
+                }
+            }
+        }
+    };
+
+    // One row tile per wave (tile slot 0 of MfmaWave; slot 1 stays inactive).
+    W w;
+    {
+        const int64_t row = row0 + lq;
+        w.kmax[0] = rows_kmax(a, row0, kRowTile);
+        w.nomask_end[0] = (row0 + kRowTile <= a.n_sel) ? static_cast<int32_t>(a.positions[row0] + 1) : 0;
+        w.pos[0] = (row < a.n_sel) ? static_cast<int32_t>(a.positions[row]) : -1;
+        w.m_run[0] = -INFINITY;
+        w.l_run[0] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < W::DT; ++dt) w.o[0][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < W::DS; ++ds) {
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (row < a.n_sel) {
+                const int64_t off = q_head * a.qs[0] + row * a.qs[1] + (32 * ds + 8 * lj);
+                raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
+            }
+            w.qf[0][ds] = __builtin_bit_cast(v8, raw);
+        }
+    }
+
+    if (n_it > 0) {
+        load(0);
+        store(lds);
+    }
+    for (int i = 0; i < n_it; ++i) {
+        const bool more = i + 1 < n_it;
+        if (more) load(i + 1);
+        __syncthreads();  // stage i is staged; stage (i + 1) & 1 is no longer read
+        const int s = 2 * i + kh;
+        const int32_t key0 = key_begin + kSub * s;
+        if (s < n_sub && key0 < w.kmax[0]) {
+            const uint16_t* Ks = lds + ((i & 1) * 2 + kh) * C::buf_elems;
+            const uint16_t* Vt = Ks + C::k_elems;
+            if (key0 + kSub > w.nomask_end[0])
+                w.template step<true, false, true>(Ks, Vt, key0, lq, lj, a.scale_log2);
+            else
+                w.template step<true, false, false>(Ks, Vt, key0, lq, lj, a.scale_log2);
+        }
+        if (more) store(lds + ((i + 1) & 1) * 2 * C::buf_elems);
+    }
+
+    // ---- combine the two key halves of each head, then output or partial ----
+    {
+        float l = w.l_run[0];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        w.l_run[0] = l;
+    }
+    constexpr int kX = W::DT * 4 + 2;  // exchanged floats per lane: O, m, l
+    float* xch = reinterpret_cast<float*>(smem) + hq * kX * 64;  // [field][lane] per head
+    __syncthreads();  // every wave is done with the K/V stages
+    if (kh == 1) {
+#pragma unroll
+        for (int dt = 0; dt < W::DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xch[(4 * dt + i) * 64 + lane] = w.o[0][dt][i];
+        xch[(kX - 2) * 64 + lane] = w.m_run[0];
+        xch[(kX - 1) * 64 + lane] = w.l_run[0];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    {
+        const float mb = xch[(kX - 2) * 64 + lane];
+        const float lb = xch[(kX - 1) * 64 + lane];
+        const float ma = w.m_run[0];
+        const float m = fmaxf(ma, mb);
+        if (m != -INFINITY) {  // some key of the chunk is visible to this row
+            const float fa = __builtin_amdgcn_exp2f(ma - m);  // exp2(-inf) = 0 for an empty half
+            const float fb = __builtin_amdgcn_exp2f(mb - m);
+#pragma unroll
+            for (int dt = 0; dt < W::DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w.o[0][dt][i] = w.o[0][dt][i] * fa + xch[(4 * dt + i) * 64 + lane] * fb;
+            w.l_run[0] = w.l_run[0] * fa + lb * fb;
+            w.m_run[0] = m;
+        }
+    }
+    const int r = lq;  // row within the group
+    const int64_t row = row0 + r;
+    if (w.kmax[0] <= key_begin || row >= a.n_sel) return;  // the row does not attend into this chunk
+    if (n_chunks == 1) {
+        const float inv = 1.f / w.l_run[0];
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + q_head * a.os[0] + row * a.os[1];
+#pragma unroll
+        for (int dt = 0; dt < W::DT; ++dt) {
+            uint16_t e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[i] = elem<T>::from_float(w.o[0][dt][i] * inv);
+            if (a.out_vec) {
+                *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * lj) =
+                    uint2{e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16)};
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[(16 * dt + 4 * lj + i) * a.os[2]] = e[i];
+            }
+        }
+    } else {
+        const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kTileGroupRows + r;
+        float* po = a.ws_o + slot * D;
+#pragma unroll
+        for (int dt = 0; dt < W::DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lj) = w.o[0][dt];
+        if (lj == 0) {
+            a.ws_ml[slot * 2 + 0] = w.m_run[0];
+            a.ws_ml[slot * 2 + 1] = w.l_run[0];
+        }
+    }
+}
+
+// ===========================================================================
 // Generic kernel (vector ALU; fp32 / fp16 / bf16, any head_dim <= 256).
 // Same work items as the MFMA kernel. 256 threads: thread t owns query
 // (tile t/64, head (t%64)/16, row t%16); K/V staged in LDS as fp32.
@@ -503,12 +735,12 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
     const int kv_head = blockIdx.x / a.n_head_groups;
     const int hg = blockIdx.x - kv_head * a.n_head_groups;
 
-    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
+    const int64_t group_row0 = static_cast<int64_t>(grp) * a.group_rows;
     const int tile = tid / 64;
     const int h = (tid % 64) / kRowTile;
     const int r = tile * kRowTile + (tid % kRowTile);
     const int64_t row = group_row0 + r;
-    const bool live = h < a.qt && row < a.n_sel;
+    const bool live = h < a.qt && r < a.group_rows && row < a.n_sel;
     const int64_t pos = live ? a.positions[row] : int64_t(-1);
     const int q_head = kv_head * a.group + hg * a.qt + h;
 
@@ -571,7 +803,7 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
         for (int d = 0; d < DMAX; ++d)
             if (d < D) op[q_head * a.os[0] + row * a.os[1] + d * a.os[2]] = E::from_float(acc[d] / l_run);
     } else {
-        const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * kGroupRows + r;
+        const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * a.group_rows + r;
 #pragma unroll
         for (int d = 0; d < DMAX; ++d)
             if (d < D) a.ws_o[slot * D + d] = acc[d];
@@ -607,11 +839,12 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     extern __shared__ __align__(16) char smem[];
     const int D = a.head_dim;
     const int RB = merge_rows_per_block(D, VEC);
-    const int blocks_per_group = a.qt * ((kGroupRows + RB - 1) / RB);
+    const int GR = a.group_rows;
+    const int blocks_per_group = a.qt * ((GR + RB - 1) / RB);
     const int grp = blockIdx.y / blocks_per_group;
     const int rem = blockIdx.y - grp * blocks_per_group;
-    const int hq = rem / ((kGroupRows + RB - 1) / RB);
-    const int r0 = (rem - hq * ((kGroupRows + RB - 1) / RB)) * RB;  // first row (within the group)
+    const int hq = rem / ((GR + RB - 1) / RB);
+    const int r0 = (rem - hq * ((GR + RB - 1) / RB)) * RB;  // first row (within the group)
     const int kv_head = blockIdx.x / a.n_head_groups;
     const int hg = blockIdx.x - kv_head * a.n_head_groups;
     const int q_head = kv_head * a.group + hg * a.qt + hq;
@@ -624,9 +857,9 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     float* W = Red + RB * kSlices * D;                     // [RB][n_chunks]
     float* Linv = W + RB * n_chunks;                       // [RB]
     int* NV = reinterpret_cast<int*>(Linv + RB);           // [RB] attended chunks
-    const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * kGroupRows;
-    const int64_t group_row0 = static_cast<int64_t>(grp) * kGroupRows;
-    const int64_t cstride = static_cast<int64_t>(kGroupRows);
+    const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * GR;
+    const int64_t group_row0 = static_cast<int64_t>(grp) * GR;
+    const int64_t cstride = static_cast<int64_t>(GR);
 
     // phase 1: one wave per row
     const int wave = threadIdx.x / 64;
@@ -635,7 +868,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
         const int r = r0 + rr;
         const int64_t row = group_row0 + r;
         int nv = 0;
-        if (r < kGroupRows && row < a.n_sel) {
+        if (r < GR && row < a.n_sel) {
             const int32_t tk = rows_kmax(a, group_row0 + (r / kRowTile) * kRowTile, kRowTile);
             // chunk starts increase, so the attended chunks are the count of starts below tk
             for (int c0 = 0; c0 < n_chunks; c0 += 64) {
@@ -668,7 +901,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
         const int d = (e % dv) * VEC;
         const int r = r0 + rr;
         fvec acc = {};
-        if (r < kGroupRows && group_row0 + r < a.n_sel) {
+        if (r < GR && group_row0 + r < a.n_sel) {
             const int nv = NV[rr];
             const float* po = a.ws_o + (slot0 + r) * D + d;
             const float* w = W + rr * n_chunks;
@@ -684,7 +917,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
         const int d = e - rr * D;
         const int r = r0 + rr;
         const int64_t row = group_row0 + r;
-        if (r >= kGroupRows || row >= a.n_sel) continue;
+        if (r >= GR || row >= a.n_sel) continue;
         float sum = 0.f;
 #pragma unroll
         for (int sl = 0; sl < kSlices; ++sl) sum += Red[(rr * kSlices + sl) * D + d];
@@ -731,8 +964,24 @@ int launch_mfma_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
     return launch_status();
 }
 
+template <typename T, int D, int QT>
+int launch_tile_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
+    using C = MfmaCfg<D, QT>;
+    constexpr size_t bytes = 2 * static_cast<size_t>(C::bytes);  // two sub-tiles per stage
+    static_assert(bytes >= static_cast<size_t>(QT) * (D / 16 * 4 + 2) * 64 * 4, "head exchange fits");
+    static const bool ok = allow_lds(attn_tile_kernel<T, D, QT>, bytes);
+    if (!ok) return KVR_E_LAUNCH_FAILED;
+    attn_tile_kernel<T, D, QT><<<grid, C::threads, bytes, s>>>(a);
+    return launch_status();
+}
+
 template <typename T, int D>
 int launch_mfma(const AttnArgs& a, int qt, dim3 grid, hipStream_t s) {
+    if (a.group_rows == kTileGroupRows) {
+        if (qt == 4) return launch_tile_inst<T, D, 4>(a, grid, s);
+        if (qt == 2) return launch_tile_inst<T, D, 2>(a, grid, s);
+        return launch_tile_inst<T, D, 1>(a, grid, s);
+    }
     if (qt == 4) return launch_mfma_inst<T, D, 4>(a, grid, s);
     if (qt == 2) return launch_mfma_inst<T, D, 2>(a, grid, s);
     return launch_mfma_inst<T, D, 1>(a, grid, s);
@@ -769,7 +1018,7 @@ int launch_merge_vec(const AttnArgs& a, int max_chunks, hipStream_t s) {
     static const bool ok = allow_lds(attn_merge_kernel<T, VEC>, merge_lds_bytes(kMaxChunksPerGroup, 256, VEC));
     if (!ok) return KVR_E_LAUNCH_FAILED;
     const int rb = merge_rows_per_block(a.head_dim, VEC);
-    const unsigned y = static_cast<unsigned>(a.n_groups) * a.qt * ((kGroupRows + rb - 1) / rb);
+    const unsigned y = static_cast<unsigned>(a.n_groups) * a.qt * ((a.group_rows + rb - 1) / rb);
     if (y > 65535u) return KVR_E_UNSUPPORTED_SHAPE;
     dim3 grid(a.n_q_heads / a.qt, y);
     attn_merge_kernel<T, VEC><<<grid, kMergeThreads, merge_lds_bytes(max_chunks, a.head_dim, VEC), s>>>(a);
@@ -781,19 +1030,20 @@ int launch_merge(const AttnArgs& a, int max_chunks, hipStream_t s) {
     return a.head_dim % 4 == 0 ? launch_merge_vec<T, 4>(a, max_chunks, s) : launch_merge_vec<T, 1>(a, max_chunks, s);
 }
 
-// Per-group causal limits on the host: group limit and the limits of its four row tiles.
+// Per-group causal limits on the host: group limit and the limits of its row
+// tiles (group_rows / 16 of them; unused entries 0).
 struct GroupKeys {
     int64_t kmax;
     int64_t tile_kmax[kTilesPerGroup];
 };
 
-GroupKeys group_keys(const int64_t* positions, int64_t n_sel, int64_t g) {
+GroupKeys group_keys(const int64_t* positions, int64_t n_sel, int64_t g, int group_rows) {
     GroupKeys k;
-    const int64_t last = (g + 1) * kGroupRows - 1 < n_sel ? (g + 1) * kGroupRows - 1 : n_sel - 1;
+    const int64_t last = (g + 1) * group_rows - 1 < n_sel ? (g + 1) * group_rows - 1 : n_sel - 1;
     k.kmax = positions[last] + 1;
     for (int t = 0; t < kTilesPerGroup; ++t) {
-        const int64_t row0 = g * kGroupRows + t * kRowTile;
-        if (row0 >= n_sel) {
+        const int64_t row0 = g * group_rows + t * kRowTile;
+        if (t * kRowTile >= group_rows || row0 >= n_sel) {
             k.tile_kmax[t] = 0;
             continue;
         }
@@ -841,11 +1091,17 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     const int group = n_q_heads / n_kv_heads;
     const int qt = pick_qt(group);
     const int n_head_groups = group / qt;
-    const int64_t n_groups = (n_sel + kGroupRows - 1) / kGroupRows;
     const int64_t heads = static_cast<int64_t>(n_kv_heads) * n_head_groups;
+    // Few rows (64-row groups x heads fill under half the grid): 16-row groups
+    // for the split-key tile kernel, so a group needs 4x fewer key chunks for
+    // the same grid and writes 4x less partial data; the chunk's K/V is then
+    // read by up to 4 row groups, from the L2 of the head's XCD.
+    const int64_t wide_units = (n_sel + kGroupRows - 1) / kGroupRows * heads;
+    const int group_rows = (mfma && 2 * wide_units <= kTargetBlocks) ? kTileGroupRows : kGroupRows;
+    const int64_t n_groups = (n_sel + group_rows - 1) / group_rows;
 
     std::vector<GroupKeys> keys(static_cast<size_t>(n_groups));
-    for (int64_t g = 0; g < n_groups; ++g) keys[g] = group_keys(positions, n_sel, g);
+    for (int64_t g = 0; g < n_groups; ++g) keys[g] = group_keys(positions, n_sel, g, group_rows);
 
     std::vector<Chunk> chunks;
     if (chunk_keys > 0) {
@@ -880,13 +1136,28 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
             total += group_cost[g];
         }
         const int64_t per_head = kTargetBlocks / heads > 1 ? kTargetBlocks / heads : 1;
-        const int64_t cap = (total + per_head - 1) / per_head;
-        for (int64_t g = 0; g < n_groups; ++g) {
+        auto chunks_of = [&](int64_t g, int64_t cap) {
             const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
             int64_t nc = (group_cost[g] + cap - 1) / cap;
             nc = nc < 1 ? 1 : nc;
             nc = nc > n_sub ? n_sub : nc;
-            nc = nc > kMaxChunksPerGroup ? kMaxChunksPerGroup : nc;
+            return nc > kMaxChunksPerGroup ? int64_t(kMaxChunksPerGroup) : nc;
+        };
+        // Per-chunk cost cap: the even share of the total. The tile kernel
+        // (one block per CU) raises it until the groups' rounded-up chunk
+        // counts fit the share too (no second, partial round of blocks), or
+        // every group is one chunk; the wide kernel runs two blocks per CU.
+        int64_t cap = (total + per_head - 1) / per_head;
+        const int64_t max_cost = *std::max_element(group_cost.begin(), group_cost.end());
+        while (group_rows == kTileGroupRows) {
+            int64_t sum = 0;
+            for (int64_t g = 0; g < n_groups; ++g) sum += chunks_of(g, cap);
+            if (sum <= per_head || cap >= max_cost) break;
+            cap += (cap + 15) / 16;
+        }
+        for (int64_t g = 0; g < n_groups; ++g) {
+            const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
+            const int64_t nc = chunks_of(g, cap);
             // Boundary i closes the chunk once the running cost reaches i/nc of
             // the group's cost, leaving at least one sub-tile per later chunk.
             int64_t s = 0, acc = 0;
@@ -942,6 +1213,7 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     h[H_NKEYS] = static_cast<int32_t>(n_keys);
     h[H_DTYPE] = dtype;
     h[H_MAXCHUNKS] = static_cast<int32_t>(max_chunks);
+    h[H_GROUP_ROWS] = group_rows;
     int32_t* groups = h + kHeader;
     int32_t* works = groups + 2 * n_groups;
     for (int64_t g = 0; g < n_groups; ++g) {
@@ -962,8 +1234,9 @@ extern "C" int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_
     if (!schedule || schedule_len < kHeader || schedule[H_MAGIC] != kMagic || schedule[H_VERSION] != kVersion)
         return KVR_E_BAD_SCHEDULE;
     if (schedule[H_HQ] != n_q_heads || schedule[H_D] != head_dim) return KVR_E_BAD_SCHEDULE;
+    if (schedule[H_GROUP_ROWS] != kGroupRows && schedule[H_GROUP_ROWS] != kTileGroupRows) return KVR_E_BAD_SCHEDULE;
     if (schedule[H_NMULTI] == 0) return 0;
-    return static_cast<int64_t>(n_q_heads) * schedule[H_NWORK] * kGroupRows * (head_dim + 2) * 4;
+    return static_cast<int64_t>(n_q_heads) * schedule[H_NWORK] * schedule[H_GROUP_ROWS] * (head_dim + 2) * 4;
 }
 
 extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const void* v, void* out,
@@ -1016,11 +1289,12 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     a.n_head_groups = hs[H_NHG];
     a.n_groups = hs[H_NGROUPS];
     a.n_work = hs[H_NWORK];
+    a.group_rows = hs[H_GROUP_ROWS];
     a.head_dim = head_dim;
     a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
     if (ws_need > 0) {
         a.ws_ml = static_cast<float*>(workspace);
-        a.ws_o = a.ws_ml + static_cast<int64_t>(n_q_heads) * a.n_work * kGroupRows * 2;
+        a.ws_o = a.ws_ml + static_cast<int64_t>(n_q_heads) * a.n_work * a.group_rows * 2;
     }
     if (a.qt <= 0 || a.qt * a.n_head_groups != a.group) return KVR_E_BAD_SCHEDULE;
 

@@ -150,12 +150,14 @@ def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
     (list(range(0, 40000, 37)), 40000, 0), ([7], 8, 0)])
 def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_keys, chunk):
     s = schedule(positions, n_keys, 32, 8, 128, chunk=chunk)
-    header, n_groups, longest, n_work = s[:16], s[3], s[4], s[5]
-    assert header[0] == 0x4B565253 and header[1] == 3 and header[2] == len(positions)
-    assert n_groups == (len(positions) + 63) // 64
-    assert len(s) == 16 + 2 * n_groups + 4 * n_work
-    groups = [(s[16 + 2 * g], s[17 + 2 * g]) for g in range(n_groups)]
-    work = [tuple(s[16 + 2 * n_groups + 4 * w:20 + 2 * n_groups + 4 * w]) for w in range(n_work)]
+    header, n_groups, longest, n_work, rows = s[:17], s[3], s[4], s[5], s[16]
+    assert header[0] == 0x4B565253 and header[1] == 4 and header[2] == len(positions)
+    # 16-row groups (tile kernel) while 64-row groups x 8 heads would fill at most half of 256 blocks
+    assert rows == (16 if 2 * 8 * ((len(positions) + 63) // 64) <= 256 else 64)
+    assert n_groups == (len(positions) + rows - 1) // rows
+    assert len(s) == 17 + 2 * n_groups + 4 * n_work
+    groups = [(s[17 + 2 * g], s[18 + 2 * g]) for g in range(n_groups)]
+    work = [tuple(s[17 + 2 * n_groups + 4 * w:21 + 2 * n_groups + 4 * w]) for w in range(n_work)]
     assert len(work) == n_work == sum(c for _, c in groups) and header[15] == max(c for _, c in groups)
     assert longest == max(e - b for _, _, b, e in work)
     for g, (base, count) in enumerate(groups):
@@ -163,7 +165,7 @@ def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_k
         # the work items of group g are its chunks 0..c-1 in key order, contiguous from
         # its base; they tile [0, last causal key + 1) with boundaries on 64-key multiples
         assert [(grp, i) for grp, i, _, _ in chunks] == [(g, c) for c in range(count)]
-        last = positions[min(64 * g + 63, len(positions) - 1)]
+        last = positions[min(rows * g + rows - 1, len(positions) - 1)]
         assert chunks[0][2] == 0 and chunks[-1][3] == last + 1
         assert all(a[3] == b[2] for a, b in zip(chunks, chunks[1:]))
         assert all(b < e and b % 64 == 0 for _, _, b, e in chunks)
@@ -171,7 +173,7 @@ def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_k
             assert all(e - b == chunk for _, _, b, e in chunks[:-1]) and chunks[-1][3] - chunks[-1][2] <= chunk
     # every (row, key <= pos) pair lies in exactly one chunk of its group
     for r, p in enumerate(positions):
-        base, count = groups[r // 64]
+        base, count = groups[r // rows]
         for key in (0, p // 2, p):
             assert sum(1 for _, _, b, e in work[base:base + count] if b <= key < e) == 1
     assert header[12] == sum(1 for _, c in groups if c > 1)  # groups needing a merge
@@ -183,16 +185,24 @@ def test_default_chunking_keeps_one_block_per_cu_for_the_c3_support():
     slots = sorted(random.Random(2).sample(range(5632 // 8), 16))
     positions = [2048 + 8 * k + i for k in slots for i in range(4)]
     s = schedule(positions, 7680, 32, 8, 128)
-    n_work = s[5]
+    n_groups, n_work = s[3], s[5]
+    assert s[16] == 16 and n_groups == 4  # 64 rows: four 16-row groups for the tile kernel
     assert 24 * 8 <= n_work * 8 <= 256
-    # chunks are cost balanced: keys attended by all four row tiles cost more, so
-    # the chunks over the early keys are no longer than those over the late keys
-    work = [tuple(s[18 + 4 * w:22 + 4 * w]) for w in range(n_work)]
-    lengths = [e - b for _, _, b, e in work]
-    assert lengths[0] <= lengths[-2]
+    # chunks are cost balanced: one row tile per group, so every chunk carries about
+    # the same number of keys (whole 64-key sub-tiles, the group's last one shorter)
+    work = [tuple(s[17 + 2 * n_groups + 4 * w:21 + 2 * n_groups + 4 * w]) for w in range(n_work)]
+    lengths = [e - b for g, c, b, e in work if c + 1 < s[18 + 2 * g]]  # all but each group's last chunk
+    assert max(lengths) - min(lengths) <= 64
     # a group that fits one block's share is never split
     s = schedule(list(range(15104)), 16128, 32, 8, 128)
-    assert s[12] == 0 and s[5] == s[3]
+    assert s[16] == 64 and s[12] == 0 and s[5] == s[3]
+
+
+def test_generic_schedules_keep_64_row_groups():
+    s = schedule(list(range(0, 640, 10)), 640, 32, 8, 128, dtype=0)  # fp32: vector-ALU kernel
+    assert s[16] == 64 and s[3] == 1
+    s = schedule(list(range(0, 640, 10)), 640, 32, 8, 96)  # head_dim 96: vector-ALU kernel
+    assert s[16] == 64
 
 
 def test_schedule_rejects_unsorted_or_out_of_range_positions():
@@ -212,7 +222,8 @@ def test_workspace_is_zero_when_every_tile_fits_one_chunk():
     assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 0
     s = schedule(list(range(0, 8000, 100)), 8000, 4, 2, 64, chunk=256)
     buf = (ctypes.c_int32 * len(s))(*s)
-    assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 64 * 66 * 4
+    assert s[16] == 16
+    assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 16 * 66 * 4
 
 
 def test_decoder_layer_descriptors_validate_before_any_launch():
