@@ -94,49 +94,55 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
     const int64_t lo_off = static_cast<int64_t>(c) * EPV;
     const int64_t hi_off = lo_off + half;
 
+    // Issue every load first (the row's position, its q/k/v chunks or their
+    // fp32 partials, the cos/sin chunks) so the thread waits once; the
+    // position is checked only before the store.
+    const int64_t pos = part == 0 ? 0 : a.positions[r];
     const char* src = nullptr;
-    char* dst;
-    if (part == 0) {
-        if (!a.src.base) src = a.q + (h * a.qs[0] + r * a.qs[1]) * E::size;
-        dst = a.q_out + (h * a.qos[0] + r * a.qos[1]) * E::size;
-    } else {
-        const int kv = part - 1;
-        const int64_t pos = a.positions[r];
-        if (pos < 0 || pos >= a.n_keys) return;
-        if (!a.src.base) src = a.fresh[kv] + (h * a.fs[kv][0] + r * a.fs[kv][1]) * E::size;
-        dst = a.out[kv] + (h * a.os[kv][0] + pos * a.os[kv][1]) * E::size;
-    }
-    u32x4 lo, hi;
-    if constexpr (EPV == 8) {
-        if (a.src.base) {  // the projection's output, rounded as its reduce kernel rounds it
-            const int64_t col = a.part_col[part] + h * a.head_dim;
-            float sums[8];
-            bits b[EPV];
-            partial_sum8(a.src, r, col + lo_off, sums);
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sums[e]);
-            __builtin_memcpy(&lo, b, 16);
-            partial_sum8(a.src, r, col + hi_off, sums);
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sums[e]);
-            __builtin_memcpy(&hi, b, 16);
-        }
-    }
+    if (!a.src.base)
+        src = part == 0 ? a.q + (h * a.qs[0] + r * a.qs[1]) * E::size
+                        : a.fresh[part - 1] + (h * a.fs[part - 1][0] + r * a.fs[part - 1][1]) * E::size;
+    u32x4 lo, hi, c_lo, c_hi, s_lo, s_hi;
     if (src) {
         lo = *reinterpret_cast<const u32x4*>(src + lo_off * E::size);
         hi = *reinterpret_cast<const u32x4*>(src + hi_off * E::size);
+    }
+    if (part != 2) {
+        const char* crow = a.cos + r * a.cs[0] * E::size;
+        const char* srow = a.sin + r * a.ss[0] * E::size;
+        c_lo = *reinterpret_cast<const u32x4*>(crow + lo_off * E::size);
+        c_hi = *reinterpret_cast<const u32x4*>(crow + hi_off * E::size);
+        s_lo = *reinterpret_cast<const u32x4*>(srow + lo_off * E::size);
+        s_hi = *reinterpret_cast<const u32x4*>(srow + hi_off * E::size);
+    }
+    if constexpr (EPV == 8) {
+        if (a.src.base) {  // the projection's output, rounded as its reduce kernel rounds it
+            const int64_t col = a.part_col[part] + h * a.head_dim;
+            float sl8[8], sh8[8];
+            partial_sum8(a.src, r, col + lo_off, sl8);
+            partial_sum8(a.src, r, col + hi_off, sh8);
+            bits b[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sl8[e]);
+            __builtin_memcpy(&lo, b, 16);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sh8[e]);
+            __builtin_memcpy(&hi, b, 16);
+        }
+    }
+    char* dst;
+    if (part == 0) {
+        dst = a.q_out + (h * a.qos[0] + r * a.qos[1]) * E::size;
+    } else {
+        const int kv = part - 1;
+        if (pos < 0 || pos >= a.n_keys) return;
+        dst = a.out[kv] + (h * a.os[kv][0] + pos * a.os[kv][1]) * E::size;
     }
     if (part == 2) {  // values: bit copy
         *reinterpret_cast<u32x4*>(dst + lo_off * E::size) = lo;
         *reinterpret_cast<u32x4*>(dst + hi_off * E::size) = hi;
         return;
     }
-    const char* crow = a.cos + r * a.cs[0] * E::size;
-    const char* srow = a.sin + r * a.ss[0] * E::size;
-    const u32x4 c_lo = *reinterpret_cast<const u32x4*>(crow + lo_off * E::size);
-    const u32x4 c_hi = *reinterpret_cast<const u32x4*>(crow + hi_off * E::size);
-    const u32x4 s_lo = *reinterpret_cast<const u32x4*>(srow + lo_off * E::size);
-    const u32x4 s_hi = *reinterpret_cast<const u32x4*>(srow + hi_off * E::size);
     bits xl[EPV], xh[EPV], cl[EPV], ch[EPV], sl[EPV], sh[EPV], ol[EPV], oh[EPV];
     __builtin_memcpy(xl, &lo, 16);
     __builtin_memcpy(xh, &hi, 16);

@@ -104,6 +104,29 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, 
     char* res_out = a.residual ? a.residual_out + row * a.ro_stride * E::size : nullptr;
     char* out = a.out + row * a.o_stride * E::size;
 
+    // Every load of the row is issued before any of it is used (weight,
+    // residual, x or the fp32 partials), so the block pays one memory round
+    // trip; the residual sums are stored after the last load.
+    u32x4 wv[NV], rv[NV], xv[NV];
+    float xs[NV][V];
+    const bool use_partials = V == 8 && a.px.base != nullptr;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int j = t + k * tpr;
+        if (!live || j >= nvec) continue;
+        wv[k] = *reinterpret_cast<const u32x4*>(a.weight + static_cast<int64_t>(j) * 16);
+        if (res) rv[k] = *reinterpret_cast<const u32x4*>(res + static_cast<int64_t>(j) * 16);
+        if (!use_partials) xv[k] = *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(j) * 16);
+    }
+    if constexpr (V == 8) {
+        if (use_partials) {  // the projection's output elements, rounded as its reduce kernel rounds them
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const int j = t + k * tpr;
+                if (live && j < nvec) partial_sum8(a.px, row, static_cast<int64_t>(j) * 8, xs[k]);
+            }
+        }
+    }
     float v[NV][V];
     float ss = 0.f;
 #pragma unroll
@@ -111,38 +134,34 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, 
         const int j = t + k * tpr;
         if (!live || j >= nvec) continue;
         bits xb[V];
-        bool from_partials = false;
-        if constexpr (V == 8) {
-            if (a.px.base) {  // the projection's output element, rounded as its reduce kernel rounds it
-                float sums[8];
-                partial_sum8(a.px, row, static_cast<int64_t>(j) * 8, sums);
+        if (use_partials) {
 #pragma unroll
-                for (int e = 0; e < V; ++e) xb[e] = E::from_float(sums[e]);
-                from_partials = true;
-            }
-        }
-        if (!from_partials) {
-            const u32x4 xv = *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(j) * 16);
-            __builtin_memcpy(xb, &xv, 16);
+            for (int e = 0; e < V; ++e) xb[e] = E::from_float(xs[k][e]);
+        } else {
+            __builtin_memcpy(xb, &xv[k], 16);
         }
         if (res) {
-            const u32x4 rv = *reinterpret_cast<const u32x4*>(res + static_cast<int64_t>(j) * 16);
             bits rb[V], sb[V];
-            __builtin_memcpy(rb, &rv, 16);
+            __builtin_memcpy(rb, &rv[k], 16);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 sb[e] = E::from_float(E::to_float(rb[e]) + E::to_float(xb[e]));  // residual + hidden_states
                 v[k][e] = E::to_float(sb[e]);
             }
-            u32x4 sv;
-            __builtin_memcpy(&sv, sb, 16);
-            *reinterpret_cast<u32x4*>(res_out + static_cast<int64_t>(j) * 16) = sv;
+            __builtin_memcpy(&rv[k], sb, 16);  // now the sum, stored below
         } else {
 #pragma unroll
             for (int e = 0; e < V; ++e) v[k][e] = E::to_float(xb[e]);
         }
 #pragma unroll
         for (int e = 0; e < V; ++e) ss += v[k][e] * v[k][e];
+    }
+    if (res) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int j = t + k * tpr;
+            if (live && j < nvec) *reinterpret_cast<u32x4*>(res_out + static_cast<int64_t>(j) * 16) = rv[k];
+        }
     }
     const int width = tpr < 64 ? tpr : 64;
     for (int off = width >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, width);
@@ -160,9 +179,8 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, 
     for (int k = 0; k < NV; ++k) {
         const int j = t + k * tpr;
         if (j >= nvec) continue;
-        const u32x4 wv = *reinterpret_cast<const u32x4*>(a.weight + static_cast<int64_t>(j) * 16);
         bits wb[V], ob[V];
-        __builtin_memcpy(wb, &wv, 16);
+        __builtin_memcpy(wb, &wv[k], 16);
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             const float y = round_through<T>(v[k][e] * inv);  // .to(input_dtype)
