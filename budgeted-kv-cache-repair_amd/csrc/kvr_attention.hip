@@ -332,46 +332,48 @@ attn_mfma_kernel(AttnArgs a) {
     const int n_sub = (n_keys_chunk + kSub - 1) / kSub;
 
     u32x4 kr[C::kp], vr0[C::vp], vr1[C::vp];
-    // Global -> registers: sub-tile s (zero beyond the chunk end).
+    // Global -> registers: sub-tile s. The loads are unconditional (key rows
+    // past the chunk end re-read its last row, in bounds) so the wait for them
+    // sits at the LDS store, after the step's compute; store() zeroes those
+    // rows. Conditional loads would make the compiler wait for them at once.
     auto load = [&](int s) {
-        const int32_t left = n_keys_chunk - kSub * s;
-        const char* kb = kbase + static_cast<int64_t>(kSub) * s * a.ks[1] * 2;
-        const char* vb = vbase + static_cast<int64_t>(kSub) * s * a.vs[1] * 2;
 #pragma unroll
         for (int p = 0; p < C::kp; ++p) {
             const int idx = tid + p * NT;
-            kr[p] = u32x4{0u, 0u, 0u, 0u};
             if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
                 const int kk = idx / C::c8;
                 const int c8 = idx - kk * C::c8;
-                if (kk < left) kr[p] = *reinterpret_cast<const u32x4*>(kb + (kk * ks1 + 8 * c8) * 2);
+                const int32_t key = min(kSub * s + kk, n_keys_chunk - 1);
+                kr[p] = *reinterpret_cast<const u32x4*>(kbase + (static_cast<int64_t>(key) * ks1 + 8 * c8) * 2);
             }
         }
 #pragma unroll
         for (int p = 0; p < C::vp; ++p) {
             const int idx = tid + p * NT;
-            vr0[p] = u32x4{0u, 0u, 0u, 0u};
-            vr1[p] = u32x4{0u, 0u, 0u, 0u};
             if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
                 const int pr = idx & 31;
                 const int c8 = idx >> 5;
-                const int kk = 2 * pr;
-                if (kk < left) vr0[p] = *reinterpret_cast<const u32x4*>(vb + (kk * vs1 + 8 * c8) * 2);
-                if (kk + 1 < left) vr1[p] = *reinterpret_cast<const u32x4*>(vb + ((kk + 1) * vs1 + 8 * c8) * 2);
+                const int32_t k0 = min(kSub * s + 2 * pr, n_keys_chunk - 1);
+                const int32_t k1 = min(kSub * s + 2 * pr + 1, n_keys_chunk - 1);
+                vr0[p] = *reinterpret_cast<const u32x4*>(vbase + (static_cast<int64_t>(k0) * vs1 + 8 * c8) * 2);
+                vr1[p] = *reinterpret_cast<const u32x4*>(vbase + (static_cast<int64_t>(k1) * vs1 + 8 * c8) * 2);
             }
         }
     };
-    // Registers -> LDS buffer: K as is, V transposed (key pairs packed per dim).
-    auto store = [&](uint16_t* buf) {
+    // Registers -> LDS buffer of sub-tile s: K as is, V transposed (key pairs
+    // packed per dim); rows past the chunk end are zeroed.
+    auto store = [&](uint16_t* buf, int s) {
         uint16_t* Ks = buf;
         uint16_t* Vt = buf + C::k_elems;
+        const int32_t left = n_keys_chunk - kSub * s;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int p = 0; p < C::kp; ++p) {
             const int idx = tid + p * NT;
             if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
                 const int kk = idx / C::c8;
                 const int c8 = idx - kk * C::c8;
-                *reinterpret_cast<u32x4*>(Ks + kk * C::kstr + 8 * c8) = kr[p];
+                *reinterpret_cast<u32x4*>(Ks + kk * C::kstr + 8 * c8) = kk < left ? kr[p] : zero;
             }
         }
 #pragma unroll
@@ -380,9 +382,11 @@ attn_mfma_kernel(AttnArgs a) {
             if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
                 const int pr = idx & 31;
                 const int c8 = idx >> 5;
+                const u32x4 v0 = 2 * pr < left ? vr0[p] : zero;
+                const u32x4 v1 = 2 * pr + 1 < left ? vr1[p] : zero;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t x0 = vr0[p][j], x1 = vr1[p][j];
+                    const uint32_t x0 = v0[j], x1 = v1[j];
                     uint16_t* col = Vt + (8 * c8 + 2 * j) * C::vstr + 2 * pr;
                     *reinterpret_cast<uint32_t*>(col) = (x0 & 0xffffu) | (x1 << 16);
                     *reinterpret_cast<uint32_t*>(col + C::vstr) = (x0 >> 16) | (x1 & 0xffff0000u);
@@ -416,7 +420,7 @@ attn_mfma_kernel(AttnArgs a) {
 
     if (n_sub > 0) {
         load(0);
-        store(lds);
+        store(lds, 0);
     }
     for (int s = 0; s < n_sub; ++s) {
         const bool more = s + 1 < n_sub;
@@ -436,7 +440,7 @@ attn_mfma_kernel(AttnArgs a) {
             w.template dispatch<true>(a0, a1, Ks, Vt, key0, lq, lj, a.scale_log2);
         else
             w.template dispatch<false>(a0, a1, Ks, Vt, key0, lq, lj, a.scale_log2);
-        if (more) store(lds + ((s + 1) & 1) * C::buf_elems);
+        if (more) store(lds + ((s + 1) & 1) * C::buf_elems, s + 1);
     }
 
     // ---- epilogue: row sums across the 4 lane groups, then output or partial ----
@@ -531,52 +535,53 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
     const int n_it = (n_sub + 1) / 2;
 
     u32x4 kr[2][C::kp], vr0[2][C::vp], vr1[2][C::vp];
-    // Global -> registers: sub-tiles 2i and 2i + 1 (zero beyond the chunk end).
+    // Global -> registers: sub-tiles 2i and 2i + 1, unconditional loads (key
+    // rows past the chunk end re-read its last row) so their wait sits at the
+    // LDS store after the step's compute; store() zeroes those rows.
     auto load = [&](int i) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int s = 2 * i + j;
-            const int32_t left = n_keys_chunk - kSub * s;
-            const char* kb = kbase + static_cast<int64_t>(kSub) * s * a.ks[1] * 2;
-            const char* vb = vbase + static_cast<int64_t>(kSub) * s * a.vs[1] * 2;
 #pragma unroll
             for (int p = 0; p < C::kp; ++p) {
                 const int idx = tid + p * NT;
-                kr[j][p] = u32x4{0u, 0u, 0u, 0u};
                 if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
                     const int kk = idx / C::c8;
                     const int c8 = idx - kk * C::c8;
-                    if (kk < left) kr[j][p] = *reinterpret_cast<const u32x4*>(kb + (kk * ks1 + 8 * c8) * 2);
+                    const int32_t key = min(kSub * s + kk, n_keys_chunk - 1);
+                    kr[j][p] = *reinterpret_cast<const u32x4*>(kbase + (static_cast<int64_t>(key) * ks1 + 8 * c8) * 2);
                 }
             }
 #pragma unroll
             for (int p = 0; p < C::vp; ++p) {
                 const int idx = tid + p * NT;
-                vr0[j][p] = u32x4{0u, 0u, 0u, 0u};
-                vr1[j][p] = u32x4{0u, 0u, 0u, 0u};
                 if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
                     const int pr = idx & 31;
                     const int c8 = idx >> 5;
-                    const int kk = 2 * pr;
-                    if (kk < left) vr0[j][p] = *reinterpret_cast<const u32x4*>(vb + (kk * vs1 + 8 * c8) * 2);
-                    if (kk + 1 < left) vr1[j][p] = *reinterpret_cast<const u32x4*>(vb + ((kk + 1) * vs1 + 8 * c8) * 2);
+                    const int32_t k0 = min(kSub * s + 2 * pr, n_keys_chunk - 1);
+                    const int32_t k1 = min(kSub * s + 2 * pr + 1, n_keys_chunk - 1);
+                    vr0[j][p] = *reinterpret_cast<const u32x4*>(vbase + (static_cast<int64_t>(k0) * vs1 + 8 * c8) * 2);
+                    vr1[j][p] = *reinterpret_cast<const u32x4*>(vbase + (static_cast<int64_t>(k1) * vs1 + 8 * c8) * 2);
                 }
             }
         }
     };
-    // Registers -> LDS stage: per sub-tile K as is, V transposed (key pairs packed per dim).
-    auto store = [&](uint16_t* stage) {
+    // Registers -> LDS stage of step i: per sub-tile K as is, V transposed (key
+    // pairs packed per dim); rows past the chunk end are zeroed.
+    auto store = [&](uint16_t* stage, int i) {
+        const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             uint16_t* Ks = stage + j * C::buf_elems;
             uint16_t* Vt = Ks + C::k_elems;
+            const int32_t left = n_keys_chunk - kSub * (2 * i + j);
 #pragma unroll
             for (int p = 0; p < C::kp; ++p) {
                 const int idx = tid + p * NT;
                 if (C::k_pieces % NT == 0 || idx < C::k_pieces) {
                     const int kk = idx / C::c8;
                     const int c8 = idx - kk * C::c8;
-                    *reinterpret_cast<u32x4*>(Ks + kk * C::kstr + 8 * c8) = kr[j][p];
+                    *reinterpret_cast<u32x4*>(Ks + kk * C::kstr + 8 * c8) = kk < left ? kr[j][p] : zero;
                 }
             }
 #pragma unroll
@@ -585,9 +590,11 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
                 if (C::v_pieces % NT == 0 || idx < C::v_pieces) {
                     const int pr = idx & 31;
                     const int c8 = idx >> 5;
+                    const u32x4 v0 = 2 * pr < left ? vr0[j][p] : zero;
+                    const u32x4 v1 = 2 * pr + 1 < left ? vr1[j][p] : zero;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const uint32_t x0 = vr0[j][p][q], x1 = vr1[j][p][q];
+                        const uint32_t x0 = v0[q], x1 = v1[q];
                         uint16_t* col = Vt + (8 * c8 + 2 * q) * C::vstr + 2 * pr;
                         *reinterpret_cast<uint32_t*>(col) = (x0 & 0xffffu) | (x1 << 16);
                         *reinterpret_cast<uint32_t*>(col + C::vstr) = (x0 >> 16) | (x1 & 0xffff0000u);
@@ -621,7 +628,7 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
 
     if (n_it > 0) {
         load(0);
-        store(lds);
+        store(lds, 0);
     }
     for (int i = 0; i < n_it; ++i) {
         const bool more = i + 1 < n_it;
@@ -637,7 +644,7 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
             else
                 w.template step<true, false, false>(Ks, Vt, key0, lq, lj, a.scale_log2);
         }
-        if (more) store(lds + ((i + 1) & 1) * 2 * C::buf_elems);
+        if (more) store(lds + ((i + 1) & 1) * 2 * C::buf_elems, i + 1);
     }
 
     // ---- combine the two key halves of each head, then output or partial ----
