@@ -102,10 +102,14 @@ class IndexedPlan:
         # int64 positions and bounds; version counters stay live even under
         # inference mode so every launch can reject in-place mutation with a
         # host-side check instead of a device read.
+        # One staged upload for the three arrays; the device tensors are
+        # contiguous views of it (sharing one version counter, so a write
+        # through any of them unseals the plan).
+        n, tiles = len(self.positions), len(self.full_prefix_tiles)
         with torch.cuda.device(device), torch.inference_mode(False):
-            positions = _upload(torch.tensor(self.positions, dtype=torch.int64), device)
-            full = _upload(torch.tensor(self.full_prefix_tiles, dtype=torch.int64), device)
-            total = _upload(torch.tensor(self.total_tiles, dtype=torch.int64), device)
+            packed = _upload(torch.tensor(self.positions + self.full_prefix_tiles + self.total_tiles,
+                                          dtype=torch.int64), device)
+            positions, full, total = packed[:n], packed[n:n + tiles], packed[n + tiles:]
         tensors = (positions, full, total)
         seal = (id(self), tuple(id(t) for t in tensors), tuple(t._version for t in tensors))
         return DeviceIndexedPlan(self, positions, full, total, seal)
