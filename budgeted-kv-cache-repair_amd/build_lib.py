@@ -17,7 +17,7 @@ REPO_ROOT = PACKAGE_ROOT.parent
 CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / "libkvrepair.so"
-SOURCES = ("kvr_common.hip", "kvr_rotate.hip", "kvr_scatter.hip", "kvr_fresh.hip", "kvr_layer.hip", "kvr_gemm.hip", "kvr_attention.hip", "kvr_decoder.hip", "kvr_writeback.hip", "kvr_inputs.hip")
+SOURCES = ("kvr_common.hip", "kvr_rotate.hip", "kvr_scatter.hip", "kvr_fresh.hip", "kvr_layer.hip", "kvr_gemm.hip", "kvr_attention.hip", "kvr_decoder.hip", "kvr_writeback.hip", "kvr_inputs.hip", "kvr_scoring.hip")
 ARCH = "gfx950"
 
 # Packed-FP32 instructions are disabled: hipcc still vectorises ordinary

@@ -100,6 +100,9 @@ def _declare(lib: ctypes.CDLL) -> None:
                                        ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int64, _vp, ctypes.c_int32,
                                        ctypes.c_float, _vp, _vp, ctypes.c_int32, _vp]
     lib.kvr_refresh_inputs.restype = ctypes.c_int
+    lib.kvr_query_relevance.argtypes = [_vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int32,
+                                        ctypes.c_int64, _vp, ctypes.c_int32, ctypes.c_float, _vp, ctypes.c_int32, _vp]
+    lib.kvr_query_relevance.restype = ctypes.c_int
     _desc_p = ctypes.POINTER(LayerDesc)
     _refresh_p = ctypes.POINTER(RefreshDesc)
     lib.kvr_decoder_scratch_bytes.argtypes = [_refresh_p]

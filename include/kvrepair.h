@@ -149,6 +149,22 @@ int kvr_refresh_inputs(const void* ids, int32_t ids_are_int32, int64_t n_ids, co
                        void* cos, void* sin, int32_t dtype, void* stream);
 
 /*
+ * Frozen-embedding query relevance of every prompt token in ONE launch (the
+ * dense scorer that ranks suffix tokens for the refresh budget,
+ * src/kv_cache_repair/scoring.py:11-72, dense_query_relevance_scores):
+ *   scores[t] = max_j cos(embed[ids[t]], embed[query_ids[j]]) + boost * [ids[t] in query_ids]
+ * cos(a, b) = a.b / (max(|a|, 1e-12) * max(|b|, 1e-12)) in fp32 (F.normalize,
+ * then the dot product). embed: [vocab][ld_embed] of `dtype`; ids: n token
+ * ids (int32 when ids_are_int32, else int64); query_ids: n_query int64 device
+ * ids (n_query > 0); scores: n fp32. One embedding row (padded to 16 bytes)
+ * must fit 64 KiB. A token or query id outside [0, vocab) gives NaN scores
+ * (nothing is read out of bounds). n == 0 enqueues nothing.
+ */
+int kvr_query_relevance(const void* embed, int64_t vocab, int64_t ld_embed, int32_t hidden, const void* ids,
+                        int32_t ids_are_int32, int64_t n, const int64_t* query_ids, int32_t n_query, float boost,
+                        float* scores, int32_t dtype, void* stream);
+
+/*
  * Fresh-row epilogue of one packed layer in ONE launch (RoPE at absolute
  * positions fused with the indexed K/V scatter):
  *   q_out[0, h, r, :]            = rope(q[0, h, r, :], cos[r], sin[r])        h < n_q_heads

@@ -214,3 +214,25 @@ def bf16_bits_to_f32(b: int) -> float:
 
 def f16_bits_to_f32(b: int) -> float:
     return float(lib().orc_f16_to_f32(int(b)))
+
+
+def query_relevance_f64(embed: np.ndarray, ids, query_ids, boost: float = 0.25) -> np.ndarray:
+    """dense_query_relevance_scores (scoring.py:11-72) in float64.
+
+    score[t] = max_j <E[ids[t]] / max(|E[ids[t]]|, 1e-12), E[q_j] / max(|E[q_j]|, 1e-12)>
+               + boost * [ids[t] in query_ids]
+    (F.normalize of each embedding row, the matmul against the normalised query
+    rows, max over the query tokens, the exact-id boost). ``embed`` holds the
+    table's values as float32/float64 (16-bit tables: their decoded values).
+    """
+    table = np.asarray(embed, dtype=np.float64)
+    ids = np.asarray(ids, dtype=np.int64).reshape(-1)
+    query = np.asarray(query_ids, dtype=np.int64).reshape(-1)
+    if query.size == 0:
+        raise ValueError("dense query scorer requires query tokens")
+
+    def unit(rows):
+        return rows / np.maximum(np.linalg.norm(rows, axis=1, keepdims=True), 1e-12)
+
+    similarity = (unit(table[ids]) @ unit(table[query]).T).max(axis=1)
+    return similarity + np.where(np.isin(ids, query), boost, 0.0)

@@ -27,7 +27,7 @@ def test_header_declares_the_entry_points():
         "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
         "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
-        "kvr_copy_kv_interval", "kvr_refresh_inputs"])
+        "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -130,6 +130,21 @@ def test_refresh_inputs_validates_before_any_launch():
     assert call(None, 0, 8, None, 4, None, 100, 32, 64, None, 64, None, 128, 1.0, None, None, 2, None) == -4  # ld
     assert call(None, 0, 8, None, 0, None, 100, 64, 64, None, 64, None, 128, 1.0, None, None, 2, None) == 0  # empty
     assert call(None, 0, 8, None, 4, None, 100, 64, 64, None, 64, None, 128, 1.0, None, None, 2, None) == -5
+
+
+def test_query_relevance_validates_before_any_launch():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    call = lib.kvr_query_relevance
+    # embed, vocab, ld, hidden, ids, int32?, n, query_ids, n_query, boost, scores, dtype
+    assert call(None, 10, 8, 8, None, 0, 4, None, 1, 0.25, None, 7, None) == -2      # dtype
+    assert call(None, 10, 8, 8, None, 0, 4, None, 0, 0.25, None, 2, None) == -1      # empty query
+    assert call(None, 0, 8, 8, None, 0, 4, None, 1, 0.25, None, 2, None) == -1       # vocab
+    assert call(None, 10, 4, 8, None, 0, 4, None, 1, 0.25, None, 2, None) == -4      # ld < hidden
+    assert call(None, 10, 40000, 40000, None, 0, 4, None, 1, 0.25, None, 2, None) == -3  # row > 64 KiB
+    assert call(None, 10, 8, 8, None, 0, 0, None, 1, 0.25, None, 2, None) == 0       # no tokens
+    assert call(None, 10, 8, 8, None, 0, 4, None, 1, 0.25, None, 2, None) == -5
 
 
 def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):

@@ -383,3 +383,42 @@ def test_positions_to_intervals_kat_and_brute_force():
         covered = sorted(p for s, e in got for p in range(s, e))
         assert covered == sorted(set(pos))
         assert all(a[1] < b[0] for a, b in zip(got, got[1:]))  # maximal: gaps between runs
+
+
+# ---- dense query relevance (scoring.py:11-72) ----
+_KAT_TABLE = np.array([[1.0, 0.0], [1.0, 0.0], [-1.0, 0.0], [0.0, 1.0]])
+
+
+def test_relevance_exact_bonus_applies_only_to_identical_ids_kat():
+    # test_scoring.py:16-26: ids [0,1,2,3], query [1] -> [1.0, 1.25, -1.0, 0.0]
+    got = orc.query_relevance_f64(_KAT_TABLE, [0, 1, 2, 3], [1])
+    assert got.tolist() == pytest.approx([1.0, 1.25, -1.0, 0.0])
+
+
+def test_relevance_is_preserved_across_the_reference_chunk_boundary_kat():
+    # test_scoring.py:29-37: 1024 x id 2 then id 3, query [1, 3] -> [0.0]*1024 + [1.25]
+    got = orc.query_relevance_f64(_KAT_TABLE, [2] * 1024 + [3], [1, 3])
+    assert got.tolist() == pytest.approx([0.0] * 1024 + [1.25])
+
+
+def test_relevance_rejects_an_empty_query():
+    with pytest.raises(ValueError, match="requires query tokens"):
+        orc.query_relevance_f64(_KAT_TABLE, [0], [])
+
+
+def test_relevance_is_a_max_of_cosines_invariant_to_row_scale():
+    rng = np.random.default_rng(11)
+    table = rng.standard_normal((50, 24))
+    ids = rng.integers(0, 50, 300)
+    query = [3, 7, 7, 41]
+    base = orc.query_relevance_f64(table, ids, query)
+    scaled = orc.query_relevance_f64(table * rng.uniform(0.1, 10.0, (50, 1)), ids, query)
+    np.testing.assert_allclose(base, scaled, rtol=0, atol=1e-12)
+    # brute force on a few tokens: cosine by the definition, boost by membership
+    for t in (0, 17, 299):
+        e = table[ids[t]]
+        cos = max(float(e @ table[q]) / (np.linalg.norm(e) * np.linalg.norm(table[q])) for q in query)
+        assert base[t] == pytest.approx(cos + (0.25 if ids[t] in query else 0.0), abs=1e-12)
+    # a zero row normalises to zero (eps clamp): cosine 0
+    table[5] = 0.0
+    assert orc.query_relevance_f64(table, [5], [3])[0] == 0.0
