@@ -23,18 +23,22 @@ steps), the per-kernel HIP event timings of K more steps that dispatch the
 same kernels one by one from Python (events around every libkvrepair
 launch), a roofline object for the dominant kernel,
 the rotate-only GB/s, the same stage run the reference way on the same GPU,
+the selection scorer (kvr_query_relevance over the c3 edited ids, beside the
+reference's eager scorer on the same GPU; selection is not part of the step),
 and the reference path timed on the host CPU (cpu_baseline).
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import random
 import sys
 import time
 from pathlib import Path
+from types import SimpleNamespace
 
 ROOT = Path(__file__).resolve().parent
 sys.path[:0] = [str(ROOT / "budgeted-kv-cache-repair_amd"), str(ROOT)]
@@ -303,6 +307,78 @@ def measured_traffic(kernel: str):
     return None
 
 
+# ----------------------------------------------------------------------------- selection scoring
+def reference_scores(embedding, ids, query):
+    """The reference's chunked eager scorer (scoring.py:11-62) on the same GPU."""
+    import torch.nn.functional as F
+
+    device = ids.device
+    q = F.normalize(embedding(torch.tensor([query], dtype=torch.long, device=device))[0].float(), dim=-1)
+    scores = torch.full((ids.shape[0],), -float("inf"), dtype=torch.float32, device=device)
+    exact = set(query)
+    for start in range(0, ids.shape[0], 1024):
+        chunk = ids[start:start + 1024]
+        sim = torch.matmul(F.normalize(embedding(chunk).float(), dim=-1), q.transpose(0, 1)).max(dim=1).values
+        boost = torch.tensor([0.25 if int(t) in exact else 0.0 for t in chunk.tolist()], dtype=torch.float32,
+                             device=device)
+        scores[start:start + chunk.shape[0]] = sim + boost
+    return [float(v) for v in scores.tolist()]
+
+
+def scoring_measurement(model, new_ids, device, launches=50, calls=10) -> dict:
+    """Dense query relevance over the c3 edited ids (7680 tokens) with the bench
+    model's embedding table and a 12-token query (half of it taken from the
+    prompt, so exact-id boosts occur): the kvr_query_relevance launch alone
+    (HIP events on the launching stream), the Python API end to end (list of
+    scores on the host), and the reference's eager scorer on the same GPU."""
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.scoring import dense_query_relevance_scores
+
+    embedding = model.get_input_embeddings()
+    holder = SimpleNamespace(generator=model)  # the reference's scorer reads model.generator
+    ids = new_ids[0]
+    rng = random.Random(3)
+    query = [int(ids[rng.randrange(ids.shape[0])]) for _ in range(6)] + [rng.randrange(VOCAB) for _ in range(6)]
+    ours = lambda: dense_query_relevance_scores(model=holder, edited_input_ids=new_ids,  # noqa: E731
+                                                query_token_ids=query)
+    theirs = lambda: reference_scores(embedding, ids, query)  # noqa: E731
+    got, _ = ours()
+    want = theirs()
+    max_abs = max(abs(a - b) for a, b in zip(got, want))
+
+    table = embedding.weight
+    lib, stream = _native.lib(), _native.stream_handle(device)
+    qd = torch.tensor(query, dtype=torch.long, device=device)
+    out = torch.empty(ids.shape[0], dtype=torch.float32, device=device)
+
+    def launch():
+        status = lib.kvr_query_relevance(table.data_ptr(), table.shape[0], table.stride(0), table.shape[1],
+                                         ids.data_ptr(), 0, ids.shape[0], qd.data_ptr(), len(query),
+                                         ctypes.c_float(0.25), out.data_ptr(), _native.DTYPE_CODES[table.dtype],
+                                         stream)
+        if status != 0:
+            raise RuntimeError(f"kvr_query_relevance returned {status}")
+
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(launches):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    kernel_us = start.elapsed_time(end) * 1000.0 / launches
+    n, hidden = ids.shape[0], table.shape[1]
+    algorithmic = 2 * hidden * (n + len(query)) + 8 * n + 4 * n  # gathered rows, query rows, ids, scores
+    return {"workload": f"c3 edited ids ({n} tokens), embedding {tuple(table.shape)} bf16, {len(query)}-token query",
+            "kernel_avg_us": kernel_us, "algorithmic_bytes": algorithmic,
+            "achieved_GBps": algorithmic / (kernel_us * 1e3),
+            "frac_of_peak": algorithmic / (kernel_us * 1e3) / HBM_PEAK_GBPS,
+            "api_ms": time_steps(ours, calls, 2), "reference_same_gpu_ms": time_steps(theirs, calls, 2),
+            "max_abs_vs_reference": max_abs}
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(layers_sample: int, repeats: int = 10) -> dict:
     """The oracle's torch restatement of the reference stage (rotate chain +
@@ -481,6 +557,7 @@ def main(argv=None) -> int:
                 "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                 "avg_launch_us": kernels[dominant]["avg_us"], "algorithmic_bytes_per_launch": per_kernel[dominant]}
 
+    scoring = scoring_measurement(model, new_ids, device)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_layers)
     line = {
         "metric": METRIC, "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -494,7 +571,7 @@ def main(argv=None) -> int:
         "rotate": {"avg_us": rotate["avg_us"], "algorithmic_bytes": rotate_bytes,
                    "frac_of_peak": rotate_bytes / (rotate["avg_us"] * 1e3) / HBM_PEAK_GBPS},
         "kernels": kernels, "instrumented_ms_per_step": instrumented_ms, "roofline": roofline,
-        "reference_same_gpu": reference, "checks": checks,
+        "reference_same_gpu": reference, "checks": checks, "selection_scoring": scoring,
         "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
     }
     print(json.dumps(line), flush=True)

@@ -189,10 +189,17 @@ __global__ void __launch_bounds__(kThreads) query_relevance_kernel(ScoreArgs a) 
 // v_mfma_f32_16x16x32 (A = 16 gathered token rows, B = 16 query rows, both
 // straight from global memory: the query rows stay in L2), fp32 accumulation
 // of exact 16-bit products. The squared norms are summed from the same
-// fragments. Wave = 16 tokens; up to kQTiles x 16 queries per pass (more
+// fragments. A wave computes 16 tokens over SPLIT-th of the hidden axis:
+// a block of 4 waves covers 64 / SPLIT tokens, and the SPLIT waves of one
+// token group add their partial dot products and norms in LDS (wave order
+// fixed). SPLIT grows as the prompt shrinks so that a launch still has about
+// two blocks per CU (SPLIT 4: 480 blocks for a 7680-token prompt; SPLIT 1:
+// 496 blocks for 31744 tokens). Up to kQTiles x 16 queries per pass (more
 // queries take further passes over the token rows).
 constexpr int kQTiles = 4;
-constexpr int kMfmaTokens = 64;  // 4 waves x 16 tokens per block
+constexpr int kMfmaWaves = kThreads / 64;
+constexpr int kMfmaMinTokens = 16;  // tokens per block at SPLIT 4
+constexpr int kParts = 5 * kQTiles + 1;  // per lane: kQTiles x 4 dots, kQTiles query norms, 1 token norm
 
 template <typename T> struct score_mma;
 template <> struct score_mma<bf16_t> {
@@ -221,16 +228,19 @@ __device__ inline float sumsq8(u32x4 v) {
     return s;
 }
 
-template <typename T>
+template <typename T, int SPLIT>
 __global__ void __launch_bounds__(kThreads) query_relevance_mfma_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
     using M = score_mma<T>;
     using v8 = typename M::v8;
+    static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "SPLIT divides the block's 4 waves");
+    __shared__ float part[SPLIT > 1 ? kMfmaWaves : 1][kParts][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int hpart = wave % SPLIT;  // this wave's part of the hidden axis
     const int lq = lane & 15;
     const int lj = lane >> 4;
-    const int64_t tbase = static_cast<int64_t>(blockIdx.x) * kMfmaTokens + wave * 16;
+    const int64_t tbase = static_cast<int64_t>(blockIdx.x) * (64 / SPLIT) + (wave / SPLIT) * 16;
     // this lane's A row: token tbase + lq (clamped in bounds; its score is not written)
     const int64_t t = tbase + lq;
     int64_t id = -1;
@@ -239,22 +249,25 @@ __global__ void __launch_bounds__(kThreads) query_relevance_mfma_kernel(ScoreArg
                      : reinterpret_cast<const int64_t*>(a.ids)[t];
     const bool ok = id >= 0 && id < a.vocab;
     const char* arow = a.embed + (ok ? id : 0) * a.ld_embed * 2 + 16 * lj;
+    // this wave's k-steps: [sbeg, send)
     const int steps = a.hidden / 32;
+    const int per = (steps + SPLIT - 1) / SPLIT;
+    const int sbeg = min(steps, hpart * per);
+    const int send = min(steps, sbeg + per);
 
-    float tn2 = 0.f;  // this lane's part of token lq's squared norm
-    float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // tokens 4 lj + i
+    float tn2 = 0.f;  // token lq's squared norm (hidden part 0, lanes (lq, *))
+    float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // tokens 4 lj + i (hidden part 0)
     bool qbad = false;
     for (int q0 = 0; q0 < a.n_query; q0 += 16 * kQTiles) {
         const int tiles = min(kQTiles, (a.n_query - q0 + 15) / 16);
         const char* brow[kQTiles];
-        bool qok[kQTiles];
 #pragma unroll
         for (int qt = 0; qt < kQTiles; ++qt) {
             const int j = q0 + 16 * qt + lq;  // this lane's B row: query j
             const int64_t qid = j < a.n_query ? a.query_ids[j] : -1;
-            qok[qt] = j < a.n_query && qid >= 0 && qid < a.vocab;
-            qbad |= j < a.n_query && !qok[qt];
-            brow[qt] = a.embed + (qok[qt] ? qid : 0) * a.ld_embed * 2 + 16 * lj;
+            const bool qok = j < a.n_query && qid >= 0 && qid < a.vocab;
+            qbad |= j < a.n_query && !qok;
+            brow[qt] = a.embed + (qok ? qid : 0) * a.ld_embed * 2 + 16 * lj;
         }
         f32x4_t acc[kQTiles];
         float qn2[kQTiles];
@@ -263,21 +276,22 @@ __global__ void __launch_bounds__(kThreads) query_relevance_mfma_kernel(ScoreArg
             acc[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
             qn2[qt] = 0.f;
         }
-        for (int s0 = 0; s0 < steps; s0 += 8) {
+        float tsum = 0.f;
+        for (int s0 = sbeg; s0 < send; s0 += 8) {
             u32x4 av[8];
 #pragma unroll
             for (int d = 0; d < 8; ++d)
-                av[d] = *reinterpret_cast<const u32x4*>(arow + static_cast<int64_t>(min(s0 + d, steps - 1)) * 64);
+                av[d] = *reinterpret_cast<const u32x4*>(arow + static_cast<int64_t>(min(s0 + d, send - 1)) * 64);
 #pragma unroll
             for (int qt = 0; qt < kQTiles; ++qt) {
                 if (qt >= tiles) break;
                 u32x4 bv[8];
 #pragma unroll
                 for (int d = 0; d < 8; ++d)
-                    bv[d] = *reinterpret_cast<const u32x4*>(brow[qt] + static_cast<int64_t>(min(s0 + d, steps - 1)) * 64);
+                    bv[d] = *reinterpret_cast<const u32x4*>(brow[qt] + static_cast<int64_t>(min(s0 + d, send - 1)) * 64);
 #pragma unroll
                 for (int d = 0; d < 8; ++d) {
-                    if (s0 + d < steps) {
+                    if (s0 + d < send) {
                         acc[qt] = M::mma(__builtin_bit_cast(v8, av[d]), __builtin_bit_cast(v8, bv[d]), acc[qt]);
                         qn2[qt] += sumsq8<T>(bv[d]);
                     }
@@ -286,34 +300,61 @@ __global__ void __launch_bounds__(kThreads) query_relevance_mfma_kernel(ScoreArg
             if (q0 == 0) {
 #pragma unroll
                 for (int d = 0; d < 8; ++d)
-                    if (s0 + d < steps) tn2 += sumsq8<T>(av[d]);
+                    if (s0 + d < send) tsum += sumsq8<T>(av[d]);
             }
         }
-        if (q0 == 0) {
-            tn2 += __shfl_xor(tn2, 16);
-            tn2 += __shfl_xor(tn2, 32);  // lanes (lq, *): token lq's squared norm
-        }
-        float tden[4];
+        if constexpr (SPLIT > 1) {  // add the token group's partials (hidden parts in order)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tden[i] = fmaxf(sqrtf(__shfl(tn2, 4 * lj + i)), kEps);
+            for (int qt = 0; qt < kQTiles; ++qt) {
 #pragma unroll
-        for (int qt = 0; qt < kQTiles; ++qt) {
-            if (qt >= tiles) break;
-            float n2 = qn2[qt];
-            n2 += __shfl_xor(n2, 16);
-            n2 += __shfl_xor(n2, 32);  // lanes (lq, *): query q0 + 16 qt + lq
-            const float qden = fmaxf(sqrtf(n2), kEps);
-            const bool live = q0 + 16 * qt + lq < a.n_query;
+                for (int i = 0; i < 4; ++i) part[wave][4 * qt + i][lane] = acc[qt][i];
+                part[wave][4 * kQTiles + qt][lane] = qn2[qt];
+            }
+            part[wave][kParts - 1][lane] = tsum;
+            __syncthreads();
+            if (hpart == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                // D layout: lane (lq, lj) holds token 4 lj + i x query lq
-                float c = live ? acc[qt][i] / (tden[i] * qden) : -INFINITY;
+                for (int w = wave + 1; w < wave + SPLIT; ++w) {
 #pragma unroll
-                for (int off = 8; off > 0; off >>= 1) c = fmaxf(c, __shfl_xor(c, off));  // max over the 16 queries
-                best[i] = fmaxf(best[i], c);
+                    for (int qt = 0; qt < kQTiles; ++qt) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[qt][i] += part[w][4 * qt + i][lane];
+                        qn2[qt] += part[w][4 * kQTiles + qt][lane];
+                    }
+                    tsum += part[w][kParts - 1][lane];
+                }
             }
         }
+        if (hpart == 0) {
+            if (q0 == 0) {
+                tn2 = tsum;
+                tn2 += __shfl_xor(tn2, 16);
+                tn2 += __shfl_xor(tn2, 32);  // lanes (lq, *): token lq's squared norm
+            }
+            float tden[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tden[i] = fmaxf(sqrtf(__shfl(tn2, 4 * lj + i)), kEps);
+#pragma unroll
+            for (int qt = 0; qt < kQTiles; ++qt) {
+                if (qt >= tiles) break;
+                float n2 = qn2[qt];
+                n2 += __shfl_xor(n2, 16);
+                n2 += __shfl_xor(n2, 32);  // lanes (lq, *): query q0 + 16 qt + lq
+                const float qden = fmaxf(sqrtf(n2), kEps);
+                const bool live = q0 + 16 * qt + lq < a.n_query;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // D layout: lane (lq, lj) holds token 4 lj + i x query lq
+                    float c = live ? acc[qt][i] / (tden[i] * qden) : -INFINITY;
+#pragma unroll
+                    for (int off = 8; off > 0; off >>= 1) c = fmaxf(c, __shfl_xor(c, off));  // max over the 16 queries
+                    best[i] = fmaxf(best[i], c);
+                }
+            }
+        }
+        if constexpr (SPLIT > 1) __syncthreads();  // the next pass rewrites part
     }
+    if (hpart != 0) return;
     qbad = __any(qbad);
     int64_t tids[4];  // ids of tokens 4 lj + i (held by lanes 4 lj + i), read while every lane is active
 #pragma unroll
@@ -344,8 +385,15 @@ int launch_scores(const ScoreArgs& a, size_t lds, hipStream_t s) {
     const int esize = elem<T>::size;
     if constexpr (!__is_same(T, f32_t)) {
         if (a.hidden % 32 == 0 && (a.ld_embed * esize) % 16 == 0 && aligned16(a.embed)) {
-            const unsigned g = static_cast<unsigned>((a.n + kMfmaTokens - 1) / kMfmaTokens);
-            query_relevance_mfma_kernel<T><<<g, kThreads, 0, s>>>(a);
+            // SPLIT: the largest of 1, 2, 4 that keeps >= 480 blocks (else 4)
+            const int64_t blocks1 = (a.n + 63) / 64;
+            if (blocks1 >= 480) {
+                query_relevance_mfma_kernel<T, 1><<<static_cast<unsigned>(blocks1), kThreads, 0, s>>>(a);
+            } else if (blocks1 >= 240) {
+                query_relevance_mfma_kernel<T, 2><<<static_cast<unsigned>((a.n + 31) / 32), kThreads, 0, s>>>(a);
+            } else {
+                query_relevance_mfma_kernel<T, 4><<<static_cast<unsigned>((a.n + 15) / 16), kThreads, 0, s>>>(a);
+            }
             return launch_status();
         }
     }
@@ -371,7 +419,7 @@ extern "C" int kvr_query_relevance(const void* embed, int64_t vocab, int64_t ld_
     const int64_t row_stride = (static_cast<int64_t>(hidden) * esize + 15) / 16 * 16;
     if (row_stride > kChunkBytes) return KVR_E_UNSUPPORTED_SHAPE;  // one query row must fit a chunk
     if (n == 0) return KVR_OK;
-    if (n > (int64_t(kTokensPerBlock) << 31) - 1) return KVR_E_UNSUPPORTED_SHAPE;
+    if (n > int64_t(kMfmaMinTokens) * 0x7fffffff) return KVR_E_UNSUPPORTED_SHAPE;  // grid.x of every path
     if (!embed || !ids || !query_ids || !scores) return KVR_E_NULL_POINTER;
     ScoreArgs a;
     a.embed = static_cast<const char*>(embed);
