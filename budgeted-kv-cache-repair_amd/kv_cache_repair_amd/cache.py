@@ -59,19 +59,32 @@ def _rotary(model: Any, device: torch.device):
     return inv_freq.contiguous(), float(getattr(rotary, "attention_scaling", 1.0)), 2 * int(inv_freq.numel())
 
 
+def _shift_launcher(old_k, old_v, new_k, new_v, *, inv_freq, scaling, rotary_dim):
+    """kvr_shift_cache_build over lists of per-layer tensors, with every pointer
+    and stride argument bound now; the returned function takes the row ranges
+    and the shift and launches (one launch per 64 layers)."""
+    first = old_k[0]
+    _, heads, _, dim = first.shape
+    fixed = (_native.ptr_array(old_k), _native.ptr_array(old_v), _native.ptr_array(new_k), _native.ptr_array(new_v),
+             len(old_k), int(heads), int(dim), int(rotary_dim), _native.i64_array(_native.strides3(first)),
+             _native.i64_array(_native.strides3(new_k[0])))
+    tail = (inv_freq.data_ptr() if inv_freq is not None else None, float(scaling), _native.DTYPE_CODES[first.dtype],
+            _native.stream_handle(first.device))
+    build = _native.lib().kvr_shift_cache_build
+
+    def launch(*, prefix_rows, old_tail_start, new_tail_start, tail_rows, shift) -> None:
+        status = build(*fixed, int(prefix_rows), int(old_tail_start), int(new_tail_start), int(tail_rows),
+                       int(shift), *tail)
+        _native.check(status, "kvr_shift_cache_build")
+    return launch
+
+
 def _shift_rows(old_k, old_v, new_k, new_v, *, prefix_rows, old_tail_start, new_tail_start, tail_rows, shift,
                 inv_freq, scaling, rotary_dim) -> None:
     """kvr_shift_cache_build over lists of per-layer tensors (one launch per 64 layers)."""
-    first = old_k[0]
-    _, heads, _, dim = first.shape
-    lib = _native.lib()
-    status = lib.kvr_shift_cache_build(
-        _native.ptr_array(old_k), _native.ptr_array(old_v), _native.ptr_array(new_k), _native.ptr_array(new_v),
-        len(old_k), int(heads), int(dim), int(rotary_dim), _native.i64_array(_native.strides3(first)),
-        _native.i64_array(_native.strides3(new_k[0])), int(prefix_rows), int(old_tail_start), int(new_tail_start),
-        int(tail_rows), int(shift), inv_freq.data_ptr() if inv_freq is not None else None, float(scaling),
-        _native.DTYPE_CODES[first.dtype], _native.stream_handle(first.device))
-    _native.check(status, "kvr_shift_cache_build")
+    _shift_launcher(old_k, old_v, new_k, new_v, inv_freq=inv_freq, scaling=scaling, rotary_dim=rotary_dim)(
+        prefix_rows=prefix_rows, old_tail_start=old_tail_start, new_tail_start=new_tail_start, tail_rows=tail_rows,
+        shift=shift)
 
 
 def _check_uniform(pairs, what: str):
@@ -196,14 +209,11 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     never mutated.
     """
     n_old = int(old_input_ids.shape[1])
-    ids = torch.cat((old_input_ids[0].reshape(-1), new_input_ids[0].reshape(-1).to(old_input_ids.dtype)))
-    ids = ids.cpu().numpy()  # one device-to-host copy for both id rows
-    align = token_alignment_arrays(ids[:n_old], ids[n_old:])
     n_new = int(new_input_ids.shape[1])
-    halo = min(max(int(halo_tokens), 0), align["suffix"])
-    recompute_end = align["new_suffix_start"] + halo
-    old_tail_start = align["old_suffix_start"] + halo
-    tail_rows = align["suffix"] - halo
+    ids = torch.cat((old_input_ids[0].reshape(-1), new_input_ids[0].reshape(-1).to(old_input_ids.dtype)))
+    # Everything that does not depend on the id values (cache checks, the
+    # output allocation, the launch arguments) is done before the one
+    # device-to-host copy of both id rows, which waits for the stream.
     old = [layer_kv(old_cache, i) for i in range(len(old_cache.layers))]
     _check_uniform(old, "build_halo_cache")
     generator = getattr(model, "generator", model)
@@ -213,27 +223,32 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     slab = torch.empty((len(old), 2, 1, k0.shape[1], n_new, k0.shape[3]), dtype=k0.dtype, device=k0.device)
     views = slab.view(2 * len(old), 1, k0.shape[1], n_new, k0.shape[3]).unbind(0)
     new = list(zip(views[0::2], views[1::2]))
+    new_k, new_v = list(views[0::2]), list(views[1::2])
+    shift_tail = _shift_launcher([k for k, _ in old], [v for _, v in old], new_k, new_v, inv_freq=inv_freq,
+                                 scaling=scaling, rotary_dim=rotary_dim) if n_new else None
+    ids = ids.cpu().numpy()
+    align = token_alignment_arrays(ids[:n_old], ids[n_old:])
+    halo = min(max(int(halo_tokens), 0), align["suffix"])
+    recompute_end = align["new_suffix_start"] + halo
+    old_tail_start = align["old_suffix_start"] + halo
+    tail_rows = align["suffix"] - halo
     if recompute_end == align["prefix"]:
         # No recomputed rows: prefix copy + shifted tail in one launch.
         if n_new:
-            _shift_rows([k for k, _ in old], [v for _, v in old], [k for k, _ in new], [v for _, v in new],
-                        prefix_rows=align["prefix"], old_tail_start=old_tail_start, new_tail_start=recompute_end,
-                        tail_rows=tail_rows, shift=align["position_shift"], inv_freq=inv_freq, scaling=scaling,
-                        rotary_dim=rotary_dim)
+            shift_tail(prefix_rows=align["prefix"], old_tail_start=old_tail_start, new_tail_start=recompute_end,
+                       tail_rows=tail_rows, shift=align["position_shift"])
     else:
         prefix_cache = clone_cache(old_cache, align["prefix"])
         recomputed = run_tokens_from_prefix(generator, prefix_cache, new_input_ids[:, align["prefix"]:recompute_end],
                                             recompute_end)
         rec = [layer_kv(recomputed, i) for i in range(len(old))]
         _check_uniform(rec, "build_halo_cache")
-        _shift_rows([k for k, _ in rec], [v for _, v in rec], [k for k, _ in new], [v for _, v in new],
+        _shift_rows([k for k, _ in rec], [v for _, v in rec], new_k, new_v,
                     prefix_rows=recompute_end, old_tail_start=0, new_tail_start=recompute_end, tail_rows=0, shift=0,
                     inv_freq=None, scaling=1.0, rotary_dim=rotary_dim)
         if tail_rows:
-            _shift_rows([k for k, _ in old], [v for _, v in old], [k for k, _ in new], [v for _, v in new],
-                        prefix_rows=0, old_tail_start=old_tail_start, new_tail_start=recompute_end,
-                        tail_rows=tail_rows, shift=align["position_shift"], inv_freq=inv_freq, scaling=scaling,
-                        rotary_dim=rotary_dim)
+            shift_tail(prefix_rows=0, old_tail_start=old_tail_start, new_tail_start=recompute_end,
+                       tail_rows=tail_rows, shift=align["position_shift"])
     return cache_from_tensors(new), {**align, "halo_tokens": halo,
                                      "recomputed_tokens": align["mandatory_changed_tokens"] + halo}
 

@@ -206,6 +206,11 @@ class _LayerPlans:
 
 _PLAN_CACHE: "weakref.WeakKeyDictionary[Any, _LayerPlans]" = weakref.WeakKeyDictionary()
 _PLAN_LOCK = Lock()
+# Per decoder (`base`): the fingerprint of the module tree that last passed
+# _qualify with its parameters on GPU `index` -> (fingerprint, index), and the
+# layer plans built for that fingerprint -> (fingerprint, plans).
+_QUALIFIED: "weakref.WeakKeyDictionary[Any, tuple]" = weakref.WeakKeyDictionary()
+_MODEL_PLANS: "weakref.WeakKeyDictionary[Any, tuple]" = weakref.WeakKeyDictionary()
 
 
 def _plain_linear(module) -> bool:
@@ -478,7 +483,8 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
 
 
 def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend):
-    """Fail closed outside the inspected contract, before any device work."""
+    """Fail closed outside the inspected contract, before any device work.
+    Returns the module tree's fingerprint (see below) for _projection_plans_for."""
     if transformers.__version__ not in _SUPPORTED_TRANSFORMERS:
         raise ValueError(f"packed HIP executor requires transformers in {_SUPPORTED_TRANSFORMERS}")
     from transformers.models.llama.modeling_llama import LlamaForCausalLM, LlamaModel
@@ -509,9 +515,22 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
             push(attrs["_modules"].values())
     training = True in [attrs["training"] for attrs in inner]
     overridden = True in ["forward" in attrs for attrs in inner]
-    hooked = True in [attrs.get("_hf_hook") is not None for attrs in inner + outer]
-    off_device = True in [p is not None and p.get_device() != index
-                          for attrs in inner + outer for p in attrs["_parameters"].values()]
+    everything = inner + outer
+    hooked = True in [attrs.get("_hf_hook") is not None for attrs in everything]
+    # Fingerprint of the tree: every module (its __dict__'s identity) and every
+    # parameter slot (the tensor's identity and storage address; an empty slot
+    # counts). A tree with the fingerprint that last qualified on this GPU has
+    # the same parameter tensors at the same addresses, so their device check
+    # holds as it did; the layer plans are reused under the same condition.
+    params = [p for attrs in everything for p in attrs["_parameters"].values()]
+    fingerprint = (tuple(map(id, everything)), tuple(map(id, params)),
+                   tuple([0 if p is None else p.data_ptr() for p in params]))
+    with _PLAN_LOCK:
+        previous = _QUALIFIED.get(base)
+    if previous is not None and previous[1] == index and previous[0] == fingerprint:
+        fingerprint, off_device = previous[0], False
+    else:
+        off_device = True in [p is not None and p.get_device() != index for p in params]
     if model.training or base.training or training:
         raise ValueError("packed executor requires eval mode on all decoder modules")
     config = model.config
@@ -528,8 +547,7 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
         raise ValueError("packed HIP executor requires one ROCm GPU device")
     if off_device:
         raise ValueError("packed executor requires all model parameters on the request device")
-    if any(layer_kv(base_cache, i)[0].device != device or layer_kv(base_cache, i)[1].device != device
-           for i in range(len(base_cache.layers))):
+    if True in [t.get_device() != index for i in range(len(base_cache.layers)) for t in layer_kv(base_cache, i)]:
         raise ValueError("packed executor requires all cache layers on the request device")
     if hooked:
         raise ValueError("packed executor does not support dispatch/offload hooks")
@@ -543,7 +561,9 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     if config.num_attention_heads % config.num_key_value_heads:
         raise ValueError("query head count must be divisible by KV head count")
     _require_gfx950(device)
-    return base
+    with _PLAN_LOCK:
+        _QUALIFIED[base] = (fingerprint, index)
+    return fingerprint
 
 
 class _PackedLayer(DynamicLayer):
@@ -654,15 +674,26 @@ def _fused_layers_for(fused_layers, dtype: torch.dtype) -> bool:
     return bool(fused_layers)
 
 
-def _projection_plans_for(base, fused_projections, dtype: torch.dtype, selected: int):
+def _projection_plans_for(base, fused_projections, dtype: torch.dtype, selected: int, fingerprint=None):
     """Per-layer projection plans, or None for the modules' own linear layers.
     Default (None): on for fp16/bf16 caches when the selected rows fit one
-    kvr_linear_multi launch (at most 64); fp32 has no such kernel."""
+    kvr_linear_multi launch (at most 64); fp32 has no such kernel.
+    ``fingerprint`` (what _qualify returned for this call): when the plans were
+    built for the same module tree they are reused without per-layer checks."""
     if fused_projections is None:
         fused_projections = dtype in (torch.float16, torch.bfloat16) and selected <= _projection.MAX_ROWS
     if not fused_projections or dtype not in (torch.float16, torch.bfloat16) or selected > _projection.MAX_ROWS:
         return None
-    return [_layer_plans(layer) for layer in base.layers]
+    if fingerprint is not None:
+        with _PLAN_LOCK:
+            cached = _MODEL_PLANS.get(base)
+        if cached is not None and cached[0] is fingerprint:
+            return cached[1]
+    plans = [_layer_plans(layer) for layer in base.layers]
+    if fingerprint is not None:
+        with _PLAN_LOCK:
+            _MODEL_PLANS[base] = (fingerprint, plans)
+    return plans
 
 
 def _native_layers_for(native_layers, base, plans, fused_epilogue: bool, fused_layers: bool):
@@ -671,7 +702,7 @@ def _native_layers_for(native_layers, base, plans, fused_epilogue: bool, fused_l
     and every layer has a native descriptor and the same attention scale."""
     possible = (plans is not None and fused_epilogue and fused_layers
                 and all(p is not None and p.desc is not None for p in plans)
-                and len({float(layer.self_attn.scaling) for layer in base.layers}) == 1)
+                and len({float(layer._modules["self_attn"].scaling) for layer in base.layers}) == 1)
     if native_layers is None:
         return possible
     if native_layers and not possible:
@@ -762,14 +793,15 @@ def _native_refresh(base, launcher: _Launcher, plans, output, layer_count: int, 
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
                   attention_backend: str, writeback_backend: str, fused_epilogue: bool = True,
                   fused_layers: bool | None = None, fused_projections: bool | None = None,
-                  native_layers: bool | None = None) -> None:
-    """Run the packed forward, scattering into the caller-owned ``output`` cache."""
+                  native_layers: bool | None = None, fingerprint=None) -> None:
+    """Run the packed forward, scattering into the caller-owned ``output`` cache
+    (``fingerprint``: what _qualify returned for this call)."""
     base = shim._base_transformer(shim.generator)
     device_plan = host_plan.to(edited_ids_t.device)
     positions = device_plan.positions
     key0 = layer_kv(output, 0)[0]
     launcher = _launcher(device_plan, base.config, key0)
-    plans = _projection_plans_for(base, fused_projections, key0.dtype, device_plan.selected_count)
+    plans = _projection_plans_for(base, fused_projections, key0.dtype, device_plan.selected_count, fingerprint)
     fused_layers = _fused_layers_for(fused_layers, key0.dtype)
     if _native_layers_for(native_layers, base, plans, fused_epilogue, fused_layers):
         _native_refresh(base, launcher, plans, output, layer_count, edited_ids_t, positions)
@@ -826,13 +858,13 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     receipt = _receipt(intervals, selected, length, layer_count, attention_backend, writeback_backend)
     if not selected:
         return base_cache, receipt
-    _qualify(shim, edited_ids_t, base_cache, attention_backend, writeback_backend)
+    fingerprint = _qualify(shim, edited_ids_t, base_cache, attention_backend, writeback_backend)
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
     from ..cache import clone_cache
 
     output = clone_cache(base_cache)
     _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend,
-                  bool(fused_epilogue), fused_layers, fused_projections, native_layers)
+                  bool(fused_epilogue), fused_layers, fused_projections, native_layers, fingerprint)
     return output, receipt
 
 
@@ -860,8 +892,8 @@ def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tenso
     receipt["base_cache_ownership"] = "owned_in_place"
     if not selected:
         return receipt
-    _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
+    fingerprint = _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
     _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue),
-                  fused_layers, fused_projections, native_layers)
+                  fused_layers, fused_projections, native_layers, fingerprint)
     return receipt

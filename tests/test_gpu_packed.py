@@ -493,6 +493,57 @@ def test_projection_plans_match_module_linears(gpu_device, family, dtype):
 
 
 
+def test_model_changes_between_refreshes_are_seen(gpu_device):
+    """The executor caches the model's qualification and layer plans under a
+    fingerprint of the module tree (module and parameter identities, storage
+    addresses). Between two refreshes: new weight values in new storage are
+    used (not the cached pointers), a replaced module is seen, and a
+    parameter moved off the GPU is refused as on a first call."""
+    from kv_cache_repair_amd.kernels import packed_cache as pc
+
+    dtype = torch.bfloat16
+    model = make_model(gpu_device, "llama", kv_heads=2, head_dim=64, dtype=dtype, layers=3)
+    shim, ids, base = make_request(model, length=140)
+    edited = ids.clone()
+    edited[0, 70:] = (edited[0, 70:] + 7) % 97
+    intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
+    decoder = shim._base_transformer(model)
+
+    def close_to_module_linears(native):
+        plain, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=False)
+        for a, b in zip(native.layers, plain.layers):
+            for x, y in ((a.keys, b.keys), (a.values, b.values)):
+                xf, yf = x.float(), y.float()
+                ulp = torch.clamp(yf.abs(), min=2.0 ** -20) * 2.0 ** -7
+                assert ((xf - yf).abs() <= 2 * ulp).float().mean().item() >= 0.99
+                cos = torch.nn.functional.cosine_similarity(xf.reshape(-1, 64), yf.reshape(-1, 64), dim=-1)
+                assert cos.min().item() >= 0.9999
+
+    first, _ = pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True)
+    close_to_module_linears(first)
+    with torch.no_grad():  # new values in new storage; the old storage is released
+        proj = decoder.layers[0].self_attn.v_proj
+        proj.weight.data = (proj.weight.data.float() * -1.5).to(dtype)
+    changed, _ = pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True)
+    assert not torch.equal(changed.layers[2].values, first.layers[2].values)
+    close_to_module_linears(changed)
+    with torch.no_grad():  # a replaced module holding the same weight tensor, now with a bias
+        old = decoder.layers[1].mlp.down_proj
+        new = torch.nn.Linear(old.in_features, old.out_features, bias=True, device=gpu_device, dtype=dtype).eval()
+        new.weight = old.weight
+        new.bias.fill_(0.25)
+        decoder.layers[1].mlp.down_proj = new
+    replaced, _ = pc.packed_interval_repair(shim, base, edited, intervals)  # plans refused: module path
+    assert not torch.equal(replaced.layers[2].keys, changed.layers[2].keys)
+    close_to_module_linears(replaced)
+    with pytest.raises(ValueError, match="native_layers"):
+        pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True)
+    with torch.no_grad():
+        decoder.layers[2].mlp.up_proj.weight.data = decoder.layers[2].mlp.up_proj.weight.data.cpu()
+    with pytest.raises(ValueError, match="request device"):
+        pc.packed_interval_repair(shim, base, edited, intervals)
+
+
 @pytest.mark.parametrize("family", ["llama", "qwen3"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_native_layer_call_is_bit_identical_to_dispatched_fused_layers(gpu_device, family, dtype):
