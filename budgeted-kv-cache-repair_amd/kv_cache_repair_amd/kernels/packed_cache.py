@@ -204,6 +204,13 @@ class _LayerPlans:
     desc: Any = None  # kvr_layer_desc template (no cache pointers) for kvr_decoder_layer, or None
 
 
+class _PlanList(list):
+    """The layers' plans of one module tree; carries the descriptor template
+    that _native_layer_descs derives from them."""
+
+    descs_template = None
+
+
 _PLAN_CACHE: "weakref.WeakKeyDictionary[Any, _LayerPlans]" = weakref.WeakKeyDictionary()
 _PLAN_LOCK = Lock()
 # Per decoder (`base`): the fingerprint of the module tree that last passed
@@ -482,6 +489,16 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
     return view
 
 
+def _subtree_dicts(root, skip) -> list:
+    """The __dict__ of every module under ``root`` (itself included), level by
+    level through the `_modules` dicts, leaving out the subtree of ``skip``."""
+    found, level = [], [root.__dict__]
+    while level:
+        found += level
+        level = [m.__dict__ for attrs in level for m in attrs["_modules"].values() if m is not None and m is not skip]
+    return found
+
+
 def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend):
     """Fail closed outside the inspected contract, before any device work.
     Returns the module tree's fingerprint (see below) for _projection_plans_for."""
@@ -502,17 +519,7 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     # parameter off the request device (compared by index: get_device() is -1
     # off the GPUs, and the request device is a GPU when it matters below).
     index = device.index if device.type == "cuda" else -2
-    inner, outer = [], []
-    for root, found in ((base, inner), (model, outer)):
-        stack = [root]
-        pop, push, add = stack.pop, stack.extend, found.append
-        while stack:
-            module = pop()
-            if module is None or (found is outer and module is base):
-                continue
-            attrs = module.__dict__
-            add(attrs)
-            push(attrs["_modules"].values())
+    inner, outer = _subtree_dicts(base, None), _subtree_dicts(model, base)
     training = True in [attrs["training"] for attrs in inner]
     overridden = True in ["forward" in attrs for attrs in inner]
     everything = inner + outer
@@ -689,7 +696,7 @@ def _projection_plans_for(base, fused_projections, dtype: torch.dtype, selected:
             cached = _MODEL_PLANS.get(base)
         if cached is not None and cached[0] is fingerprint:
             return cached[1]
-    plans = [_layer_plans(layer) for layer in base.layers]
+    plans = _PlanList(_layer_plans(layer) for layer in base.layers)
     if fingerprint is not None:
         with _PLAN_LOCK:
             _MODEL_PLANS[base] = (fingerprint, plans)
@@ -714,17 +721,25 @@ def _native_layers_for(native_layers, base, plans, fused_epilogue: bool, fused_l
 def _native_layer_descs(plans, output, layer_count):
     """Per-refresh array of the layers' descriptors with this cache's pointers;
     each layer but the last computes the next layer's input norm in its down
-    projection's reduction, and the next layer skips it."""
-    descs = (_native.LayerDesc * layer_count)()
-    for i in range(layer_count):
-        keys, values = layer_kv(output, i)
-        descs[i] = plans[i].desc
-        desc = descs[i]
+    projection's reduction, and the next layer skips it. The cache-independent
+    part is built once per plan list and copied."""
+    template = getattr(plans, "descs_template", None)
+    if template is None or len(template) != layer_count:
+        template = (_native.LayerDesc * layer_count)()
+        for i in range(layer_count):
+            template[i] = plans[i].desc
+            desc = template[i]
+            if i + 1 < layer_count:
+                desc.next_norm, desc.eps_next = plans[i + 1].desc.input_norm, plans[i + 1].desc.eps_input
+            desc.input_normed = 1 if i > 0 else 0
+        if isinstance(plans, _PlanList):
+            plans.descs_template = template
+    descs = (_native.LayerDesc * layer_count).from_buffer_copy(template)
+    for desc, layer in zip(descs, output.layers):
+        keys, values = layer.keys, layer.values
         desc.cache_k, desc.cache_v = keys.data_ptr(), values.data_ptr()
-        desc.cache_strides[:] = (*_native.strides3(keys), *_native.strides3(values))
-        if i + 1 < layer_count:
-            desc.next_norm, desc.eps_next = plans[i + 1].desc.input_norm, plans[i + 1].desc.eps_input
-        desc.input_normed = 1 if i > 0 else 0
+        ks, vs = keys.stride(), values.stride()
+        desc.cache_strides[:] = (ks[1], ks[2], ks[3], vs[1], vs[2], vs[3])
     return descs
 
 
