@@ -868,6 +868,29 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     const int64_t group_row0 = static_cast<int64_t>(grp) * GR;
     const int64_t cstride = static_cast<int64_t>(GR);
 
+    // The partial O of this thread's first (row, slice, VEC dims) item for its
+    // first kPre chunks is loaded before phase 1 (every slot of the group is
+    // in bounds; slots of chunks a row does not attend hold stale values and
+    // are selected away), so the loads of both phases overlap.
+    const int dv = D / VEC;
+    constexpr int kPre = 4;
+    fvec pre[kPre];
+    {
+        const int e = threadIdx.x;
+        const int rr = e / (kSlices * dv);
+        const int sl = (e / dv) % kSlices;
+        const int d = (e % dv) * VEC;
+        const int r = r0 + rr;
+        const bool live = e < RB * kSlices * dv && r < GR && group_row0 + r < a.n_sel;
+        const float* po = a.ws_o + (slot0 + (live ? r : 0)) * D + (live ? d : 0);
+#pragma unroll
+        for (int j = 0; j < kPre; ++j) {
+            const int c = sl + kSlices * j;
+            pre[j] = fvec{};
+            if (live && c < n_chunks) pre[j] = *reinterpret_cast<const fvec*>(po + c * cstride * D);
+        }
+    }
+
     // phase 1: one wave per row
     const int wave = threadIdx.x / 64;
     const int lane = threadIdx.x % 64;
@@ -876,32 +899,54 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
         const int64_t row = group_row0 + r;
         int nv = 0;
         if (r < GR && row < a.n_sel) {
-            const int32_t tk = rows_kmax(a, group_row0 + (r / kRowTile) * kRowTile, kRowTile);
-            // chunk starts increase, so the attended chunks are the count of starts below tk
-            for (int c0 = 0; c0 < n_chunks; c0 += 64) {
-                const int c = c0 + lane;
-                nv += __popcll(__ballot(c < n_chunks && wk[kWorkInts * c + 2] < tk));
+            if (n_chunks <= 64) {
+                // one lane per chunk: the chunk start, m and l loads are independent of the row limit
+                const bool in = lane < n_chunks;
+                const int64_t s = (slot0 + (in ? lane : 0) * cstride + r) * 2;
+                const int32_t kb = in ? wk[kWorkInts * lane + 2] : 0;
+                const float mc = a.ws_ml[s];
+                const float lc = a.ws_ml[s + 1];
+                const int32_t tk = rows_kmax(a, group_row0 + (r / kRowTile) * kRowTile, kRowTile);
+                // chunk starts increase, so the attended chunks are a prefix
+                const bool att = in && kb < tk;
+                nv = __popcll(__ballot(att));
+                float mx = att ? mc : -INFINITY;
+                for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                const float m_use = (mx == -INFINITY) ? 0.f : mx;
+                float l = 0.f;
+                if (att) {
+                    const float w = exp2f(mc - m_use);
+                    W[rr * n_chunks + lane] = w;
+                    l = w * lc;
+                }
+                for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+                if (lane == 0) Linv[rr] = 1.f / l;
+            } else {
+                const int32_t tk = rows_kmax(a, group_row0 + (r / kRowTile) * kRowTile, kRowTile);
+                for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+                    const int c = c0 + lane;
+                    nv += __popcll(__ballot(c < n_chunks && wk[kWorkInts * c + 2] < tk));
+                }
+                float mx = -INFINITY;
+                for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, a.ws_ml[(slot0 + c * cstride + r) * 2]);
+                for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                const float m_use = (mx == -INFINITY) ? 0.f : mx;
+                float l = 0.f;
+                for (int c = lane; c < nv; c += 64) {
+                    const int64_t s = (slot0 + c * cstride + r) * 2;
+                    const float w = exp2f(a.ws_ml[s] - m_use);
+                    W[rr * n_chunks + c] = w;
+                    l += w * a.ws_ml[s + 1];
+                }
+                for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+                if (lane == 0) Linv[rr] = 1.f / l;
             }
-            float mx = -INFINITY;
-            for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, a.ws_ml[(slot0 + c * cstride + r) * 2]);
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            const float m_use = (mx == -INFINITY) ? 0.f : mx;
-            float l = 0.f;
-            for (int c = lane; c < nv; c += 64) {
-                const int64_t s = (slot0 + c * cstride + r) * 2;
-                const float w = exp2f(a.ws_ml[s] - m_use);
-                W[rr * n_chunks + c] = w;
-                l += w * a.ws_ml[s + 1];
-            }
-            for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-            if (lane == 0) Linv[rr] = 1.f / l;
         }
         if (lane == 0) NV[rr] = nv;
     }
     __syncthreads();
 
-    // phase 2: (row, slice, VEC dims) per thread-iteration; independent loads
-    const int dv = D / VEC;
+    // phase 2: (row, slice, VEC dims) per thread-iteration, chunks in slice order
     for (int e = threadIdx.x; e < RB * kSlices * dv; e += kMergeThreads) {
         const int rr = e / (kSlices * dv);
         const int sl = (e / dv) % kSlices;
@@ -912,8 +957,14 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
             const int nv = NV[rr];
             const float* po = a.ws_o + (slot0 + r) * D + d;
             const float* w = W + rr * n_chunks;
+            int c = sl;
+            if (e == static_cast<int>(threadIdx.x)) {
+#pragma unroll
+                for (int j = 0; j < kPre; ++j, c += kSlices)
+                    if (c < nv) acc += w[c] * pre[j];
+            }
 #pragma unroll 8
-            for (int c = sl; c < nv; c += kSlices)
+            for (; c < nv; c += kSlices)
                 acc += w[c] * *reinterpret_cast<const fvec*>(po + c * cstride * D);
         }
         *reinterpret_cast<fvec*>(Red + (rr * kSlices + sl) * D + d) = acc;
