@@ -97,7 +97,6 @@ shift_rows_vec_kernel(LayerTable tab, RowMap m, const float* __restrict__ inv_fr
     const int rows_per_pass = kBlockThreads >> tpr_log2;
     const int64_t total_rows = m.prefix_rows + m.tail_rows;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rows_per_pass * kRowPasses + (threadIdx.x >> tpr_log2);
-    if (row0 >= total_rows) return;
 
     const char* src = static_cast<const char*>(tab.src[kv][layer]);
     char* dst = static_cast<char*>(tab.dst[kv][layer]);
@@ -105,13 +104,7 @@ shift_rows_vec_kernel(LayerTable tab, RowMap m, const float* __restrict__ inv_fr
     const int64_t src_head = static_cast<int64_t>(head) * m.src_stride[0];
     const int64_t dst_head = static_cast<int64_t>(head) * m.dst_stride[0];
 
-    float cs_c[EPV], cs_s[EPV];
-    const bool any_rot = (kv == 0) && (m.rotate != 0) && (m.tail_rows > 0);
-    if (any_rot) {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) rope_cs<T>(inv_freq, chunk * EPV + e, m.shift_f, m.scaling, cs_c[e], cs_s[e]);
-    }
-
+    // Loads first (they do not depend on cos/sin), then the cos/sin table.
     u32x4 lo[kRowPasses], hi[kRowPasses];
     int64_t dst_off[kRowPasses];
     bool rot[kRowPasses], live[kRowPasses];
@@ -128,6 +121,23 @@ shift_rows_vec_kernel(LayerTable tab, RowMap m, const float* __restrict__ inv_fr
             dst_off[p] = (dst_head + dr * m.dst_stride[1]) + static_cast<int64_t>(chunk) * EPV;
             lo[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + so * E::size));
             hi[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (so + half) * E::size));
+        }
+    }
+
+    // Every rotated row uses the same shift: the block computes the half-row
+    // of cos/sin once into LDS (dynamic, 2 * half floats) and each thread reads
+    // its chunk's values (the same rope_cs roundings as one thread per value).
+    float cs_c[EPV], cs_s[EPV];
+    const bool any_rot = (kv == 0) && (m.rotate != 0) && (m.tail_rows > 0);  // block-uniform
+    if (any_rot) {
+        extern __shared__ float cs_lds[];  // [cos half][sin half]
+        for (int i = threadIdx.x; i < half; i += kBlockThreads)
+            rope_cs<T>(inv_freq, i, m.shift_f, m.scaling, cs_lds[i], cs_lds[half + i]);
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+            cs_c[e] = cs_lds[chunk * EPV + e];
+            cs_s[e] = cs_lds[half + chunk * EPV + e];
         }
     }
 #pragma unroll
@@ -205,7 +215,8 @@ int launch_shift(const LayerTable& tab, const RowMap& m, const float* inv_freq, 
     if (vec) {
         const int rows_per_block = (kBlockThreads >> tpr_log2) * kRowPasses;
         dim3 grid(static_cast<unsigned>(ceil_div(total_rows, rows_per_block)), m.n_heads * n_kv, n_layers);
-        shift_rows_vec_kernel<T><<<grid, kBlockThreads, 0, stream>>>(tab, m, inv_freq, n_kv, tpr_log2);
+        const size_t lds = m.rotate ? static_cast<size_t>(m.head_dim) * sizeof(float) : 0;  // cos + sin halves
+        shift_rows_vec_kernel<T><<<grid, kBlockThreads, lds, stream>>>(tab, m, inv_freq, n_kv, tpr_log2);
     } else {
         const int lanes_per_row = (m.rotary_dim >> 1) + (m.head_dim - m.rotary_dim);
         dim3 grid(static_cast<unsigned>(ceil_div(total_rows * lanes_per_row, kBlockThreads)), m.n_heads * n_kv,
