@@ -64,6 +64,40 @@ __device__ inline void rope_cs(const float* inv_freq, int i, float shift_f, floa
 }
 
 // One rotated pair: lo = k[i], hi = k[i + half].
+// bf16 pairs through v_cvt_pk_bf16_f32 (round to nearest even, as the
+// software rounding of elem<bf16_t> for every non-NaN value): the eager
+// sequence of rotate_pair for two elements at once. A NaN stays NaN through
+// the intermediate roundings; the final rounding returns torch's canonical
+// NaN (0x7FC0) for it.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ inline f32x2 round2_bf16(f32x2 v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    return f32x2{__uint_as_float(b << 16), __uint_as_float(b & 0xffff0000u)};
+}
+
+__device__ inline uint32_t pack2_bf16(f32x2 v) {
+    const float qnan = __uint_as_float(0x7fc00000u);
+    const f32x2 c = {v.x != v.x ? qnan : v.x, v.y != v.y ? qnan : v.y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(c, bf16x2));
+}
+
+// Rotated halves of two adjacent elements (e, e + 1): lo/hi hold the first- and
+// second-half inputs, c/s their cos/sin; returns the packed bf16 outputs.
+__device__ inline void rotate_pair2_bf16(uint32_t lo, uint32_t hi, f32x2 c, f32x2 s, uint32_t& out_lo,
+                                         uint32_t& out_hi) {
+#pragma clang fp contract(off)
+    const f32x2 l = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u)};
+    const f32x2 h = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+    const f32x2 a0 = round2_bf16(l * c);
+    const f32x2 b0 = round2_bf16((-h) * s);
+    const f32x2 a1 = round2_bf16(h * c);
+    const f32x2 b1 = round2_bf16(l * s);
+    out_lo = pack2_bf16(a0 + b0);
+    out_hi = pack2_bf16(a1 + b1);
+}
+
 template <typename T>
 __device__ inline void rotate_pair(float lo, float hi, float c, float s, float& out_lo, float& out_hi) {
 #pragma clang fp contract(off)
@@ -145,18 +179,29 @@ shift_rows_vec_kernel(LayerTable tab, RowMap m, const float* __restrict__ inv_fr
         if (!live[p]) continue;
         u32x4 olo = lo[p], ohi = hi[p];
         if (rot[p]) {
-            bits lb[EPV], hb[EPV], olb[EPV], ohb[EPV];
-            __builtin_memcpy(lb, &lo[p], 16);
-            __builtin_memcpy(hb, &hi[p], 16);
+            if constexpr (__is_same(T, bf16_t)) {
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                float a, b;
-                rotate_pair<T>(E::to_float(lb[e]), E::to_float(hb[e]), cs_c[e], cs_s[e], a, b);
-                olb[e] = E::from_float(a);
-                ohb[e] = E::from_float(b);
+                for (int q = 0; q < 4; ++q) {
+                    uint32_t rl, rh;
+                    rotate_pair2_bf16(lo[p][q], hi[p][q], f32x2{cs_c[2 * q], cs_c[2 * q + 1]},
+                                      f32x2{cs_s[2 * q], cs_s[2 * q + 1]}, rl, rh);
+                    olo[q] = rl;
+                    ohi[q] = rh;
+                }
+            } else {
+                bits lb[EPV], hb[EPV], olb[EPV], ohb[EPV];
+                __builtin_memcpy(lb, &lo[p], 16);
+                __builtin_memcpy(hb, &hi[p], 16);
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    float a, b;
+                    rotate_pair<T>(E::to_float(lb[e]), E::to_float(hb[e]), cs_c[e], cs_s[e], a, b);
+                    olb[e] = E::from_float(a);
+                    ohb[e] = E::from_float(b);
+                }
+                __builtin_memcpy(&olo, olb, 16);
+                __builtin_memcpy(&ohi, ohb, 16);
             }
-            __builtin_memcpy(&olo, olb, 16);
-            __builtin_memcpy(&ohi, ohb, 16);
         }
         __builtin_nontemporal_store(olo, reinterpret_cast<u32x4*>(dst + dst_off[p] * E::size));
         __builtin_nontemporal_store(ohi, reinterpret_cast<u32x4*>(dst + (dst_off[p] + half) * E::size));

@@ -127,6 +127,26 @@ def test_shifted_suffix_keys_equals_reference_eager_chain_on_device(gpu_device, 
     assert torch.equal(ours.view(torch.uint8), eager.contiguous().view(torch.uint8))
 
 
+@pytest.mark.parametrize("dim,theta", [(128, 5e5), (64, 1e4)])
+@pytest.mark.parametrize("shift", [-512, 7, -100000])
+def test_every_bf16_pattern_rotates_as_the_reference_eager_chain(gpu_device, dim, theta, shift):
+    """All 65536 bfloat16 bit patterns (zeros, denormals, infinities, NaNs) as
+    key elements, each meeting a random rotate_half partner: the kernel's
+    hardware round-to-nearest-even pairs give the eager chain's bits,
+    torch's canonical NaN (0x7FC0) included."""
+    from kv_cache_repair_amd.cache import OperatorShim, shifted_suffix_keys
+
+    model = _tiny_llama(gpu_device, torch.bfloat16, theta=theta, dim=dim)
+    pattern = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    for seed in (0, 1):
+        order = torch.randperm(65536, generator=torch.Generator().manual_seed(seed)) if seed else torch.arange(65536)
+        key = pattern[order].view(torch.bfloat16).reshape(1, 2, -1, dim).to(gpu_device)
+        ours = shifted_suffix_keys(OperatorShim(model), key, shift)
+        eager = ref.shifted_suffix_keys(model, key, shift)
+        torch.cuda.synchronize()
+        assert torch.equal(ours.view(torch.int16), eager.contiguous().view(torch.int16))
+
+
 def test_build_halo_cache_matches_reference_config1(gpu_device):
     """tiny Llama, 256 ids, delete positions 64-95 (shift -32)."""
     from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache
