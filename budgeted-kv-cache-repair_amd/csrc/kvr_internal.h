@@ -43,12 +43,13 @@ template <> struct elem<bf16_t> {
     static constexpr int size = 2;
     __device__ static inline float to_float(bits b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
     // Round-to-nearest-even with a canonical quiet NaN (0x7FC0): the rounding
-    // that PyTorch's bfloat16 tensor ops apply to their fp32 results.
+    // that PyTorch's bfloat16 tensor ops apply to their fp32 results. The
+    // conversion is gfx950's v_cvt_pk_bf16_f32 (round to nearest even,
+    // denormals kept: the same bits as adding 0x7FFF plus the kept lsb and
+    // truncating, for every non-NaN fp32 value); NaN is replaced after it.
     __device__ static inline bits from_float(float f) {
-        uint32_t u = __float_as_uint(f);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>(0x7fc0u);
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return static_cast<uint16_t>(u >> 16);
+        const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+        return f != f ? static_cast<uint16_t>(0x7fc0u) : b;
     }
 };
 
