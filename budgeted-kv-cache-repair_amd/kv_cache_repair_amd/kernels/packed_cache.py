@@ -501,7 +501,8 @@ def _subtree_dicts(root, skip) -> list:
 
 def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend):
     """Fail closed outside the inspected contract, before any device work.
-    Returns the module tree's fingerprint (see below) for _projection_plans_for."""
+    Returns (the module tree's fingerprint (see below) for _projection_plans_for,
+    whether any decoder module or the process carries forward hooks)."""
     if transformers.__version__ not in _SUPPORTED_TRANSFORMERS:
         raise ValueError(f"packed HIP executor requires transformers in {_SUPPORTED_TRANSFORMERS}")
     from transformers.models.llama.modeling_llama import LlamaForCausalLM, LlamaModel
@@ -524,6 +525,12 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     overridden = True in ["forward" in attrs for attrs in inner]
     everything = inner + outer
     hooked = True in [attrs.get("_hf_hook") is not None for attrs in everything]
+    # Forward hooks on the decoder's modules (or global ones) run only where the
+    # modules' own forwards run: the refresh then takes the module path.
+    from torch.nn.modules import module as _module
+
+    forward_hooked = (True in [bool(attrs["_forward_hooks"]) or bool(attrs["_forward_pre_hooks"]) for attrs in inner]
+                      or bool(_module._global_forward_hooks) or bool(_module._global_forward_pre_hooks))
     # Fingerprint of the tree: every module (its __dict__'s identity) and every
     # parameter slot (the tensor's identity and storage address; an empty slot
     # counts). A tree with the fingerprint that last qualified on this GPU has
@@ -570,7 +577,7 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     _require_gfx950(device)
     with _PLAN_LOCK:
         _QUALIFIED[base] = (fingerprint, index)
-    return fingerprint
+    return fingerprint, forward_hooked
 
 
 class _PackedLayer(DynamicLayer):
@@ -808,9 +815,17 @@ def _native_refresh(base, launcher: _Launcher, plans, output, layer_count: int, 
 def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_count: int,
                   attention_backend: str, writeback_backend: str, fused_epilogue: bool = True,
                   fused_layers: bool | None = None, fused_projections: bool | None = None,
-                  native_layers: bool | None = None, fingerprint=None) -> None:
+                  native_layers: bool | None = None, qualified=(None, False)) -> None:
     """Run the packed forward, scattering into the caller-owned ``output`` cache
-    (``fingerprint``: what _qualify returned for this call)."""
+    (``qualified``: what _qualify returned for this call). With forward hooks
+    present the projections, norms and layers run as the modules themselves
+    (the fused kernels would skip the hooks); asking for them then is an error."""
+    fingerprint, forward_hooked = qualified
+    if forward_hooked:
+        if fused_layers or fused_projections or native_layers:
+            raise ValueError("module forward hooks need the module path: fused_layers, fused_projections and "
+                             "native_layers must not be requested")
+        fused_layers = fused_projections = native_layers = False
     base = shim._base_transformer(shim.generator)
     device_plan = host_plan.to(edited_ids_t.device)
     positions = device_plan.positions
@@ -873,13 +888,13 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     receipt = _receipt(intervals, selected, length, layer_count, attention_backend, writeback_backend)
     if not selected:
         return base_cache, receipt
-    fingerprint = _qualify(shim, edited_ids_t, base_cache, attention_backend, writeback_backend)
+    qualified = _qualify(shim, edited_ids_t, base_cache, attention_backend, writeback_backend)
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
     from ..cache import clone_cache
 
     output = clone_cache(base_cache)
     _refresh_into(shim, output, edited_ids_t, host_plan, layer_count, attention_backend, writeback_backend,
-                  bool(fused_epilogue), fused_layers, fused_projections, native_layers, fingerprint)
+                  bool(fused_epilogue), fused_layers, fused_projections, native_layers, qualified)
     return output, receipt
 
 
@@ -907,8 +922,8 @@ def packed_refresh_owned_(shim: Any, owned_cache: Any, edited_ids_t: torch.Tenso
     receipt["base_cache_ownership"] = "owned_in_place"
     if not selected:
         return receipt
-    fingerprint = _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
+    qualified = _qualify(shim, edited_ids_t, owned_cache, "hip", "hip")
     host_plan = plan if plan is not None else IndexedPlan(selected, length)
     _refresh_into(shim, owned_cache, edited_ids_t, host_plan, layer_count, "hip", "hip", bool(fused_epilogue),
-                  fused_layers, fused_projections, native_layers, fingerprint)
+                  fused_layers, fused_projections, native_layers, qualified)
     return receipt

@@ -544,6 +544,39 @@ def test_model_changes_between_refreshes_are_seen(gpu_device):
         pc.packed_interval_repair(shim, base, edited, intervals)
 
 
+def test_forward_hooks_take_the_module_path(gpu_device):
+    """A forward hook on a decoder module runs as in the reference's packed
+    forward (the modules' own forwards): the fused projections, norms and
+    native layers, which would skip it, are off by default and refused when
+    asked for; without hooks the fused path is back."""
+    from kv_cache_repair_amd.kernels import packed_cache as pc
+
+    model = make_model(gpu_device, "llama", kv_heads=2, head_dim=64, dtype=torch.bfloat16, layers=3)
+    shim, ids, base = make_request(model, length=140)
+    edited = ids.clone()
+    edited[0, 70:] = (edited[0, 70:] + 7) % 97
+    intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
+    decoder = shim._base_transformer(model)
+    calls = []
+    handle = decoder.layers[1].self_attn.q_proj.register_forward_hook(lambda m, args, out: calls.append(out.shape))
+    try:
+        hooked, _ = pc.packed_interval_repair(shim, base, edited, intervals)
+        assert calls == [torch.Size([1, 31, 256])]  # the hooked projection ran once, over the 31 selected rows
+        plain, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=False,
+                                             fused_layers=False, native_layers=False)
+        assert all(torch.equal(a.keys.view(torch.int16), b.keys.view(torch.int16))
+                   and torch.equal(a.values.view(torch.int16), b.values.view(torch.int16))
+                   for a, b in zip(hooked.layers, plain.layers))
+        for option in ("native_layers", "fused_projections", "fused_layers"):
+            with pytest.raises(ValueError, match="module path"):
+                pc.packed_interval_repair(shim, base, edited, intervals, **{option: True})
+    finally:
+        handle.remove()
+    calls.clear()
+    pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True)  # accepted again
+    assert calls == []
+
+
 @pytest.mark.parametrize("family", ["llama", "qwen3"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_native_layer_call_is_bit_identical_to_dispatched_fused_layers(gpu_device, family, dtype):
