@@ -189,17 +189,15 @@ __global__ void __launch_bounds__(kThreads) query_relevance_kernel(ScoreArgs a) 
 // v_mfma_f32_16x16x32 (A = 16 gathered token rows, B = 16 query rows, both
 // straight from global memory: the query rows stay in L2), fp32 accumulation
 // of exact 16-bit products. The squared norms are summed from the same
-// fragments. A wave computes 16 tokens over SPLIT-th of the hidden axis:
-// a block of 4 waves covers 64 / SPLIT tokens, and the SPLIT waves of one
-// token group add their partial dot products and norms in LDS (wave order
-// fixed). SPLIT grows as the prompt shrinks so that a launch still has about
-// two blocks per CU (SPLIT 4: 480 blocks for a 7680-token prompt; SPLIT 1:
-// 496 blocks for 31744 tokens). Up to kQTiles x 16 queries per pass (more
-// queries take further passes over the token rows).
-constexpr int kQTiles = 4;
-constexpr int kMfmaWaves = kThreads / 64;
-constexpr int kMfmaMinTokens = 16;  // tokens per block at SPLIT 4
-constexpr int kParts = 5 * kQTiles + 1;  // per lane: kQTiles x 4 dots, kQTiles query norms, 1 token norm
+// fragments. A wave computes 16 tokens over SPLIT-th of the hidden axis: a
+// block of max(4, SPLIT) waves covers 16 * waves / SPLIT tokens, and the
+// SPLIT waves of one token group add their partial dot products and norms in
+// LDS (wave order fixed). SPLIT grows as the prompt shrinks so that a launch
+// keeps every CU busy (SPLIT 8: 480 blocks of 8 waves for a 7680-token
+// prompt; SPLIT 1: 496 blocks of 4 waves for 31744 tokens). QT x 16 queries
+// per pass (QT 1 for up to 16 queries, else 4; more queries take further
+// passes over the token rows).
+constexpr int kMfmaMinTokens = 16;  // tokens per block at SPLIT 8
 
 template <typename T> struct score_mma;
 template <> struct score_mma<bf16_t> {
@@ -228,19 +226,22 @@ __device__ inline float sumsq8(u32x4 v) {
     return s;
 }
 
-template <typename T, int SPLIT>
-__global__ void __launch_bounds__(kThreads) query_relevance_mfma_kernel(ScoreArgs a) {
+template <typename T, int SPLIT, int QT>
+__global__ void __launch_bounds__(64 * (SPLIT > 4 ? SPLIT : 4)) query_relevance_mfma_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
     using M = score_mma<T>;
     using v8 = typename M::v8;
-    static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "SPLIT divides the block's 4 waves");
+    static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4 || SPLIT == 8, "SPLIT divides the block's waves");
+    constexpr int kMfmaWaves = SPLIT > 4 ? SPLIT : 4;
+    constexpr int kQTiles = QT;
+    constexpr int kParts = 5 * kQTiles + 1;  // per lane: kQTiles x 4 dots, kQTiles query norms, 1 token norm
     __shared__ float part[SPLIT > 1 ? kMfmaWaves : 1][kParts][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int hpart = wave % SPLIT;  // this wave's part of the hidden axis
     const int lq = lane & 15;
     const int lj = lane >> 4;
-    const int64_t tbase = static_cast<int64_t>(blockIdx.x) * (64 / SPLIT) + (wave / SPLIT) * 16;
+    const int64_t tbase = static_cast<int64_t>(blockIdx.x) * (16 * kMfmaWaves / SPLIT) + (wave / SPLIT) * 16;
     // this lane's A row: token tbase + lq (clamped in bounds; its score is not written)
     const int64_t t = tbase + lq;
     int64_t id = -1;
@@ -380,21 +381,31 @@ __global__ void __launch_bounds__(kThreads) query_relevance_mfma_kernel(ScoreArg
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// SPLIT: the smallest of 1, 2, 4, 8 whose grid still covers the CUs about
+// twice (>= 480 blocks of 64 / SPLIT tokens; 8-wave blocks of 16 tokens below).
+template <typename T, int QT>
+int launch_mfma_split(const ScoreArgs& a, hipStream_t s) {
+    const int64_t blocks1 = (a.n + 63) / 64;
+    const unsigned b16 = static_cast<unsigned>((a.n + 15) / 16);
+    if (blocks1 >= 480) {
+        query_relevance_mfma_kernel<T, 1, QT><<<static_cast<unsigned>(blocks1), 256, 0, s>>>(a);
+    } else if (blocks1 >= 240) {
+        query_relevance_mfma_kernel<T, 2, QT><<<static_cast<unsigned>((a.n + 31) / 32), 256, 0, s>>>(a);
+    } else if (blocks1 >= 160) {
+        query_relevance_mfma_kernel<T, 4, QT><<<b16, 256, 0, s>>>(a);
+    } else {
+        query_relevance_mfma_kernel<T, 8, QT><<<b16, 512, 0, s>>>(a);
+    }
+    return launch_status();
+}
+
 template <typename T>
 int launch_scores(const ScoreArgs& a, size_t lds, hipStream_t s) {
     const int esize = elem<T>::size;
     if constexpr (!__is_same(T, f32_t)) {
         if (a.hidden % 32 == 0 && (a.ld_embed * esize) % 16 == 0 && aligned16(a.embed)) {
-            // SPLIT: the largest of 1, 2, 4 that keeps >= 480 blocks (else 4)
-            const int64_t blocks1 = (a.n + 63) / 64;
-            if (blocks1 >= 480) {
-                query_relevance_mfma_kernel<T, 1><<<static_cast<unsigned>(blocks1), kThreads, 0, s>>>(a);
-            } else if (blocks1 >= 240) {
-                query_relevance_mfma_kernel<T, 2><<<static_cast<unsigned>((a.n + 31) / 32), kThreads, 0, s>>>(a);
-            } else {
-                query_relevance_mfma_kernel<T, 4><<<static_cast<unsigned>((a.n + 15) / 16), kThreads, 0, s>>>(a);
-            }
-            return launch_status();
+            if (a.n_query <= 16) return launch_mfma_split<T, 1>(a, s);
+            return launch_mfma_split<T, 4>(a, s);
         }
     }
     const unsigned grid = static_cast<unsigned>((a.n + kTokensPerBlock - 1) / kTokensPerBlock);

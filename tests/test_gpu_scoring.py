@@ -77,10 +77,12 @@ def test_rejects_empty_query_and_out_of_range_query_ids(gpu_device):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-# token counts pick each MFMA launch shape: 40000 -> 64 tokens per block, 20000 -> 32, <= 15359 -> 16;
-# more than 64 queries take several passes
-@pytest.mark.parametrize("hidden,n,n_query", [(4096, 20000, 20), (1024, 40000, 70), (256, 900, 100), (100, 3001, 5),
-                                             (2048, 1025, 17), (64, 7, 1)])
+# token counts pick each MFMA launch shape (hidden axis over 1, 2, 4 or 8 waves): 40000 and 36000 -> 1,
+# 20000 -> 2, 12000 -> 4, <= 10176 -> 8; up to 16 queries take one query tile per pass, more take four, more
+# than 64 several passes
+@pytest.mark.parametrize("hidden,n,n_query", [(4096, 20000, 20), (1024, 40000, 70), (256, 36000, 9),
+                                             (512, 12000, 3), (256, 900, 100), (100, 3001, 5), (2048, 1025, 17),
+                                             (64, 7, 1)])
 @pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
 def test_scores_match_the_oracle_and_the_eager_restatement(gpu_device, dtype, hidden, n, n_query, ids_dtype):
     from kv_cache_repair_amd.scoring import dense_query_relevance_scores
