@@ -14,7 +14,8 @@
 // projections never reach HBM.
 //
 // Work split: block = 4 waves x 16 streamed weight rows (64 rows) x one K
-// slice. The slice is walked in chunks of 256: x[:, chunk] is staged in one of
+// slice. The slice is walked in chunks of 256 (128 in launches with more blocks
+// than CUs): x[:, chunk] is staged in one of
 // two LDS buffers (the next chunk's global loads are in flight while the
 // current one is multiplied) and shared by the 4 waves; W streams into
 // registers through a ring of 8 loads per lane (one chunk ahead), each load
@@ -48,21 +49,29 @@ constexpr int kTileN = 16 * kWaves;         // streamed weight rows per block
 constexpr int kHalf = kTileN / 2;           // gated: output columns per block
 constexpr int kRowsMax = 64;                // M <= 64 (four 16-row MFMA tiles)
 constexpr int kStep = 32;                   // K per MFMA
-constexpr int kChunkSteps = KVR_GEMM_CHUNK_STEPS;  // k-steps per staged x chunk = W ring depth
-constexpr int kChunk = kChunkSteps * kStep; // K per chunk
-constexpr int kXStride = kChunk + 8;        // LDS row stride (elements): 16 B pad, conflict-free B reads
-constexpr int kXBuf = kRowsMax * kXStride;  // one chunk buffer (elements)
+constexpr int kSliceChunk = KVR_GEMM_CHUNK_STEPS * kStep;  // split-K slices are whole multiples of this
 constexpr int kRingChunks = KVR_GEMM_RING_CHUNKS;  // W ring depth in chunks
-#ifndef KVR_GEMM_RING
-#define KVR_GEMM_RING (KVR_GEMM_RING_CHUNKS * KVR_GEMM_CHUNK_STEPS)
-#endif
-constexpr int kRing = KVR_GEMM_RING;               // W fragments in flight per lane (k-steps)
 static_assert(kRingChunks == 1 || kRingChunks == 2, "chunk buffers alternate with the ring");
-static_assert((kRingChunks * kChunkSteps) % kRing == 0, "ring slots repeat within the unrolled chunks");
-static_assert(kRing % 2 == 0 && kChunkSteps % 2 == 0, "whole-line loads come in pairs");
-constexpr int kGranules = kChunk / 8;       // 16-B x granules per row per chunk
-constexpr int kXLoads = kRowsMax * kGranules / kComputeThreads;  // x granules per thread per chunk
-static_assert(kXLoads * kComputeThreads == kRowsMax * kGranules && kComputeThreads % kGranules == 0, "x staging map");
+
+// Staged x chunk of CS k-steps (CS = the W ring depth per chunk): 8 for
+// launches of at most one block per CU, 4 (half the LDS, chunks turned over
+// twice as often) where some CUs run two blocks.
+template <int CS>
+struct ChunkCfg {
+    static constexpr int kChunkSteps = CS;            // k-steps per staged x chunk = W ring depth
+    static constexpr int kChunk = CS * kStep;         // K per chunk
+    static constexpr int kXStride = kChunk + 8;       // LDS row stride (elements): 16 B pad, conflict-free B reads
+    static constexpr int kXBuf = kRowsMax * kXStride; // one chunk buffer (elements)
+    static constexpr int kRing = kRingChunks * CS;    // W fragments in flight per lane (k-steps)
+    static constexpr int kGranules = kChunk / 8;      // 16-B x granules per row per chunk
+    static constexpr int kXLoads = kRowsMax * kGranules / kComputeThreads;  // x granules per thread per chunk
+    // two x chunk buffers + the per-wave W transpose tiles
+    static constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + kWaves * 2048;
+    static_assert(kRing % 2 == 0 && CS % 2 == 0, "whole-line loads come in pairs");
+    static_assert(kSliceChunk % kChunk == 0, "slices are whole chunks");
+    static_assert(kXLoads * kComputeThreads == kRowsMax * kGranules && kComputeThreads % kGranules == 0,
+                  "x staging map");
+};
 constexpr int kMinSlice = 512;              // K per split at least (bounds the partial traffic)
 #ifndef KVR_GEMM_TARGET_BLOCKS
 #define KVR_GEMM_TARGET_BLOCKS 256
@@ -123,12 +132,20 @@ __device__ inline float with_residual(const GemmArgs& a, float sum, int m, int c
 // the waves stream gate rows tile*kHalf + 16w + 0..15 and the second half the
 // same rows of up. The fp32 tile (column c = 16w + 4lj + i) thus holds gate
 // in columns [0, kHalf) and up in [kHalf, kTileN) in gated mode.
-template <typename T, int MT>
+template <typename T, int MT, int CS>
 __global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))  // two blocks per CU
 skinny_gemm_kernel(GemmArgs a) {
     using G = gemm_t<T>;
     using E = elem<T>;
     using v8 = typename G::v8;
+    using K = ChunkCfg<CS>;
+    constexpr int kChunkSteps = K::kChunkSteps;
+    constexpr int kChunk = K::kChunk;
+    constexpr int kXStride = K::kXStride;
+    constexpr int kXBuf = K::kXBuf;
+    constexpr int kRing = K::kRing;
+    constexpr int kGranules = K::kGranules;
+    constexpr int kXLoads = K::kXLoads;
     extern __shared__ __align__(16) char smem[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // two chunk buffers [64][kXStride]
 
@@ -369,9 +386,7 @@ __global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(GemmArgs 
     }
 }
 
-// two x chunk buffers + the per-wave W transpose tiles
-constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + kWaves * 2048;
-static_assert(kLdsBytes >= static_cast<size_t>(kRowsMax) * kRedStride * 4, "gated epilogue tile fits");
+static_assert(ChunkCfg<4>::kLdsBytes >= static_cast<size_t>(kRowsMax) * kRedStride * 4, "gated epilogue tile fits");
 
 template <typename F>
 bool allow_lds(F fn, size_t bytes) {
@@ -380,12 +395,22 @@ bool allow_lds(F fn, size_t bytes) {
                                static_cast<int>(bytes)) == hipSuccess;
 }
 
+template <typename T, int MT, int CS>
+int launch_cs(const GemmArgs& a, dim3 grid, hipStream_t s) {
+    constexpr size_t lds = ChunkCfg<CS>::kLdsBytes;
+    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT, CS>, lds);
+    if (!ok) return KVR_E_LAUNCH_FAILED;
+    skinny_gemm_kernel<T, MT, CS><<<grid, kGemmThreads, lds, s>>>(a);
+    return KVR_OK;
+}
+
 template <typename T, int MT>
 int launch_mt(const GemmArgs& a, hipStream_t s, bool reduce) {
-    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT>, kLdsBytes);
-    if (!ok) return KVR_E_LAUNCH_FAILED;
     const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, kTileN)), static_cast<unsigned>(a.splits));
-    skinny_gemm_kernel<T, MT><<<grid, kGemmThreads, kLdsBytes, s>>>(a);
+    // more blocks than CUs (some CUs run two): 4-step chunks; else 8
+    const int st = static_cast<int64_t>(grid.x) * grid.y > kTargetBlocks ? launch_cs<T, MT, 4>(a, grid, s)
+                                                                        : launch_cs<T, MT, 8>(a, grid, s);
+    if (st != KVR_OK) return st;
     if (a.splits > 1 && reduce)
         splitk_reduce_kernel<T><<<dim3(grid.x, static_cast<unsigned>(MT)), kReduceThreads, 0, s>>>(a);
     return launch_status();
@@ -423,7 +448,7 @@ Split plan_split(int32_t rows, int32_t k) {
     while (tiles * want < kTargetBlocks && want < 64) want *= 2;
     const int32_t cap = k / kMinSlice > 1 ? k / kMinSlice : 1;
     const int32_t s = want < cap ? want : cap;
-    const int32_t slice = static_cast<int32_t>(ceil_div(ceil_div(k, s), kChunk) * kChunk);
+    const int32_t slice = static_cast<int32_t>(ceil_div(ceil_div(k, s), kSliceChunk) * kSliceChunk);
     return Split{static_cast<int32_t>(ceil_div(k, slice)), slice};
 }
 }  // namespace
