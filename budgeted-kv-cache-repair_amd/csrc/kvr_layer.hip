@@ -87,16 +87,16 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_kernel(NormArgs a) {
 // partial sums through LDS.
 constexpr int kMaxVec = 4;
 
-template <typename T, int NV>
-__global__ void __launch_bounds__(kNormThreads) rms_norm_vec_kernel(NormArgs a, int tpr_log2) {
+template <typename T, int NV, int NT>
+__global__ void __launch_bounds__(NT) rms_norm_vec_kernel(NormArgs a, int tpr_log2) {
 #pragma clang fp contract(off)
     using E = elem<T>;
     using bits = typename E::bits;
     constexpr int V = 16 / E::size;  // elements per vector
-    __shared__ float partial[kNormThreads / 64];
+    __shared__ float partial[NT / 64];
     const int tpr = 1 << tpr_log2;
     const int t = threadIdx.x & (tpr - 1);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kNormThreads >> tpr_log2) + (threadIdx.x >> tpr_log2);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (NT >> tpr_log2) + (threadIdx.x >> tpr_log2);
     const bool live = row < a.rows;
     const int nvec = a.hidden / V;
     const char* x = a.x ? a.x + row * a.x_stride * E::size : nullptr;
@@ -233,18 +233,31 @@ int launch_norm(const NormArgs& a, hipStream_t s, bool require_vec = false) {
                aligned16(a.out) && aligned16(a.weight) &&
                (!a.residual || (a.r_stride % V == 0 && a.ro_stride % V == 0 && aligned16(a.residual) &&
                                 aligned16(a.residual_out)));
+    // Rows of at least 512 vectors take a 512-thread block each (twice the
+    // loads in flight per row); shorter rows share 256-thread blocks.
+    const bool wide = nvec >= 512;
+    const int nt = wide ? 512 : kNormThreads;
     int tpr_log2 = 0;
-    while ((int64_t(1) << tpr_log2) < nvec && tpr_log2 < 8) ++tpr_log2;
+    while ((int64_t(1) << tpr_log2) < nvec && (1 << tpr_log2) < nt) ++tpr_log2;
     const int64_t per_thread = ceil_div(nvec, int64_t(1) << tpr_log2);
     vec = vec && per_thread <= kMaxVec && nvec > 0;
     if (vec) {
-        const int64_t blocks = ceil_div(a.rows, kNormThreads >> tpr_log2);
+        const int64_t blocks = ceil_div(a.rows, nt >> tpr_log2);
         const unsigned g = static_cast<unsigned>(blocks);
-        switch (per_thread) {
-            case 1: rms_norm_vec_kernel<T, 1><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
-            case 2: rms_norm_vec_kernel<T, 2><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
-            case 3: rms_norm_vec_kernel<T, 3><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
-            default: rms_norm_vec_kernel<T, 4><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
+        if (wide) {
+            switch (per_thread) {
+                case 1: rms_norm_vec_kernel<T, 1, 512><<<g, 512, 0, s>>>(a, tpr_log2); break;
+                case 2: rms_norm_vec_kernel<T, 2, 512><<<g, 512, 0, s>>>(a, tpr_log2); break;
+                case 3: rms_norm_vec_kernel<T, 3, 512><<<g, 512, 0, s>>>(a, tpr_log2); break;
+                default: rms_norm_vec_kernel<T, 4, 512><<<g, 512, 0, s>>>(a, tpr_log2); break;
+            }
+        } else {
+            switch (per_thread) {
+                case 1: rms_norm_vec_kernel<T, 1, kNormThreads><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
+                case 2: rms_norm_vec_kernel<T, 2, kNormThreads><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
+                case 3: rms_norm_vec_kernel<T, 3, kNormThreads><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
+                default: rms_norm_vec_kernel<T, 4, kNormThreads><<<g, kNormThreads, 0, s>>>(a, tpr_log2); break;
+            }
         }
         return launch_status();
     }
