@@ -19,7 +19,7 @@
 namespace kvr {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 64;  // one wave per block: a refresh's few thousand head rows reach ~4x more CUs
 
 struct FreshArgs {
     const char* q;
