@@ -152,14 +152,18 @@ template <> struct mma_t<f16_t> {
 };
 
 // LDS layout of one staged 64-key sub-tile: K row-major [64][D + 8] then V
-// transposed [D][64 + 4] (16-bit elements). The paddings make the 16-byte
-// K-fragment reads, the 8-byte V^T-fragment reads and the 4-byte transposing
-// V writes conflict-free within each 16/32-lane phase.
+// transposed [D][64 + 8] (16-bit elements; 16-byte aligned rows). V^T column
+// of key k of a sub-tile: k = 32h + 16a + 4j + i sits at 32h + 8j + 4a + i,
+// so the 8 keys a lane's PV fragment pairs with P^T (keys 32h + 4j + i and
+// 32h + 16 + 4j + i) are one 16-byte read; key pairs stay adjacent for the
+// 4-byte transposing V writes.
+__device__ inline int vt_pos(int k) { return (k & 32) | ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3); }
+
 template <int D, int QT>
 struct MfmaCfg {
     static constexpr int threads = 128 * QT;  // two waves per query head
     static constexpr int kstr = D + 8;
-    static constexpr int vstr = kSub + 4;
+    static constexpr int vstr = kSub + 8;
     static constexpr int k_elems = kSub * kstr;
     static constexpr int v_elems = D * vstr;
     static constexpr int buf_elems = k_elems + v_elems;
@@ -267,10 +271,8 @@ struct MfmaWave {
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint16_t* row = Vt + (16 * dt + lq) * C::vstr + 32 * h + 4 * lj;
-                const uint2 lo = *reinterpret_cast<const uint2*>(row);
-                const uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
-                const v8 vf = __builtin_bit_cast(v8, u32x4{lo.x, lo.y, hi.x, hi.y});
+                const uint16_t* row = Vt + (16 * dt + lq) * C::vstr + 32 * h + 8 * lj;
+                const v8 vf = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(row));
                 if (A0) {
                     o[0][dt] = M::mma(vf, __builtin_bit_cast(v8, phi[0][h]), o[0][dt]);
                     o[0][dt] = M::mma(vf, __builtin_bit_cast(v8, plo[0][h]), o[0][dt]);
@@ -387,7 +389,7 @@ attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t x0 = v0[j], x1 = v1[j];
-                    uint16_t* col = Vt + (8 * c8 + 2 * j) * C::vstr + 2 * pr;
+                    uint16_t* col = Vt + (8 * c8 + 2 * j) * C::vstr + vt_pos(2 * pr);
                     *reinterpret_cast<uint32_t*>(col) = (x0 & 0xffffu) | (x1 << 16);
                     *reinterpret_cast<uint32_t*>(col + C::vstr) = (x0 >> 16) | (x1 & 0xffff0000u);
                 }
@@ -595,7 +597,7 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const uint32_t x0 = v0[q], x1 = v1[q];
-                        uint16_t* col = Vt + (8 * c8 + 2 * q) * C::vstr + 2 * pr;
+                        uint16_t* col = Vt + (8 * c8 + 2 * q) * C::vstr + vt_pos(2 * pr);
                         *reinterpret_cast<uint32_t*>(col) = (x0 & 0xffffu) | (x1 << 16);
                         *reinterpret_cast<uint32_t*>(col + C::vstr) = (x0 >> 16) | (x1 & 0xffff0000u);
                     }
