@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 namespace kvr {
@@ -1128,6 +1129,39 @@ struct Chunk {
     int32_t group, index, begin, end;
 };
 
+// ---------------------------------------------------------------------------
+// Static scratch of kvr_packed_causal_attention_noalloc: the split-K partials
+// live in this file-scope device array instead of a caller workspace. Each
+// device that runs the library holds its own copy until the process ends. In
+// host code the array's name is only a stand-in for the device symbol: the
+// device address comes from hipGetSymbolAddress, looked up once per device
+// (with that device current) and kept per device.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device of `stream` (which must be the
+// current device); nullptr when the lookup fails.
+void* scratch_address(void* stream) {
+    int current = -1;
+    if (hipGetDevice(&current) != hipSuccess || current < 0 || current >= kMaxDevices) return nullptr;
+    if (stream) {
+        int owner = -1;
+        if (hipStreamGetDevice(as_stream(stream), &owner) != hipSuccess || owner != current) return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[current]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_ptr[current] = ptr;
+    }
+    return g_scratch_ptr[current];
+}
+
 }  // namespace
 }  // namespace kvr
 
@@ -1299,12 +1333,17 @@ extern "C" int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_
     return static_cast<int64_t>(n_q_heads) * schedule[H_NWORK] * schedule[H_GROUP_ROWS] * (head_dim + 2) * 4;
 }
 
-extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const void* v, void* out,
-                                           const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
-                                           int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, float scale,
-                                           const int64_t strides[12], const int32_t* schedule, int64_t schedule_len,
-                                           const int32_t* host_schedule, void* workspace, int64_t workspace_bytes,
-                                           int32_t dtype, void* stream) {
+namespace {
+
+// Argument checks and launches of kvr_packed_causal_attention; `workspace` is
+// the caller's buffer, or the library's static scratch array for the
+// no-allocation entry point (`scratch_limit` > 0: a request needing more than
+// that many bytes is refused before anything is launched).
+int attention_call(const void* q, const void* k, const void* v, void* out, const int64_t* positions, int64_t n_sel,
+                   int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, float scale,
+                   const int64_t strides[12], const int32_t* schedule, int64_t schedule_len,
+                   const int32_t* host_schedule, void* workspace, int64_t workspace_bytes, int64_t scratch_limit,
+                   int32_t dtype, void* stream) {
     const int esize = dtype_size(dtype);
     if (esize == 0) return KVR_E_UNSUPPORTED_DTYPE;
     if (n_sel < 0 || n_keys < 0 || n_sel > n_keys) return KVR_E_INVALID_ARGUMENT;
@@ -1325,6 +1364,14 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
     if (hs[H_MAXCHUNKS] > kMaxChunksPerGroup || hs[H_NWORK] <= 0 || hs[H_NWORK] > 65535) return KVR_E_BAD_SCHEDULE;
     const int64_t ws_need = kvr_attention_workspace_bytes(hs, schedule_len, n_q_heads, head_dim);
     if (ws_need < 0) return KVR_E_BAD_SCHEDULE;
+    if (scratch_limit > 0) {
+        if (ws_need > scratch_limit) return KVR_E_SCRATCH_LIMIT;
+        if (ws_need > 0) {
+            workspace = scratch_address(stream);
+            if (!workspace) return KVR_E_DEVICE;
+            workspace_bytes = scratch_limit;
+        }
+    }
     if (workspace_bytes < ws_need || (ws_need > 0 && !workspace)) return KVR_E_WORKSPACE_TOO_SMALL;
 
     AttnArgs a;
@@ -1398,4 +1445,28 @@ extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const v
         case KVR_DTYPE_F16: return launch_merge<f16_t>(a, hs[H_MAXCHUNKS], s);
         default: return launch_merge<bf16_t>(a, hs[H_MAXCHUNKS], s);
     }
+}
+
+}  // namespace
+
+extern "C" int kvr_packed_causal_attention(const void* q, const void* k, const void* v, void* out,
+                                           const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
+                                           int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, float scale,
+                                           const int64_t strides[12], const int32_t* schedule, int64_t schedule_len,
+                                           const int32_t* host_schedule, void* workspace, int64_t workspace_bytes,
+                                           int32_t dtype, void* stream) {
+    return attention_call(q, k, v, out, positions, n_sel, n_q_heads, n_kv_heads, n_keys, head_dim, scale, strides,
+                          schedule, schedule_len, host_schedule, workspace, workspace_bytes, 0, dtype, stream);
+}
+
+extern "C" int64_t kvr_attention_scratch_limit(void) { return kScratchBytes; }
+
+extern "C" int kvr_packed_causal_attention_noalloc(const void* q, const void* k, const void* v, void* out,
+                                                   const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
+                                                   int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, float scale,
+                                                   const int64_t strides[12], const int32_t* schedule,
+                                                   int64_t schedule_len, const int32_t* host_schedule, int32_t dtype,
+                                                   void* stream) {
+    return attention_call(q, k, v, out, positions, n_sel, n_q_heads, n_kv_heads, n_keys, head_dim, scale, strides,
+                          schedule, schedule_len, host_schedule, nullptr, 0, kScratchBytes, dtype, stream);
 }

@@ -15,6 +15,8 @@ extern "C" const char* kvr_status_string(int status) {
         case KVR_E_BAD_SCHEDULE: return "attention schedule does not match the call";
         case KVR_E_LAUNCH_FAILED: return "kernel launch failed";
         case KVR_E_CAPACITY: return "output buffer too small";
+        case KVR_E_SCRATCH_LIMIT: return "request needs more scratch than the static scratch array holds";
+        case KVR_E_DEVICE: return "device query failed (current device, stream device or symbol address)";
         default: return "unknown status";
     }
 }

@@ -125,6 +125,13 @@ def _declare(lib: ctypes.CDLL) -> None:
                                                 _i64p, _vp, ctypes.c_int64, _i32p, _vp, ctypes.c_int64,
                                                 ctypes.c_int32, _vp]
     lib.kvr_packed_causal_attention.restype = ctypes.c_int
+    lib.kvr_packed_causal_attention_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32,
+                                                        ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                                        ctypes.c_float, _i64p, _vp, ctypes.c_int64, _i32p,
+                                                        ctypes.c_int32, _vp]
+    lib.kvr_packed_causal_attention_noalloc.restype = ctypes.c_int
+    lib.kvr_attention_scratch_limit.argtypes = []
+    lib.kvr_attention_scratch_limit.restype = ctypes.c_int64
 
 
 def lib() -> ctypes.CDLL:

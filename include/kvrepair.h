@@ -58,6 +58,8 @@ enum kvr_status {
     KVR_E_BAD_SCHEDULE = -7,
     KVR_E_LAUNCH_FAILED = -8,
     KVR_E_CAPACITY = -9,
+    KVR_E_SCRATCH_LIMIT = -10,  /* request needs more than the library's static scratch array */
+    KVR_E_DEVICE = -11,         /* device query failed (current device, stream device, symbol address) */
 };
 
 /* ABI version of the loaded library (KVR_ABI_VERSION at build time). */
@@ -386,6 +388,31 @@ int kvr_packed_causal_attention(const void* q, const void* k, const void* v, voi
                                 int32_t head_dim, float scale, const int64_t strides[12], const int32_t* schedule,
                                 int64_t schedule_len, const int32_t* host_schedule, void* workspace,
                                 int64_t workspace_bytes, int32_t dtype, void* stream);
+
+/*
+ * Allocation-free variant of kvr_packed_causal_attention. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels and results as
+ * kvr_packed_causal_attention, without `workspace`: the split-K partials go to
+ * a static device array of kvr_attention_scratch_limit() bytes (64 MiB) that
+ * the library holds on every device it runs on until the process ends. A
+ * schedule whose kvr_attention_workspace_bytes exceeds that limit is refused
+ * with KVR_E_SCRATCH_LIMIT before anything is launched; use the workspace
+ * entry point for it. The call allocates and frees nothing. `stream` must
+ * belong to the current device. All calls on one device share the array
+ * (its previous contents are never read: every partial a launch reads is
+ * written by the same launch), so calls that overlap on one device --
+ * concurrent streams or threads -- race and must be serialised by the caller.
+ */
+int kvr_packed_causal_attention_noalloc(const void* q, const void* k, const void* v, void* out,
+                                        const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
+                                        int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, float scale,
+                                        const int64_t strides[12], const int32_t* schedule, int64_t schedule_len,
+                                        const int32_t* host_schedule, int32_t dtype, void* stream);
+
+/* Bytes of the static scratch array behind kvr_packed_causal_attention_noalloc. */
+int64_t kvr_attention_scratch_limit(void);
 
 #ifdef __cplusplus
 }

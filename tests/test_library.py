@@ -27,7 +27,8 @@ def test_header_declares_the_entry_points():
         "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
         "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
-        "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance"])
+        "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance", "kvr_packed_causal_attention_noalloc",
+        "kvr_attention_scratch_limit"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -239,6 +240,24 @@ def test_workspace_is_zero_when_every_tile_fits_one_chunk():
     buf = (ctypes.c_int32 * len(s))(*s)
     assert s[16] == 16
     assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 16 * 66 * 4
+
+
+def test_noalloc_attention_refuses_oversized_schedules_before_any_launch():
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    limit = int(lib.kvr_attention_scratch_limit())
+    assert limit == 64 << 20
+    positions = list(range(8192, 8192 + 4096))
+    s = schedule(positions, 12288, 32, 8, 128, chunk=64)
+    buf = (ctypes.c_int32 * len(s))(*s)
+    assert lib.kvr_attention_workspace_bytes(buf, len(s), 32, 128) > limit
+    fake = 4096  # never dereferenced: the request is refused on the host
+    strides = _native.i64_array([128, 128 * 32, 1] + [12288 * 128, 128, 1] * 2 + [128, 128 * 32, 1])
+    status = lib.kvr_packed_causal_attention_noalloc(fake, fake, fake, fake, fake, len(positions), 32, 8, 12288, 128,
+                                                     ctypes.c_float(0.125), strides, fake, len(s), buf, 2, None)
+    assert status == -10
+    assert lib.kvr_status_string(status) == b"request needs more scratch than the static scratch array holds"
 
 
 def test_decoder_layer_descriptors_validate_before_any_launch():
