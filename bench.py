@@ -1,42 +1,52 @@
 #!/usr/bin/env python3
 """Refresh-stage benchmark of the MI355X packed refresh executor (one GPU).
 
-Workload (the headline metric's config): an
-8B-shaped Llama (32 layers, hidden 4096, MLP 14336, 32 query / 8 KV heads x
+Headline workload (the metric's config, the default):
+an 8B-shaped Llama (32 layers, hidden 4096, MLP 14336, 32 query / 8 KV heads x
 128, RoPE theta 5e5, vocab 128256, random init, bf16); a synthetic 8192-token
-cache with K/V ~ N(0,1) (seed 1); a 512-token deletion at position 2048
-(shift -512, 5632-row suffix); a 64-token budget as 16 intervals of 4 rows at
-random suffix slots (seed 2).
+cache with K/V ~ N(0,1) (seed 1); a 512-token deletion at position 2048 (shift
+-512, 5632-row suffix); a 64-token budget as 16 intervals of 4 rows at random
+suffix slots (seed 2).
 
 One step = one full refresh stage, inputs resident in HBM: shift-cache build
 (prefix copy + RoPE delta rotation of every suffix K row + V copy, all layers)
--> plan upload -> packed forward through all 32 layers with, per layer, the
-libkvrepair projection GEMMs (q/k/v in one launch, o, gate/up with the SiLU
-gate, down), the RMSNorms (residual add fused), the fused fresh-row epilogue
-(RoPE of the fresh Q/K + K/V scatter, one launch) and the packed attention.
-Prefill, tokenisation and selection are outside
-the step, as in the reference benchmark (benchmark_refresh.py:3-9); unlike it,
-the rotation is inside.
+-> plan upload -> packed forward through all layers with, per layer, the
+projections, the norms, the fused fresh-row epilogue (RoPE of the fresh Q/K +
+K/V scatter) and the packed attention. Prefill, tokenisation and selection are
+outside the step, as in the reference benchmark (benchmark_refresh.py:3-9);
+unlike it, the rotation is inside.
 
-Printed (one JSON line): stage latency (ms per repair, K uninstrumented
-steps), the per-kernel HIP event timings of K more steps that dispatch the
-same kernels one by one from Python (events around every libkvrepair
-launch), a roofline object for the dominant kernel,
-the rotate-only GB/s, the same stage run the reference way on the same GPU,
-the selection scorer (kvr_query_relevance over the c3 edited ids, beside the
-reference's eager scorer on the same GPU; selection is not part of the step),
-and the reference path timed on the host CPU (cpu_baseline).
+Printed (one JSON line): stage latency (ms per repair over K steps), the same
+stage run the reference way on the same GPU, the device time of every
+libkvrepair kernel of the step (HIP events around replays of a graph of
+back-to-back launches of that kernel with the stage's own shapes: no host time
+inside), a roofline object for the dominant kernel and one per north-star
+kernel (rotate, shift-cache build, scatter, fresh-row epilogue, attention),
+the end-to-end parity checks at full depth against the reference path and an
+fp32 control, the selection scorer, and the reference path timed on the host
+CPU (cpu_baseline).
+
+Other modes (secondary lines, not the headline):
+  --workload c2|c4|c5   the same measurements on BASELINE configs 2, 4, 5 at
+                        full depth, with kernel-level CPU timings;
+  --grid                the reference benchmark's grid (lengths 2048/8192 x
+                        1/4/16 intervals, 64-token budget, refresh only:
+                        benchmark_refresh.py:35-49, 129-182), one line per case.
 """
 
 from __future__ import annotations
 
 import argparse
+import copy
 import ctypes
 import json
+import math
 import os
 import random
+import statistics
 import sys
 import time
+from dataclasses import dataclass, field
 from pathlib import Path
 from types import SimpleNamespace
 
@@ -49,40 +59,113 @@ METRIC = "refresh-stage latency (ms) per repair at 8k ctx/64-tok budget; rotate 
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
-# BASELINE config 3 geometry
-LAYERS, HIDDEN, MLP, HQ, HKV, DIM, VOCAB, THETA = 32, 4096, 14336, 32, 8, 128, 128256, 500000.0
-TOTAL, DELETE_AT, DELETE_SPAN, BUDGET_INTERVALS, ROWS_PER_INTERVAL = 8192, 2048, 512, 16, 4
+
+# ----------------------------------------------------------------------------- workloads
+@dataclass(frozen=True)
+class Workload:
+    """One BASELINE configuration: model geometry, cache, edit and support."""
+
+    name: str
+    family: str  # "llama" or "qwen3"
+    layers: int
+    hidden: int
+    mlp: int
+    hq: int
+    hkv: int
+    dim: int
+    vocab: int
+    theta: float
+    total: int         # prefilled (old) cache length
+    delete_at: int
+    delete_span: int
+    seed: int          # weights and K/V
+    description: str
+    support: tuple = field(default=())
+
+    @property
+    def edited(self) -> int:
+        return self.total - self.delete_span
+
+    @property
+    def suffix(self) -> int:
+        return self.total - self.delete_at - self.delete_span
+
+    def intervals(self) -> list[tuple[int, int]]:
+        return [tuple(iv) for iv in self.support]
+
+    def positions(self) -> list[int]:
+        return [p for s, e in self.intervals() for p in range(s, e)]
 
 
 def c3_intervals() -> list[tuple[int, int]]:
-    """16 intervals of 4 rows at random 8-token slots of the suffix (seed 2)."""
-    suffix = TOTAL - DELETE_AT - DELETE_SPAN
-    slots = sorted(random.Random(2).sample(range(suffix // 8), BUDGET_INTERVALS))
-    return [(DELETE_AT + 8 * s, DELETE_AT + 8 * s + ROWS_PER_INTERVAL) for s in slots]
+    """16 intervals of 4 rows at random 8-token slots of the c3 suffix (seed 2)."""
+    suffix = 8192 - 2048 - 512
+    slots = sorted(random.Random(2).sample(range(suffix // 8), 16))
+    return [(2048 + 8 * s, 2048 + 8 * s + 4) for s in slots]
 
 
-def make_model(device, layers=LAYERS, seed=1):
-    """Random-init 8B-shaped Llama in bf16 on ``device``.
+def c4_intervals() -> list[tuple[int, int]]:
+    """ceil(5% of 27648) = 1383 rows: 7 intervals of 44 and 25 of 43 at random
+    88-token slots of the c4 suffix (seed 3)."""
+    slots = sorted(random.Random(3).sample(range(27648 // 88), 32))
+    return [(4096 + 88 * s, 4096 + 88 * s + (44 if i < 7 else 43)) for i, s in enumerate(slots)]
+
+
+_LLAMA8B = dict(family="llama", layers=32, hidden=4096, mlp=14336, hq=32, hkv=8, dim=128, vocab=128256,
+                theta=500000.0)
+WORKLOADS = {
+    "c2": Workload("c2", total=2048, delete_at=512, delete_span=128, seed=1, support=((928, 992),),
+                   description="c2: 8B-shaped Llama, 2048-token cache, delete 128 @512, 64 rows in 1 interval",
+                   **_LLAMA8B),
+    "c3": Workload("c3", total=8192, delete_at=2048, delete_span=512, seed=1, support=tuple(c3_intervals()),
+                   description="c3: 8B-shaped Llama, 8192-token cache, delete 512 @2048, 64-token budget in 16x4",
+                   **_LLAMA8B),
+    "c4": Workload("c4", family="qwen3", layers=36, hidden=4096, mlp=12288, hq=32, hkv=8, dim=128, vocab=151936,
+                   theta=1000000.0, total=32768, delete_at=4096, delete_span=1024, seed=3,
+                   support=tuple(c4_intervals()),
+                   description="c4: Qwen3-8B-shaped, 32768-token cache, delete 1024 @4096, 5% budget (1383 rows) "
+                               "in 32 intervals"),
+    "c5": Workload("c5", total=16384, delete_at=1024, delete_span=256, seed=4, support=((1024, 16128),),
+                   description="c5: 8B-shaped Llama, 16384-token cache, delete 256 @1024, 100% budget "
+                               "(15104 rows)", **_LLAMA8B),
+}
+C3 = WORKLOADS["c3"]
+
+# headline (c3) geometry, kept as module constants for callers
+LAYERS, HIDDEN, MLP, HQ, HKV, DIM, VOCAB, THETA = C3.layers, C3.hidden, C3.mlp, C3.hq, C3.hkv, C3.dim, C3.vocab, \
+    C3.theta
+TOTAL, DELETE_AT, DELETE_SPAN, BUDGET_INTERVALS, ROWS_PER_INTERVAL = C3.total, C3.delete_at, C3.delete_span, 16, 4
+
+
+def make_model(device, workload: Workload = C3, layers: int | None = None, seed: int | None = None,
+               dtype=torch.bfloat16, vocab: int | None = None):
+    """Random-init model of the workload's shape on ``device``.
 
     Built on the meta device and materialised directly: linear and embedding
-    weights ~ N(0, 0.02) (drawn in fp32, cast to bf16), RMSNorm weights 1, RoPE
-    buffers recomputed -- the values HF's own init gives, without its slow
-    per-element bf16 sampling on the host.
+    weights ~ N(0, 0.02) (drawn in fp32, cast to ``dtype``), RMSNorm weights
+    (q/k norms included) 1, RoPE buffers recomputed -- the values HF's own init
+    gives, without its slow per-element sampling on the host.
     """
-    from transformers import LlamaConfig, LlamaForCausalLM
+    from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM
 
-    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=HIDDEN, intermediate_size=MLP, num_hidden_layers=layers,
-                      num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=DIM, rope_theta=THETA,
-                      max_position_embeddings=TOTAL)
+    w = workload
+    n_layers = w.layers if layers is None else layers
+    common = dict(vocab_size=w.vocab if vocab is None else vocab, hidden_size=w.hidden, intermediate_size=w.mlp,
+                  num_hidden_layers=n_layers, num_attention_heads=w.hq, num_key_value_heads=w.hkv, head_dim=w.dim,
+                  rope_theta=w.theta, max_position_embeddings=w.total)
+    if w.family == "qwen3":
+        cfg, ctor = Qwen3Config(layer_types=["full_attention"] * n_layers, **common), Qwen3ForCausalLM
+    else:
+        cfg, ctor = LlamaConfig(**common), LlamaForCausalLM
     previous = torch.get_default_dtype()
-    torch.set_default_dtype(torch.bfloat16)
+    torch.set_default_dtype(dtype)
     try:
         with torch.device("meta"):
-            model = LlamaForCausalLM(cfg)
+            model = ctor(cfg)
     finally:
         torch.set_default_dtype(previous)
     model = model.to_empty(device=device).eval()
-    gen = torch.Generator(device=device).manual_seed(seed)
+    gen = torch.Generator(device=device).manual_seed(w.seed if seed is None else seed)
     with torch.no_grad():
         for name, param in model.named_parameters():
             if name.endswith("norm.weight"):
@@ -101,18 +184,21 @@ def make_model(device, layers=LAYERS, seed=1):
     return model
 
 
-def make_request(device, layers=LAYERS):
-    """Synthetic stale cache (K/V ~ N(0,1), seed 1) and the c3 edit."""
+def make_request(device, workload: Workload = C3, layers: int | None = None, vocab: int | None = None):
+    """Synthetic stale cache (K/V ~ N(0,1), bf16, workload seed) and the workload's edit:
+    old ids random, the shared prefix kept exactly ``delete_at`` tokens long."""
     from kv_cache_repair_amd.cache import cache_from_tensors
 
-    gen = torch.Generator(device=device).manual_seed(1)
-    pairs = [(torch.randn(1, HKV, TOTAL, DIM, device=device, generator=gen, dtype=torch.bfloat16),
-              torch.randn(1, HKV, TOTAL, DIM, device=device, generator=gen, dtype=torch.bfloat16))
-             for _ in range(layers)]
-    old_ids = torch.randint(0, VOCAB, (1, TOTAL), device=device, generator=gen)
-    # keep the shared prefix exactly DELETE_AT tokens long
-    old_ids[0, DELETE_AT] = (old_ids[0, DELETE_AT + DELETE_SPAN] + 1) % VOCAB
-    new_ids = torch.cat((old_ids[:, :DELETE_AT], old_ids[:, DELETE_AT + DELETE_SPAN:]), dim=1)
+    w = workload
+    n_layers = w.layers if layers is None else layers
+    n_vocab = w.vocab if vocab is None else vocab
+    gen = torch.Generator(device=device).manual_seed(w.seed)
+    pairs = [(torch.randn(1, w.hkv, w.total, w.dim, device=device, generator=gen, dtype=torch.bfloat16),
+              torch.randn(1, w.hkv, w.total, w.dim, device=device, generator=gen, dtype=torch.bfloat16))
+             for _ in range(n_layers)]
+    old_ids = torch.randint(0, n_vocab, (1, w.total), device=device, generator=gen)
+    old_ids[0, w.delete_at] = (old_ids[0, w.delete_at + w.delete_span] + 1) % n_vocab
+    new_ids = torch.cat((old_ids[:, :w.delete_at], old_ids[:, w.delete_at + w.delete_span:]), dim=1)
     return cache_from_tensors(pairs), old_ids, new_ids
 
 
@@ -124,53 +210,6 @@ def hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=None):
     cache, _ = build_halo_cache(shim, old, old_ids, new_ids, 0)
     packed_refresh_owned_(shim, cache, new_ids, intervals, native_layers=native_layers)
     return cache
-
-
-class KernelTimer:
-    """Brackets every libkvrepair launch with HIP events on the launching stream."""
-
-    NAMES = ("kvr_shift_cache_build", "kvr_rope_scatter_kv", "kvr_indexed_scatter_kv",
-             "kvr_packed_causal_attention", "kvr_rope_delta_rotate", "kvr_linear_multi", "kvr_rms_norm")
-
-    def __init__(self):
-        from kv_cache_repair_amd import _native
-
-        self.lib = _native.lib()
-        self.original = {n: getattr(self.lib, n) for n in self.NAMES}
-        self.events: dict[str, list] = {n: [] for n in self.NAMES}
-        self.active = False
-
-    def install(self):
-        for name, fn in self.original.items():
-            setattr(self.lib, name, self._wrap(name, fn))
-
-    def uninstall(self):
-        for name, fn in self.original.items():
-            setattr(self.lib, name, fn)
-
-    def _wrap(self, name, fn):
-        def call(*args):
-            if not self.active:
-                return fn(*args)
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            status = fn(*args)
-            end.record()
-            self.events[name].append((start, end))
-            return status
-        return call
-
-    def reset(self):
-        self.events = {n: [] for n in self.NAMES}
-
-    def summary(self, steps):
-        out = {}
-        for name, pairs in self.events.items():
-            if pairs:
-                times = [s.elapsed_time(e) * 1000.0 for s, e in pairs]  # us
-                out[name] = {"launches_per_step": len(times) / steps, "avg_us": sum(times) / len(times),
-                             "total_us_per_step": sum(times) / steps}
-        return out
 
 
 def time_steps(fn, steps, warmup):
@@ -188,12 +227,12 @@ def time_steps(fn, steps, warmup):
 
 
 # ----------------------------------------------------------------------------- reference stage (same GPU)
-def reference_stage(model, old, old_ids, new_ids, intervals):
+def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
     """The reference's eager path on this GPU: build_halo_cache with the per-layer
     rotate chain and cats (cache.py:103-144), clone_cache, boolean mask and
-    index_copy_ + HF sdpa_attention_forward per layer (packed_cache.py:179-298)."""
-    import copy
-
+    index_copy_ + HF sdpa_attention_forward per layer (packed_cache.py:179-298).
+    With ``shifted`` (a shifted cache) only the packed refresh runs, as the
+    reference benchmark times it (benchmark_refresh.py:129-164)."""
     from transformers.cache_utils import Cache, DynamicLayer
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
@@ -208,37 +247,40 @@ def reference_stage(model, old, old_ids, new_ids, intervals):
                                           is_causal=False)
         ALL_ATTENTION_FUNCTIONS.register(name, attend)
 
-    # build_halo_cache: host alignment, prefix clone, rotate chain, cats
-    old_l = [int(x) for x in old_ids[0].tolist()]
-    new_l = [int(x) for x in new_ids[0].tolist()]
-    prefix = 0
-    while prefix < min(len(old_l), len(new_l)) and old_l[prefix] == new_l[prefix]:
-        prefix += 1
-    suffix = 0
-    while suffix < min(len(old_l), len(new_l)) - prefix and old_l[-1 - suffix] == new_l[-1 - suffix]:
-        suffix += 1
-    shift = (len(new_l) - suffix) - (len(old_l) - suffix)
-    ots = len(old_l) - suffix
-    shifted = []
-    for layer in old.layers:
-        k, v = layer.keys, layer.values
-        pk, pv = k[:, :, :prefix].clone(), v[:, :, :prefix].clone()
-        tail = k[:, :, ots:]
-        pos = torch.full((1, tail.shape[2]), shift, dtype=torch.long, device=tail.device)
-        cos, sin = base.rotary_emb(tail, pos)
-        cos, sin = cos.unsqueeze(1).to(tail.dtype), sin.unsqueeze(1).to(tail.dtype)
-        half = tail.shape[-1] // 2
-        rot = torch.cat((-tail[..., half:], tail[..., :half]), dim=-1)
-        nk = torch.cat((pk, tail * cos + rot * sin), dim=2)
-        nv = torch.cat((pv, v[:, :, ots:].clone()), dim=2)
-        shifted.append((torch.cat((torch.empty_like(nk[:, :, :0]), nk), dim=2),
-                        torch.cat((torch.empty_like(nv[:, :, :0]), nv), dim=2)))  # DynamicLayer.update cat
+    if shifted is None:
+        # build_halo_cache: host alignment, prefix clone, rotate chain, cats
+        old_l = [int(x) for x in old_ids[0].tolist()]
+        new_l = [int(x) for x in new_ids[0].tolist()]
+        prefix = 0
+        while prefix < min(len(old_l), len(new_l)) and old_l[prefix] == new_l[prefix]:
+            prefix += 1
+        suffix = 0
+        while suffix < min(len(old_l), len(new_l)) - prefix and old_l[-1 - suffix] == new_l[-1 - suffix]:
+            suffix += 1
+        shift = (len(new_l) - suffix) - (len(old_l) - suffix)
+        ots = len(old_l) - suffix
+        pairs = []
+        for layer in old.layers:
+            k, v = layer.keys, layer.values
+            pk, pv = k[:, :, :prefix].clone(), v[:, :, :prefix].clone()
+            tail = k[:, :, ots:]
+            pos = torch.full((1, tail.shape[2]), shift, dtype=torch.long, device=tail.device)
+            cos, sin = base.rotary_emb(tail, pos)
+            cos, sin = cos.unsqueeze(1).to(tail.dtype), sin.unsqueeze(1).to(tail.dtype)
+            half = tail.shape[-1] // 2
+            rot = torch.cat((-tail[..., half:], tail[..., :half]), dim=-1)
+            nk = torch.cat((pk, tail * cos + rot * sin), dim=2)
+            nv = torch.cat((pv, v[:, :, ots:].clone()), dim=2)
+            pairs.append((torch.cat((torch.empty_like(nk[:, :, :0]), nk), dim=2),
+                          torch.cat((torch.empty_like(nv[:, :, :0]), nv), dim=2)))  # DynamicLayer.update cat
+    else:
+        pairs = [(layer.keys, layer.values) for layer in shifted.layers]
     # packed_interval_repair (sdpa + torch writeback)
     selected = [p for s, e in intervals for p in range(s, e)]
     positions = torch.tensor(selected, dtype=torch.long, device=new_ids.device)
     length = new_ids.shape[1]
     mask = (torch.arange(length, device=new_ids.device)[None, :] <= positions[:, None])[None, None]
-    output = cache_from_tensors([(k.clone(), v.clone()) for k, v in shifted])
+    output = cache_from_tensors([(k.clone(), v.clone()) for k, v in pairs])
 
     class _Layer(DynamicLayer):
         def __init__(self, k, v):
@@ -275,11 +317,263 @@ def reference_stage(model, old, old_ids, new_ids, intervals):
     return output
 
 
-# ----------------------------------------------------------------------------- HBM traffic (rocprofv3 PMC)
-TRAFFIC_SUMMARIES = (ROOT / "profiles" / "attention_c3_hbm_traffic.md",
-                     ROOT / "profiles" / "projection_gemm_c3_hbm_traffic.md")
+# ----------------------------------------------------------------------------- end-to-end parity at full depth
+def row_errors(a: torch.Tensor, b: torch.Tensor) -> dict:
+    """max-abs, RMSE and the smallest per-row cosine of a against b (rows = head_dim vectors)."""
+    a, b = a.double(), b.double()
+    d = a - b
+    cos = torch.nn.functional.cosine_similarity(a.reshape(-1, a.shape[-1]), b.reshape(-1, b.shape[-1]), dim=-1)
+    return {"max_abs": d.abs().max().item(), "rmse": d.square().mean().sqrt().item(), "min_cos": cos.min().item()}
+
+
+def depth_parity(ours, theirs, control, positions) -> dict:
+    """Per layer and per K/V: the refreshed rows of our cache and of the
+    reference path's cache against an fp32 control (the reference's own gate,
+    tests/test_packed_cache.py:291-315: ours <= 2 x the reference's error on
+    max-abs and RMSE, fp32-eps floor) and against each other; the other rows
+    must be bit-identical to the reference's."""
+    device = ours.layers[0].keys.device
+    n = ours.layers[0].keys.shape[2]
+    keep = torch.ones(n, dtype=torch.bool, device=device)
+    keep[positions] = False
+    index = torch.tensor(positions, dtype=torch.long, device=device)
+    rows, bit_exact = [], True
+    for i, (o, t, c) in enumerate(zip(ours.layers, theirs.layers, control.layers)):
+        for part, a, b, f in (("k", o.keys, t.keys, c.keys), ("v", o.values, t.values, c.values)):
+            bit_exact &= bool(torch.equal(a[:, :, keep].view(torch.int16), b[:, :, keep].view(torch.int16)))
+            sa, sb, sf = a.index_select(2, index), b.index_select(2, index), f.index_select(2, index)
+            floor = torch.finfo(torch.float32).eps * max(1.0, sf.abs().max().item())
+            ours_f, ref_f, ours_ref = row_errors(sa, sf), row_errors(sb, sf), row_errors(sa, sb)
+            gate = all(ours_f[m] <= 2.0 * max(ref_f[m], floor) for m in ("max_abs", "rmse"))
+            rows.append({"layer": i, "part": part, "ours_vs_fp32": ours_f, "reference_vs_fp32": ref_f,
+                         "ours_vs_reference": ours_ref, "gate": gate})
+    worst = lambda key, m, f: f(r[key][m] for r in rows)  # noqa: E731
+    return {
+        "unselected_rows_bit_exact_vs_reference": bit_exact,
+        "precision_floor_gate_all_layers": all(r["gate"] for r in rows),
+        "ours_vs_fp32": {"max_abs": worst("ours_vs_fp32", "max_abs", max), "rmse": worst("ours_vs_fp32", "rmse", max),
+                         "min_cos": worst("ours_vs_fp32", "min_cos", min)},
+        "reference_vs_fp32": {"max_abs": worst("reference_vs_fp32", "max_abs", max),
+                              "rmse": worst("reference_vs_fp32", "rmse", max),
+                              "min_cos": worst("reference_vs_fp32", "min_cos", min)},
+        "ours_vs_reference": {"max_abs": worst("ours_vs_reference", "max_abs", max),
+                              "min_cos": worst("ours_vs_reference", "min_cos", min)},
+        "max_error_ratio_vs_reference": max(
+            r["ours_vs_fp32"][m] / max(r["reference_vs_fp32"][m], 1e-30) for r in rows for m in ("max_abs", "rmse")),
+        "layers": rows,
+    }
+
+
+def fp32_control(model, old):
+    """The same model and stale cache in fp32 (bf16 values upcast exactly)."""
+    from kv_cache_repair_amd.cache import cache_from_tensors
+
+    control_model = copy.deepcopy(model).float()
+    control_old = cache_from_tensors([(l.keys.float(), l.values.float()) for l in old.layers])
+    return control_model, control_old
+
+
+def parity_checks(model, shim, old, old_ids, new_ids, intervals, with_control=True) -> dict:
+    positions = [p for s, e in intervals for p in range(s, e)]
+    ours = hip_stage(shim, old, old_ids, new_ids, intervals)
+    theirs = reference_stage(model, old, old_ids, new_ids, intervals)
+    if with_control:
+        control_model, control_old = fp32_control(model, old)
+        control = reference_stage(control_model, control_old, old_ids, new_ids, intervals)
+        del control_model, control_old
+    else:
+        control = theirs
+    result = depth_parity(ours, theirs, control, positions)
+    if not with_control:
+        result.pop("precision_floor_gate_all_layers")
+    result["layers"] = [{"layer": r["layer"], "part": r["part"], "gate": r["gate"],
+                         "ours_vs_fp32_max_abs": r["ours_vs_fp32"]["max_abs"],
+                         "reference_vs_fp32_max_abs": r["reference_vs_fp32"]["max_abs"]}
+                        for r in result["layers"]] if with_control else []
+    del ours, theirs, control
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return result
+
+
+# ----------------------------------------------------------------------------- kernel device timings
+def graph_device_us(launch, per_graph: int = 20, replays: int = 5) -> float:
+    """Device time of one ``launch`` (a raw libkvrepair call with bound
+    arguments): ``per_graph`` back-to-back launches are captured in a graph, which
+    is replayed ``replays`` times between two HIP events on the current stream,
+    so no host time lies inside the measurement."""
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            launch()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / (replays * per_graph)
+    del graph
+    return us
+
+
+def _checked(fn, *args):
+    """A launch of ``fn(*args, stream)`` on the stream current at call time (a
+    graph capture swaps it), raising on a nonzero status."""
+    from kv_cache_repair_amd import _native
+
+    def launch():
+        status = fn(*args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if status != 0:
+            raise RuntimeError(f"{fn.__name__} returned {status}: {_native.lib().kvr_status_string(status)}")
+    return launch
+
+
+def kernel_launchers(model, workload: Workload, old, old_ids, new_ids, device):
+    """Raw libkvrepair calls with the stage's own shapes and layouts, arguments
+    bound once: (launch, algorithmic bytes, flops or 0, launches per step)."""
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.cache import build_halo_cache
+    from kv_cache_repair_amd.kernels.indexed_attention import IndexedPlan
+
+    w = workload
+    lib = _native.lib()
+    esz = 2
+    code = _native.DTYPE_CODES[torch.bfloat16]
+    positions = w.positions()
+    b, n = len(positions), w.edited
+    shim_model = SimpleNamespace(generator=model)
+    shifted, _ = build_halo_cache(shim_model, old, old_ids, new_ids, 0)
+    inv = model.model.rotary_emb.inv_freq.to(device=device, dtype=torch.float32).contiguous()
+    out = {}
+
+    # shift-cache build: prefix copy + rotated K tail + V tail, every layer, one launch
+    olds_k = [l.keys for l in old.layers]
+    olds_v = [l.values for l in old.layers]
+    news_k = [l.keys for l in shifted.layers]
+    news_v = [l.values for l in shifted.layers]
+    s3o, s3n = _native.i64_array(_native.strides3(olds_k[0])), _native.i64_array(_native.strides3(news_k[0]))
+    args = (_native.ptr_array(olds_k), _native.ptr_array(olds_v), _native.ptr_array(news_k),
+            _native.ptr_array(news_v), len(olds_k), w.hkv, w.dim, w.dim, s3o, s3n, w.delete_at,
+            w.delete_at + w.delete_span, w.delete_at, w.suffix, -w.delete_span, inv.data_ptr(), 1.0, code)
+    out["kvr_shift_cache_build"] = (_checked(lib.kvr_shift_cache_build, *args),
+                                    2 * 2 * w.layers * w.hkv * (w.delete_at + w.suffix) * w.dim * esz, 0, 1)
+
+    # rotate only: the suffix K rows of every layer (BASELINE "rotate GB/s")
+    keys = [k[:, :, w.delete_at + w.delete_span:] for k in olds_k]
+    outs = [k[:, :, w.delete_at:] for k in news_k]
+    args = (_native.ptr_array(keys), _native.ptr_array(outs), len(keys), w.hkv, w.suffix, w.dim, w.dim,
+            _native.i64_array(_native.strides3(keys[0])), _native.i64_array(_native.strides3(outs[0])),
+            -w.delete_span, inv.data_ptr(), 1.0, code)
+    out["kvr_rope_delta_rotate"] = (_checked(lib.kvr_rope_delta_rotate, *args),
+                                    2 * w.layers * w.hkv * w.suffix * w.dim * esz, 0, 0)
+
+    # per-layer operators on layer 0 of the shifted cache, the stage's layouts:
+    # fresh q/k/v as token-major transposed views, attention output [1, B, Hq, D]
+    plan = IndexedPlan(positions, n).to(device)
+    pos_ptr = plan.positions.data_ptr()
+    cache_k, cache_v = news_k[0], news_v[0]
+    gen = torch.Generator(device=device).manual_seed(5)
+    qkv = torch.randn(1, b, (w.hq + 2 * w.hkv) * w.dim, device=device, generator=gen, dtype=torch.bfloat16)
+    q = qkv[..., :w.hq * w.dim].view(1, b, w.hq, w.dim).transpose(1, 2)
+    fk = qkv[..., w.hq * w.dim:(w.hq + w.hkv) * w.dim].view(1, b, w.hkv, w.dim).transpose(1, 2)
+    fv = qkv[..., (w.hq + w.hkv) * w.dim:].view(1, b, w.hkv, w.dim).transpose(1, 2)
+    q_out = torch.empty(1, b, w.hq, w.dim, device=device, dtype=torch.bfloat16).transpose(1, 2)
+    cos, sin = model.model.rotary_emb(qkv, plan.positions.unsqueeze(0))
+    cos, sin = cos.contiguous(), sin.contiguous()
+    st18 = _native.i64_array(sum((_native.strides3(t) for t in (q, q_out, fk, fv, cache_k, cache_v)), []))
+    cs = _native.i64_array([int(cos.stride(-2)), int(cos.stride(-1)), int(sin.stride(-2)), int(sin.stride(-1))])
+    args = (q.data_ptr(), q_out.data_ptr(), fk.data_ptr(), fv.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), pos_ptr, b, w.hq, w.hkv, n, w.dim, st18, cs, code)
+    out["kvr_rope_scatter_kv"] = (_checked(lib.kvr_rope_scatter_kv, *args),
+                                  (2 * (w.hq + 2 * w.hkv) + 2) * b * w.dim * esz, 0, w.layers)
+
+    st12 = _native.i64_array(sum((_native.strides3(t) for t in (cache_k, cache_v, fk, fv)), []))
+    args = (cache_k.data_ptr(), cache_v.data_ptr(), fk.data_ptr(), fv.data_ptr(), pos_ptr, b, w.hkv, n, w.dim, st12,
+            code)
+    out["kvr_indexed_scatter_kv"] = (_checked(lib.kvr_indexed_scatter_kv, *args),
+                                     2 * 2 * w.hkv * b * w.dim * esz, 0, 0)
+
+    host, dev = plan.attention_schedule(w.hq, w.hkv, w.dim, torch.bfloat16)
+    ws_bytes = int(lib.kvr_attention_workspace_bytes(host, len(host), w.hq, w.dim))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    attn_out = torch.empty(1, b, w.hq, w.dim, device=device, dtype=torch.bfloat16).permute(0, 2, 1, 3)
+    st_attn = _native.i64_array(sum((_native.strides3(t) for t in (q, cache_k, cache_v, attn_out)), []))
+    args = (q.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), attn_out.data_ptr(), pos_ptr, b, w.hq, w.hkv, n,
+            w.dim, ctypes.c_float(w.dim ** -0.5), st_attn, dev.data_ptr(), len(host), host, ws.data_ptr(), ws_bytes,
+            code)
+    max_pos = max(positions)
+    attn_bytes = (2 * b * w.hq * w.dim + 2 * w.hkv * (max_pos + 1) * w.dim) * esz
+    attn_flops = 4 * w.hq * w.dim * sum(p + 1 for p in positions)
+    out["kvr_packed_causal_attention"] = (_checked(lib.kvr_packed_causal_attention, *args), attn_bytes, attn_flops,
+                                          w.layers)
+
+    # projections of one layer (<= 64 rows: the stage runs them on kvr_linear_multi)
+    if b <= 64:
+        from kv_cache_repair_amd.kernels import projection as proj
+
+        layer = model.model.layers[0]
+        a, m = layer.self_attn, layer.mlp
+        x = torch.randn(b, w.hidden, device=device, generator=gen, dtype=torch.bfloat16)
+        xi = torch.randn(b, w.mlp, device=device, generator=gen, dtype=torch.bfloat16)
+        xo = torch.randn(b, w.hq * w.dim, device=device, generator=gen, dtype=torch.bfloat16)
+        calls, total_bytes = [], 0
+        for weights, epi, xin, residual in (
+                ([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], proj.CONCAT, x, False),
+                ([a.o_proj.weight], proj.CONCAT, xo, True),
+                ([m.gate_proj.weight, m.up_proj.weight], proj.SILU_GATE, x, False),
+                ([m.down_proj.weight], proj.CONCAT, xi, True)):
+            pl = proj.ProjectionPlan(weights, epi)
+            need = pl.workspace_bytes(b)
+            wsp = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+            y = torch.empty(b, pl.n_out, device=device, dtype=torch.bfloat16)
+            res = torch.randn(b, pl.n_out, device=device, generator=gen, dtype=torch.bfloat16) if residual else None
+            calls.append((_checked(lib.kvr_linear_multi, xin.data_ptr(), pl._count, pl._w, pl._rows, pl._ldw,
+                                   y.data_ptr(), b, pl.k, xin.stride(0), pl.n_out,
+                                   proj.RESIDUAL if residual else epi, res.data_ptr() if residual else None,
+                                   pl.n_out if residual else 0, wsp.data_ptr(), need, code),
+                          (xin, y, wsp, res)))
+            total_bytes += esz * (pl.rows * pl.k + b * pl.k + b * pl.n_out * (2 if residual else 1))
+        keep = [c[1] for c in calls]
+
+        def launch_all():
+            for c, _ in calls:
+                c()
+        launch_all.keep = keep  # the bound tensors live as long as the launcher
+        # one "launch" = the four projections of a layer; bytes/flops averaged per kvr_linear_multi call
+        out["kvr_linear_multi"] = (launch_all, total_bytes, 0, 4 * w.layers, 4)
+    launch_keep = (shifted, plan, qkv, q_out, cos, sin, ws, attn_out, host, dev)
+    return out, launch_keep
+
+
+def measure_kernels(model, workload, old, old_ids, new_ids, device) -> dict:
+    launchers, keep = kernel_launchers(model, workload, old, old_ids, new_ids, device)
+    kernels = {}
+    for name, entry in launchers.items():
+        launch, nbytes, flops, per_step = entry[:4]
+        calls = entry[4] if len(entry) > 4 else 1
+        us = graph_device_us(launch) / calls
+        rec = {"avg_us": us, "algorithmic_bytes": nbytes / calls, "achieved_GBps": nbytes / calls / (us * 1e3),
+               "frac_of_hbm_peak": nbytes / calls / (us * 1e3) / HBM_PEAK_GBPS, "launches_per_step": per_step,
+               "total_us_per_step": us * per_step}
+        if flops:
+            rec["achieved_TFLOPs"] = flops / (us * 1e6)
+            rec["frac_of_bf16_mfma_peak"] = flops / (us * 1e6) / MFMA_BF16_PEAK_TFLOPS
+        kernels[name] = rec
+    del keep
+    torch.cuda.synchronize()
+    return kernels
+
+
+TRAFFIC_SUMMARIES = tuple(sorted((ROOT / "profiles").glob("*hbm_traffic*.md")))
 KERNEL_SOURCES = {"kvr_packed_causal_attention": "kvr_attention.hip", "kvr_shift_cache_build": "kvr_rotate.hip",
-                  "kvr_indexed_scatter_kv": "kvr_scatter.hip", "kvr_linear_multi": "kvr_gemm.hip"}
+                  "kvr_rope_delta_rotate": "kvr_rotate.hip", "kvr_indexed_scatter_kv": "kvr_scatter.hip",
+                  "kvr_rope_scatter_kv": "kvr_fresh.hip", "kvr_linear_multi": "kvr_gemm.hip"}
 
 
 def source_digest(name: str) -> str:
@@ -289,22 +583,45 @@ def source_digest(name: str) -> str:
     return hashlib.sha256(path.read_bytes()).hexdigest()[:16]
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` from a committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counts), or None when no
-    summary covers it or it was measured on another version of the kernel source."""
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of ``kernel`` on ``workload`` from a committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's
+    counts), or None when no summary covers it or it was measured on another
+    version of the kernel source."""
     if kernel not in KERNEL_SOURCES:
         return None
     for summary in TRAFFIC_SUMMARIES:
-        if not summary.exists():
-            continue
         for line in summary.read_text().splitlines():
             if not line.startswith("traffic:"):
                 continue
             fields = dict(item.partition("=")[::2] for item in line[len("traffic:"):].split())
-            if fields.get("kernel") == kernel and fields.get("source_sha256") == source_digest(KERNEL_SOURCES[kernel]):
+            if (fields.get("kernel") == kernel and fields.get("workload", "c3") == workload
+                    and fields.get("source_sha256") == source_digest(KERNEL_SOURCES[kernel])):
                 return int(fields["bytes_per_launch"])
     return None
+
+
+def rooflines(kernels: dict, workload: str) -> tuple[dict, dict]:
+    """(roofline of the dominant kernel of the step, rooflines of the north-star kernels)."""
+    def entry(name, bound="hbm"):
+        k = kernels[name]
+        if bound == "mfma":
+            achieved, peak, unit = k["achieved_TFLOPs"], MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            achieved, peak, unit = k["achieved_GBps"], HBM_PEAK_GBPS, "GB/s"
+        return {"kernel": name, "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                "frac": achieved / peak, "traffic": measured_traffic(name, workload), "avg_launch_us": k["avg_us"],
+                "algorithmic_bytes_per_launch": k["algorithmic_bytes"]}
+
+    stepping = {n: k for n, k in kernels.items() if k["launches_per_step"]}
+    dominant = max(stepping, key=lambda n: stepping[n]["total_us_per_step"])
+    attention_bound = "mfma" if workload in ("c4", "c5") else "hbm"
+    north = {"rotate": entry("kvr_rope_delta_rotate"), "shift_cache_build": entry("kvr_shift_cache_build"),
+             "scatter": entry("kvr_indexed_scatter_kv"), "fresh_row_epilogue": entry("kvr_rope_scatter_kv"),
+             "attention": entry("kvr_packed_causal_attention", attention_bound)}
+    north["attention"]["achieved_TFLOPs"] = kernels["kvr_packed_causal_attention"]["achieved_TFLOPs"]
+    north["attention"]["achieved_GBps"] = kernels["kvr_packed_causal_attention"]["achieved_GBps"]
+    return entry(dominant), north
 
 
 # ----------------------------------------------------------------------------- selection scoring
@@ -326,11 +643,11 @@ def reference_scores(embedding, ids, query):
 
 
 def scoring_measurement(model, new_ids, device, launches=50, calls=10) -> dict:
-    """Dense query relevance over the c3 edited ids (7680 tokens) with the bench
-    model's embedding table and a 12-token query (half of it taken from the
-    prompt, so exact-id boosts occur): the kvr_query_relevance launch alone
-    (HIP events on the launching stream), the Python API end to end (list of
-    scores on the host), and the reference's eager scorer on the same GPU."""
+    """Dense query relevance over the edited ids with the bench model's
+    embedding table and a 12-token query (half of it taken from the prompt, so
+    exact-id boosts occur): the kvr_query_relevance launch alone (HIP events on
+    the launching stream), the Python API end to end (list of scores on the
+    host), and the reference's eager scorer on the same GPU."""
     from kv_cache_repair_amd import _native
     from kv_cache_repair_amd.scoring import dense_query_relevance_scores
 
@@ -338,7 +655,8 @@ def scoring_measurement(model, new_ids, device, launches=50, calls=10) -> dict:
     holder = SimpleNamespace(generator=model)  # the reference's scorer reads model.generator
     ids = new_ids[0]
     rng = random.Random(3)
-    query = [int(ids[rng.randrange(ids.shape[0])]) for _ in range(6)] + [rng.randrange(VOCAB) for _ in range(6)]
+    vocab = int(embedding.weight.shape[0])
+    query = [int(ids[rng.randrange(ids.shape[0])]) for _ in range(6)] + [rng.randrange(vocab) for _ in range(6)]
     ours = lambda: dense_query_relevance_scores(model=holder, edited_input_ids=new_ids,  # noqa: E731
                                                 query_token_ids=query)
     theirs = lambda: reference_scores(embedding, ids, query)  # noqa: E731
@@ -347,31 +665,16 @@ def scoring_measurement(model, new_ids, device, launches=50, calls=10) -> dict:
     max_abs = max(abs(a - b) for a, b in zip(got, want))
 
     table = embedding.weight
-    lib, stream = _native.lib(), _native.stream_handle(device)
+    lib = _native.lib()
     qd = torch.tensor(query, dtype=torch.long, device=device)
     out = torch.empty(ids.shape[0], dtype=torch.float32, device=device)
-
-    def launch():
-        status = lib.kvr_query_relevance(table.data_ptr(), table.shape[0], table.stride(0), table.shape[1],
-                                         ids.data_ptr(), 0, ids.shape[0], qd.data_ptr(), len(query),
-                                         ctypes.c_float(0.25), out.data_ptr(), _native.DTYPE_CODES[table.dtype],
-                                         stream)
-        if status != 0:
-            raise RuntimeError(f"kvr_query_relevance returned {status}")
-
-    for _ in range(3):
-        launch()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(launches):
-        launch()
-    end.record()
-    torch.cuda.synchronize()
-    kernel_us = start.elapsed_time(end) * 1000.0 / launches
+    launch = _checked(lib.kvr_query_relevance, table.data_ptr(), table.shape[0], table.stride(0), table.shape[1],
+                      ids.data_ptr(), 0, ids.shape[0], qd.data_ptr(), len(query), ctypes.c_float(0.25),
+                      out.data_ptr(), _native.DTYPE_CODES[table.dtype])
+    kernel_us = graph_device_us(launch)
     n, hidden = ids.shape[0], table.shape[1]
     algorithmic = 2 * hidden * (n + len(query)) + 8 * n + 4 * n  # gathered rows, query rows, ids, scores
-    return {"workload": f"c3 edited ids ({n} tokens), embedding {tuple(table.shape)} bf16, {len(query)}-token query",
+    return {"workload": f"edited ids ({n} tokens), embedding {tuple(table.shape)} bf16, {len(query)}-token query",
             "kernel_avg_us": kernel_us, "algorithmic_bytes": algorithmic,
             "achieved_GBps": algorithmic / (kernel_us * 1e3),
             "frac_of_peak": algorithmic / (kernel_us * 1e3) / HBM_PEAK_GBPS,
@@ -379,55 +682,279 @@ def scoring_measurement(model, new_ids, device, launches=50, calls=10) -> dict:
             "max_abs_vs_reference": max_abs}
 
 
-# ----------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(layers_sample: int, repeats: int = 10) -> dict:
+# ----------------------------------------------------------------------------- CPU baselines
+def _cpu_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(workload: Workload, layers_sample: int, repeats: int = 10) -> dict:
     """The oracle's torch restatement of the reference stage (rotate chain +
-    packed SDPA forward), timed on this host's CPU cores over the first
-    ``layers_sample`` layers of the c3 workload (median of ``repeats`` runs)
-    and scaled to 32 layers."""
+    packed SDPA forward), timed on every host core over the first
+    ``layers_sample`` layers of the workload (median of ``repeats`` runs after
+    one warm-up) and scaled to all layers."""
     from oracle import reference_path as ref
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = max(1, os.cpu_count() or 1)
     previous = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        model = make_model("cpu", layers=layers_sample, seed=1)
-        old, old_ids, new_ids = make_request("cpu", layers=layers_sample)
-        intervals = c3_intervals()
+        model = make_model("cpu", workload, layers=layers_sample)
+        old, old_ids, new_ids = make_request("cpu", workload, layers=layers_sample)
+        intervals = workload.intervals()
         ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)  # warm-up (allocator, kernels)
         samples = []
         for _ in range(repeats):
             t0 = time.perf_counter()
             ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)
             samples.append((time.perf_counter() - t0) * 1000.0)
-        per_sample_ms = sorted(samples)[len(samples) // 2]
+        per_sample_ms = statistics.median(samples)
     finally:
         torch.set_num_threads(previous)
-    cpu_name = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_name = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": per_sample_ms * LAYERS / layers_sample, "unit": "ms", "cores": threads, "kind": "port",
+    scale = workload.layers / layers_sample
+    return {"value": per_sample_ms * scale, "unit": "ms", "cores": threads, "kind": "port",
             "sample": f"oracle torch restatement of the reference stage (eager rotate chain, clone, boolean mask, "
-                      f"index_copy_, HF sdpa) on the first {layers_sample} of 32 layers of the c3 workload, bf16, "
-                      f"median of {repeats} runs after one warm-up, scaled x{LAYERS / layers_sample:g} to "
-                      f"32 layers",
-            "cpu": cpu_name}
+                      f"index_copy_, HF sdpa) on the first {layers_sample} of {workload.layers} layers of the "
+                      f"{workload.name} workload, bf16, median of {repeats} runs after one warm-up, scaled "
+                      f"x{scale:g} to {workload.layers} layers; torch threads = os.cpu_count()",
+            "cpu": _cpu_name(), "os_cpu_count": os.cpu_count()}
+
+
+def cpu_kernel_baseline(workload: Workload, repeats: int = 2) -> dict:
+    """The three north-star steps the reference way (eager rotate chain,
+    index_copy_ pair, repeat_kv + masked SDPA) on every host core, for one layer
+    of the workload (attention over ``heads`` query heads of one KV group where
+    a full layer would take minutes), scaled to the whole step: bounded
+    samples for configs whose full CPU stage is impractical."""
+    from oracle import reference_path as ref
+
+    w = workload
+    threads = max(1, os.cpu_count() or 1)
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(w.seed)
+    try:
+        inv = 1.0 / (w.theta ** (torch.arange(0, w.dim, 2, dtype=torch.float32) / w.dim))
+        tail = torch.randn(1, w.hkv, w.suffix, w.dim, generator=gen).to(torch.bfloat16)
+        shift = -w.delete_span
+
+        def rotate():
+            freqs = inv[None, :] * float(shift)
+            emb = torch.cat((freqs, freqs), dim=-1)
+            cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+            return tail * cos + ref.rotate_half(tail) * sin
+
+        positions = torch.tensor(w.positions(), dtype=torch.long)
+        b = positions.numel()
+        cache_k = torch.randn(1, w.hkv, w.edited, w.dim, generator=gen).to(torch.bfloat16)
+        cache_v = torch.randn(1, w.hkv, w.edited, w.dim, generator=gen).to(torch.bfloat16)
+        fresh = torch.randn(1, w.hkv, b, w.dim, generator=gen).to(torch.bfloat16)
+
+        def scatter():
+            cache_k.index_copy_(2, positions, fresh)
+            cache_v.index_copy_(2, positions, fresh)
+
+        group = w.hq // w.hkv
+        heads = group if b * w.edited > 64 * 8192 else w.hq  # one KV group for the large configs
+        q = torch.randn(1, heads, b, w.dim, generator=gen).to(torch.bfloat16)
+        kv_heads = heads // group
+        mask = (torch.arange(w.edited)[None, :] <= positions[:, None])[None, None]
+
+        def attention():
+            k = cache_k[:, :kv_heads].repeat_interleave(group, dim=1)
+            v = cache_v[:, :kv_heads].repeat_interleave(group, dim=1)
+            return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+
+        def timed(fn):
+            fn()
+            samples = []
+            for _ in range(repeats):
+                t0 = time.perf_counter()
+                fn()
+                samples.append((time.perf_counter() - t0) * 1000.0)
+            return statistics.median(samples)
+
+        rot_ms, sc_ms, at_ms = timed(rotate), timed(scatter), timed(attention)
+    finally:
+        torch.set_num_threads(previous)
+    return {"cores": threads, "cpu": _cpu_name(), "kind": "port", "repeats": repeats,
+            "rotate_ms_per_step": rot_ms * w.layers, "scatter_ms_per_step": sc_ms * w.layers,
+            "attention_ms_per_step": at_ms * w.layers * (w.hq / heads),
+            "sample": f"one layer of {w.name} per op on the host CPU (bf16, eager torch as the reference runs it: "
+                      f"rotate chain over {w.hkv}x{w.suffix} rows, index_copy_ K/V of {b} rows, repeat_kv + "
+                      f"masked SDPA over {heads} of {w.hq} query heads), median of {repeats} after a warm-up, "
+                      f"scaled to {w.layers} layers and {w.hq} heads"}
+
+
+# ----------------------------------------------------------------------------- reference benchmark grid
+def selected_intervals(length: int, budget: int, count: int) -> list[tuple[int, int]]:
+    """The reference benchmark's support geometry (benchmark_refresh.py:35-49):
+    ``count`` intervals of budget/count rows placed symmetrically about the
+    context middle, so the causal pair count is the same for every count."""
+    if length <= 0 or budget <= 0 or count <= 0 or budget % count:
+        raise ValueError("length and budget must be positive; budget must be divisible by interval count")
+    width = budget // count
+    if count == 1:
+        starts = [(length - width) // 2]
+    else:
+        starts = [round(length / 4 + i * length / (2 * (count - 1)) - width / 2) for i in range(count)]
+    intervals = [(s, s + width) for s in starts]
+    if intervals[0][0] < 0 or intervals[-1][1] > length:
+        raise ValueError("selected support does not fit the sequence")
+    if any(a[1] >= b[0] for a, b in zip(intervals, intervals[1:])):
+        raise ValueError("intervals must be separated; increase length or reduce budget/count")
+    return intervals
+
+
+def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats: int, seed: int) -> dict:
+    """One case of the reference grid: a stale cache of ``length + 8`` tokens (K/V
+    ~ N(0,1)) loses 8 tokens at length // 8 and is shifted (untimed); then the
+    packed refresh alone (ownership copy, plan upload, layer-major forward) is
+    timed for this build and for the reference path, interleaved in shuffled
+    order (benchmark_refresh.py:52-61, 106-126)."""
+    from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache, cache_from_tensors
+    from kv_cache_repair_amd.kernels.packed_cache import packed_interval_repair
+
+    device = model.device
+    w = WORKLOADS["c3"]
+    gen = torch.Generator(device=device).manual_seed(seed)
+    old = cache_from_tensors([(torch.randn(1, w.hkv, length + 8, w.dim, device=device, generator=gen,
+                                           dtype=torch.bfloat16),
+                               torch.randn(1, w.hkv, length + 8, w.dim, device=device, generator=gen,
+                                           dtype=torch.bfloat16)) for _ in range(w.layers)])
+    old_ids = torch.randint(4, w.vocab, (1, length + 8), device=device, generator=gen)
+    at = length // 8
+    old_ids[0, at] = (old_ids[0, at + 8] + 1) % w.vocab
+    ids = torch.cat((old_ids[:, :at], old_ids[:, at + 8:]), dim=1)
+    shim = OperatorShim(model)
+    shifted, alignment = build_halo_cache(shim, old, old_ids, ids, 0)
+    intervals = selected_intervals(length, budget, count)
+    positions = [p for s, e in intervals for p in range(s, e)]
+    calls = {"hip": lambda: packed_interval_repair(shim, shifted, ids, intervals)[0],
+             "reference_packed_sdpa": lambda: reference_stage(model, None, None, ids, intervals, shifted=shifted)}
+    outputs = {name: fn() for name, fn in calls.items()}
+    index = torch.tensor(positions, device=device)
+    max_abs = max((a.index_select(2, index).float() - b.index_select(2, index).float()).abs().max().item()
+                  for la, lb in zip(outputs["hip"].layers, outputs["reference_packed_sdpa"].layers)
+                  for a, b in ((la.keys, lb.keys), (la.values, lb.values)))
+    del outputs
+    names = list(calls)
+    for _ in range(warmups):
+        for name in names:
+            calls[name]()
+            torch.cuda.synchronize()
+    samples = {name: [] for name in names}
+    rng = random.Random(seed)
+    for _ in range(repeats):
+        order = names.copy()
+        rng.shuffle(order)
+        for name in order:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = calls[name]()
+            torch.cuda.synchronize()
+            samples[name].append((time.perf_counter() - t0) * 1000.0)
+            del out
+
+    def summary(values):
+        ordered = sorted(values)
+        return {"median_ms": statistics.median(values), "mean_ms": statistics.mean(values),
+                "p95_ms": ordered[math.ceil(0.95 * len(ordered)) - 1], "raw_ms": values}
+
+    lat = {name: summary(v) for name, v in samples.items()}
+    return {"metric": "refresh-only latency (ms), reference benchmark grid", "length": length,
+            "interval_count": count, "token_budget": budget, "intervals": intervals,
+            "causal_query_key_pairs": sum(p + 1 for p in positions), "position_shift": alignment["position_shift"],
+            "value": lat["hip"]["median_ms"], "unit": "ms", "higher_is_better": False,
+            "reference_same_gpu_ms": lat["reference_packed_sdpa"]["median_ms"],
+            "speedup": lat["reference_packed_sdpa"]["median_ms"] / lat["hip"]["median_ms"],
+            "latency": lat, "max_abs_vs_reference": max_abs, "warmups": warmups, "repeats": repeats, "seed": seed,
+            "scope": "refresh only (ownership copy, plan upload, packed forward); the shift is untimed as in the "
+                     "reference benchmark", "dtype": "bf16",
+            "data": "synthetic (random-init 8B-shaped Llama, K/V ~ N(0,1), random ids)"}
 
 
 # ----------------------------------------------------------------------------- main
+def run_workload(args, workload: Workload, device) -> dict:
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.cache import OperatorShim
+
+    _native.lib()
+    model = make_model(device, workload)
+    shim = OperatorShim(model)
+    old, old_ids, new_ids = make_request(device, workload)
+    intervals = workload.intervals()
+    headline = workload.name == "c3"
+
+    # correctness gate (untimed): rotated/copied rows bit-exact, refreshed rows against
+    # the reference path and an fp32 control at every layer
+    checks = {} if args.no_reference else parity_checks(model, shim, old, old_ids, new_ids, intervals,
+                                                        with_control=not args.no_fp32_control)
+
+    step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals)  # noqa: E731
+    ms = time_steps(step, args.steps, args.warmup)
+    kernels = measure_kernels(model, workload, old, old_ids, new_ids, device)
+    roofline, north = rooflines(kernels, workload.name)
+
+    reference = None
+    if not args.no_reference:
+        ref_ms = time_steps(lambda: reference_stage(model, old, old_ids, new_ids, intervals), args.steps,
+                            max(1, args.warmup))
+        reference = {"ms_per_step": ref_ms, "speedup": ref_ms / ms,
+                     "what": "reference eager path on the same GPU: per-layer rotate chain + cats, clone_cache, "
+                             "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv"}
+    scoring = scoring_measurement(model, new_ids, device) if headline else None
+    del old
+    if args.no_cpu_baseline:
+        cpu = None
+    elif headline:
+        cpu = cpu_baseline(workload, args.cpu_layers)
+    else:
+        cpu = cpu_kernel_baseline(workload)
+    suffix = workload.suffix
+    rotate = kernels["kvr_rope_delta_rotate"]
+    line = {
+        "metric": METRIC if headline else f"refresh-stage latency (ms) per repair, {workload.name}",
+        "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init model of the workload's shape, K/V ~ N(0,1), random ids)",
+        "config": {"workload": workload.description, "layers": workload.layers, "kv_heads": workload.hkv,
+                   "q_heads": workload.hq, "head_dim": workload.dim, "cache_tokens": workload.total,
+                   "edited_tokens": workload.edited, "suffix_rows": suffix, "shift": -workload.delete_span,
+                   "budget_rows": len(workload.positions()),
+                   "intervals": intervals if len(intervals) <= 16 else f"{len(intervals)} intervals"},
+        "rotate_GBps": rotate["achieved_GBps"],
+        "rotate": {"avg_us": rotate["avg_us"], "algorithmic_bytes": rotate["algorithmic_bytes"],
+                   "frac_of_peak": rotate["frac_of_hbm_peak"]},
+        "roofline": roofline, "rooflines": north, "kernels": kernels,
+        "kernel_timing": "HIP events around 5 replays of a graph of 20 back-to-back launches of each libkvrepair "
+                         "call with the stage's shapes (device time only); kvr_linear_multi = one layer's four "
+                         "projections, per call",
+        "reference_same_gpu": reference, "checks": checks, "selection_scoring": scoring,
+        "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
+    }
+    return line
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
+                        help="BASELINE configuration (c3 is the headline; others print a secondary line)")
+    parser.add_argument("--grid", action="store_true", help="the reference benchmark's grid (one line per case)")
+    parser.add_argument("--grid-repeats", type=int, default=20)
+    parser.add_argument("--grid-warmups", type=int, default=10)
     parser.add_argument("--cpu-layers", type=int, default=4, help="layers in the bounded CPU-baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-reference", action="store_true", help="skip the same-GPU reference stage")
+    parser.add_argument("--no-reference", action="store_true", help="skip the same-GPU reference stage and checks")
+    parser.add_argument("--no-fp32-control", action="store_true", help="parity checks without the fp32 control")
     parser.add_argument("--calibration-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB three times with a plain device-to-device "
                              "copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
@@ -440,140 +967,19 @@ def main(argv=None) -> int:
         parser.error("steps must be positive and warmup nonnegative")
     if not torch.cuda.is_available():
         parser.error("bench.py needs a GPU")
-
-    from kv_cache_repair_amd import _native
-    from kv_cache_repair_amd.cache import OperatorShim, rope_delta_rotate_
-
-    _native.lib()
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
-    model = make_model(device)
-    shim = OperatorShim(model)
-    old, old_ids, new_ids = make_request(device)
-    intervals = c3_intervals()
-    positions = [p for s, e in intervals for p in range(s, e)]
+    if args.grid:
+        from kv_cache_repair_amd import _native
 
-    # correctness gate (untimed): rotated/copied rows bit-exact, refreshed rows close
-    ours = hip_stage(shim, old, old_ids, new_ids, intervals)
-    checks = {}
-    if not args.no_reference:
-        theirs = reference_stage(model, old, old_ids, new_ids, intervals)
-        keep = torch.ones(new_ids.shape[1], dtype=torch.bool, device=device)
-        keep[positions] = False
-        bit_exact, max_abs, min_cos = True, 0.0, 1.0
-        for a_l, b_l in zip(ours.layers, theirs.layers):
-            for a, b in ((a_l.keys, b_l.keys), (a_l.values, b_l.values)):
-                bit_exact &= bool(torch.equal(a[:, :, keep].view(torch.int16), b[:, :, keep].view(torch.int16)))
-                sa, sb = a[:, :, positions].float(), b[:, :, positions].float()
-                max_abs = max(max_abs, (sa - sb).abs().max().item())
-                cos = torch.nn.functional.cosine_similarity(sa.reshape(-1, DIM), sb.reshape(-1, DIM), dim=-1)
-                min_cos = min(min_cos, cos.min().item())
-        checks = {"unselected_rows_bit_exact_vs_reference": bit_exact, "selected_rows_max_abs": max_abs,
-                  "selected_rows_min_cos": min_cos}
-        del theirs
-    del ours
-    torch.cuda.synchronize()
-
-    step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals)  # noqa: E731
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # `value`: K uninstrumented steps (each decoder layer is one native call that
-    # enqueues its kernels from C). Then K more steps with every layer's kernels
-    # dispatched one by one from Python (native_layers=False: the same kernels
-    # with the same arguments, bit-identical output) and HIP events around each
-    # libkvrepair launch, for the per-kernel timings and the roofline.
-    ms = time_steps(step, args.steps, 0)
-    dispatched = lambda: hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=False)  # noqa: E731
-    dispatched()
-    torch.cuda.synchronize()
-    timer = KernelTimer()
-    timer.install()
-    timer.active = True
-    instrumented_ms = time_steps(dispatched, args.steps, 0)
-    timer.active = False
-    torch.cuda.synchronize()
-    kernels = timer.summary(args.steps)
-
-    # rotate-only launch over the same 32 suffix K views (BASELINE "rotate GB/s")
-    suffix = TOTAL - DELETE_AT - DELETE_SPAN
-    keys = [l.keys[:, :, DELETE_AT + DELETE_SPAN:] for l in old.layers]
-    outs = [torch.empty(1, HKV, suffix, DIM, dtype=torch.bfloat16, device=device) for _ in keys]
-    inv = model.model.rotary_emb.inv_freq.to(device=device, dtype=torch.float32).contiguous()
-    for _ in range(3):
-        rope_delta_rotate_(keys, outs, -DELETE_SPAN, inv)
-    torch.cuda.synchronize()
-    timer.reset()
-    timer.active = True
-    for _ in range(20):
-        rope_delta_rotate_(keys, outs, -DELETE_SPAN, inv)
-    timer.active = False
-    torch.cuda.synchronize()
-    rotate = timer.summary(20)["kvr_rope_delta_rotate"]
-    timer.uninstall()
-    del outs
-
-    reference = None
-    if not args.no_reference:
-        ref_ms = time_steps(lambda: reference_stage(model, old, old_ids, new_ids, intervals), args.steps,
-                            max(1, args.warmup))
-        reference = {"ms_per_step": ref_ms, "speedup": ref_ms / ms,
-                     "what": "reference eager path on the same GPU: per-layer rotate chain + cats, clone_cache, "
-                             "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv"}
-
-    # algorithmic bytes (one launch)
-    esz = 2
-    rotate_bytes = 2 * LAYERS * HKV * suffix * DIM * esz
-    build_bytes = 2 * 2 * LAYERS * HKV * (DELETE_AT + suffix) * DIM * esz
-    max_pos = max(positions)
-    attn_bytes = (2 * len(positions) * HQ * DIM + 2 * HKV * (max_pos + 1) * DIM) * esz
-    attn_flops = 4 * HQ * DIM * sum(p + 1 for p in positions)
-    scatter_bytes = 2 * 2 * HKV * len(positions) * DIM * esz
-    # fresh-row epilogue: read q, k, v and cos/sin, write rotated q, cache K and V rows
-    rope_scatter_bytes = (2 * (HQ + 2 * HKV) + 2) * len(positions) * DIM * esz
-    # projections (q/k/v, o, gate/up, down per layer): every weight byte once, plus x in and y out;
-    # averaged over the step's launches of kvr_linear_multi (four shapes)
-    rows = len(positions)
-    qkv_cols = (HQ + 2 * HKV) * DIM
-    gemm_layer_bytes = esz * (HIDDEN * qkv_cols + HQ * DIM * HIDDEN + 2 * MLP * HIDDEN + MLP * HIDDEN
-                              + rows * (HIDDEN + qkv_cols) + rows * (HQ * DIM + HIDDEN)
-                              + rows * (HIDDEN + MLP) + rows * (MLP + HIDDEN))
-    gemm_launches = kernels.get("kvr_linear_multi", {}).get("launches_per_step", 0.0)
-    gemm_bytes = LAYERS * gemm_layer_bytes / gemm_launches if gemm_launches else 0
-    per_kernel = {
-        "kvr_shift_cache_build": build_bytes, "kvr_packed_causal_attention": attn_bytes,
-        "kvr_rope_scatter_kv": rope_scatter_bytes, "kvr_indexed_scatter_kv": scatter_bytes,
-        "kvr_linear_multi": gemm_bytes}
-    for name, b in per_kernel.items():
-        if name in kernels:
-            kernels[name]["algorithmic_bytes"] = b
-            kernels[name]["achieved_GBps"] = b / (kernels[name]["avg_us"] * 1e3)
-    kernels["kvr_packed_causal_attention"]["achieved_TFLOPs"] = \
-        attn_flops / (kernels["kvr_packed_causal_attention"]["avg_us"] * 1e6)
-    dominant = max(per_kernel, key=lambda n: kernels.get(n, {}).get("total_us_per_step", 0.0))
-    achieved = kernels[dominant]["achieved_GBps"]
-    traffic = measured_traffic(dominant)
-    roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                "avg_launch_us": kernels[dominant]["avg_us"], "algorithmic_bytes_per_launch": per_kernel[dominant]}
-
-    scoring = scoring_measurement(model, new_ids, device)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_layers)
-    line = {
-        "metric": METRIC, "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (random-init 8B-shaped Llama, K/V ~ N(0,1), random ids)",
-        "config": {"workload": "c3: 8B-shaped Llama, 8192-token cache, delete 512 @2048, 64-token budget in 16x4",
-                   "layers": LAYERS, "kv_heads": HKV, "q_heads": HQ, "head_dim": DIM, "cache_tokens": TOTAL,
-                   "edited_tokens": TOTAL - DELETE_SPAN, "suffix_rows": suffix, "shift": -DELETE_SPAN,
-                   "budget_rows": len(positions), "intervals": intervals},
-        "rotate_GBps": rotate_bytes / (rotate["avg_us"] * 1e3),
-        "rotate": {"avg_us": rotate["avg_us"], "algorithmic_bytes": rotate_bytes,
-                   "frac_of_peak": rotate_bytes / (rotate["avg_us"] * 1e3) / HBM_PEAK_GBPS},
-        "kernels": kernels, "instrumented_ms_per_step": instrumented_ms, "roofline": roofline,
-        "reference_same_gpu": reference, "checks": checks, "selection_scoring": scoring,
-        "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
-    }
+        _native.lib()
+        model = make_model(device, C3)
+        for length in (2048, 8192):
+            for count in (1, 4, 16):
+                print(json.dumps(grid_case(model, length, count, 64, args.grid_warmups, args.grid_repeats, 71)),
+                      flush=True)
+        return 0
+    line = run_workload(args, WORKLOADS[args.workload], device)
     print(json.dumps(line), flush=True)
     if args.calibration_copy_mib > 0:
         src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=device)

@@ -1193,6 +1193,25 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     const int64_t wide_units = (n_sel + kGroupRows - 1) / kGroupRows * heads;
     const int group_rows = (mfma && 2 * wide_units <= kTargetBlocks) ? kTileGroupRows : kGroupRows;
     const int64_t n_groups = (n_sel + group_rows - 1) / group_rows;
+    if (n_groups == 0) {
+        // No selected rows: a header-only schedule (no groups, no work).
+        const int64_t need = kHeader;
+        if (!schedule) return need;
+        if (capacity < need) return KVR_E_CAPACITY;
+        memset(schedule, 0, sizeof(int32_t) * kHeader);
+        schedule[H_MAGIC] = kMagic;
+        schedule[H_VERSION] = kVersion;
+        schedule[H_QT] = qt;
+        schedule[H_NHG] = n_head_groups;
+        schedule[H_HQ] = n_q_heads;
+        schedule[H_HKV] = n_kv_heads;
+        schedule[H_D] = head_dim;
+        schedule[H_KIND] = mfma ? KIND_MFMA : KIND_GENERIC;
+        schedule[H_NKEYS] = static_cast<int32_t>(n_keys);
+        schedule[H_DTYPE] = dtype;
+        schedule[H_GROUP_ROWS] = group_rows;
+        return need;
+    }
 
     std::vector<GroupKeys> keys(static_cast<size_t>(n_groups));
     for (int64_t g = 0; g < n_groups; ++g) keys[g] = group_keys(positions, n_sel, g, group_rows);

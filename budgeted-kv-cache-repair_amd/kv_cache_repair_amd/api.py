@@ -19,6 +19,7 @@ from typing import Any, Sequence
 
 import torch
 
+from .alignment import token_alignment_arrays
 from .cache import OperatorShim, build_halo_cache
 from .execution import positions_to_intervals
 from .kernels.executor import layer_kv
@@ -57,11 +58,22 @@ def _check_budget(budget_percent: float) -> float:
     return value
 
 
-def _encode(model: Any, tokenizer: Any, text: str) -> torch.Tensor:
+def _encode_host(model: Any, tokenizer: Any, text: str) -> torch.Tensor:
+    """Token ids [1, tokens] (int64, host), checked against the embedding table:
+    the refresh gathers embedding rows by these ids on the GPU, so an id outside
+    the vocabulary is refused here, before any device work."""
     ids = tokenizer(text, add_special_tokens=False, return_tensors="pt")["input_ids"]
     if not isinstance(ids, torch.Tensor) or ids.ndim != 2 or ids.shape[0] != 1:
         raise ValueError("tokenizer must return input_ids with shape [1, tokens]")
-    return ids.to(device=model.get_input_embeddings().weight.device, dtype=torch.long)
+    ids = ids.to(device="cpu", dtype=torch.long)
+    vocab = int(model.get_input_embeddings().weight.shape[0])
+    if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= vocab):
+        raise ValueError(f"tokenizer returned token ids outside the model vocabulary [0, {vocab})")
+    return ids
+
+
+def _to_model_device(model: Any, ids: torch.Tensor) -> torch.Tensor:
+    return ids.to(device=model.get_input_embeddings().weight.device)
 
 
 def _selection(positions: Sequence[int], suffix_start: int, length: int, budget: int, metadata) -> Selection:
@@ -90,8 +102,9 @@ def _budget_selection(length: int, suffix_start: int, budget_percent: float) -> 
         metadata["selection"] = "full_suffix"
         return _selection(range(suffix_start, length), suffix_start, length, budget, metadata)
     raise NotImplementedError(
-        "query-relevance (SUR) support selection is not part of this build; select positions with the "
-        "reference select_support and call repair_with_positions")
+        f"a {budget_percent:g}% budget ({budget} of {suffix_tokens} suffix tokens) needs query-relevance (SUR) "
+        "support selection, which is not part of this build; select positions with the reference select_support "
+        "and call repair_with_positions, or use a 0% or 100% budget")
 
 
 @torch.no_grad()
@@ -103,7 +116,7 @@ def select_support(model: Any, tokenizer: Any, edited_text: str, query: str, *, 
     selection, which this build does not provide (NotImplementedError).
     """
     budget_percent = _check_budget(budget_percent)
-    ids = _encode(model, tokenizer, edited_text)
+    ids = _encode_host(model, tokenizer, edited_text)
     return _budget_selection(int(ids.shape[1]), suffix_start, budget_percent)
 
 
@@ -123,15 +136,17 @@ def _check_model(model: Any) -> None:
     if (getattr(config, "use_sliding_window", False) or getattr(base, "has_sliding_layers", False)
             or any(kind != "full_attention" for kind in getattr(config, "layer_types", []) or [])):
         raise ValueError("repair requires full attention, not sliding or hybrid attention")
-    device = model.get_input_embeddings().weight.device
-    if device.type != "cuda" or torch.version.hip is None or any(p.device != device for p in model.parameters()):
-        raise ValueError("repair requires one ROCm GPU device holding every parameter")
     if any(getattr(module, "_hf_hook", None) is not None for module in model.modules()):
         raise ValueError("repair does not support dispatch or offload hooks")
     if any("forward" in module.__dict__ for module in model.modules()):
         raise ValueError("repair does not support per-instance forward overrides")
     if getattr(model, "is_quantized", False):
         raise ValueError("repair does not support quantized models")
+    # The device check comes last: every other rejection above is host-only and
+    # names its cause whatever device the model is on.
+    device = model.get_input_embeddings().weight.device
+    if device.type != "cuda" or torch.version.hip is None or any(p.device != device for p in model.parameters()):
+        raise ValueError("repair requires one ROCm GPU device holding every parameter")
 
 
 def _check_span(original_text: str, delete_span) -> tuple[int, int]:
@@ -145,28 +160,39 @@ def _check_span(original_text: str, delete_span) -> tuple[int, int]:
 
 
 def _prepare(model, tokenizer, old_cache, original_text, start, end):
+    """Model contract, both tokenizations (host) and the old cache's shape, in
+    the reference's order (api.py:208-219); no device work."""
     _check_model(model)
-    old_ids = _encode(model, tokenizer, original_text)
+    old_ids = _encode_host(model, tokenizer, original_text)
     old_length = int(old_ids.shape[1])
-    if not old_length or len(old_cache.layers) != model.config.num_hidden_layers:
+    layers = getattr(old_cache, "layers", None)
+    if not old_length or layers is None or len(layers) != model.config.num_hidden_layers:
         raise ValueError("old_cache must contain every model layer for a nonempty prompt")
-    for i in range(len(old_cache.layers)):
+    device = model.get_input_embeddings().weight.device
+    for i in range(len(layers)):
         key, value = layer_kv(old_cache, i)
         if key.ndim != 4 or key.shape != value.shape or key.shape[0] != 1 or key.shape[2] != old_length:
             raise ValueError("old_cache shape does not match the batch-one original prompt")
-        if key.device != old_ids.device or value.device != old_ids.device:
+        if key.device != device or value.device != device:
             raise ValueError("cache and model must be on the same device")
     edited_text = original_text[:start] + original_text[end:]
-    edited_ids = _encode(model, tokenizer, edited_text)
+    edited_ids = _encode_host(model, tokenizer, edited_text)
     return old_ids, edited_text, edited_ids
 
 
 def _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text, selector):
-    shim = OperatorShim(model, tokenizer)
-    shifted, alignment = build_halo_cache(shim, old_cache, old_ids, edited_ids, halo_tokens=0)
+    """Select on the host first (the suffix start comes from the host alignment,
+    the same one build_halo_cache computes), so a request this build cannot
+    serve is refused before any device work; then shift and refresh."""
+    alignment = token_alignment_arrays(old_ids[0].numpy(), edited_ids[0].numpy())
     selection = selector(int(edited_ids.shape[1]), int(alignment["new_suffix_start"]))
-    execution = packed_refresh_owned_(shim, shifted, edited_ids, list(selection.intervals))
-    return RepairResult(cache=shifted, edited_text=edited_text, input_ids=edited_ids, selection=selection,
+    shim = OperatorShim(model, tokenizer)
+    old_dev, edited_dev = _to_model_device(model, old_ids), _to_model_device(model, edited_ids)
+    shifted, alignment = build_halo_cache(shim, old_cache, old_dev, edited_dev, halo_tokens=0)
+    if int(alignment["new_suffix_start"]) != selection.suffix_start:
+        raise RuntimeError("host alignment and shift-cache alignment disagree")
+    execution = packed_refresh_owned_(shim, shifted, edited_dev, list(selection.intervals))
+    return RepairResult(cache=shifted, edited_text=edited_text, input_ids=edited_dev, selection=selection,
                         metadata={"alignment": alignment, "execution": execution, "executor": "packed"})
 
 
@@ -184,7 +210,7 @@ def repair_after_deletion(model: Any, tokenizer: Any, old_cache: Any, original_t
     """
     budget_percent = _check_budget(budget_percent)
     if executor != "packed":
-        raise ValueError("executor must be 'packed'")
+        raise ValueError("executor must be 'packed' (the sequential interval executor is not part of this build)")
     start, end = _check_span(original_text, delete_span)
     old_ids, edited_text, edited_ids = _prepare(model, tokenizer, old_cache, original_text, start, end)
     return _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text,

@@ -59,6 +59,13 @@ def _rotary(model: Any, device: torch.device):
     return inv_freq.contiguous(), float(getattr(rotary, "attention_scaling", 1.0)), 2 * int(inv_freq.numel())
 
 
+def _vocab_size(model: Any) -> int | None:
+    """Rows of the model's input embedding table, or None when it has none."""
+    get = getattr(model, "get_input_embeddings", None)
+    weight = getattr(get(), "weight", None) if callable(get) else None
+    return int(weight.shape[0]) if isinstance(weight, torch.Tensor) and weight.ndim == 2 else None
+
+
 def _shift_launcher(old_k, old_v, new_k, new_v, *, inv_freq, scaling, rotary_dim):
     """kvr_shift_cache_build over lists of per-layer tensors, with every pointer
     and stride argument bound now; the returned function takes the row ranges
@@ -227,6 +234,11 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     shift_tail = _shift_launcher([k for k, _ in old], [v for _, v in old], new_k, new_v, inv_freq=inv_freq,
                                  scaling=scaling, rotary_dim=rotary_dim) if n_new else None
     ids = ids.cpu().numpy()
+    vocab = _vocab_size(generator)
+    if ids.size and (int(ids.min()) < 0 or (vocab is not None and int(ids.max()) >= vocab)):
+        # the refresh and any boundary recomputation gather embedding rows by
+        # these ids on the GPU: refuse them here, before any launch
+        raise ValueError("token ids must lie in [0, vocab_size) of the model's embedding table")
     align = token_alignment_arrays(ids[:n_old], ids[n_old:])
     halo = min(max(int(halo_tokens), 0), align["suffix"])
     recompute_end = align["new_suffix_start"] + halo

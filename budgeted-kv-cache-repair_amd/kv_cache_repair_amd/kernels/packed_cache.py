@@ -557,12 +557,6 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
         raise ValueError("packed executor requires full attention")
     if any(kind != "full_attention" for kind in getattr(config, "layer_types", []) or []):
         raise ValueError("packed executor rejects sliding/hybrid attention")
-    if device.type != "cuda" or torch.version.hip is None:
-        raise ValueError("packed HIP executor requires one ROCm GPU device")
-    if off_device:
-        raise ValueError("packed executor requires all model parameters on the request device")
-    if True in [t.get_device() != index for i in range(len(base_cache.layers)) for t in layer_kv(base_cache, i)]:
-        raise ValueError("packed executor requires all cache layers on the request device")
     if hooked:
         raise ValueError("packed executor does not support dispatch/offload hooks")
     if overridden:
@@ -574,6 +568,13 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
         raise ValueError("packed HIP executor requires an even head dimension <= 256")
     if config.num_attention_heads % config.num_key_value_heads:
         raise ValueError("query head count must be divisible by KV head count")
+    # Device checks last: every rejection above is host-only and names its cause.
+    if device.type != "cuda" or torch.version.hip is None:
+        raise ValueError("packed HIP executor requires one ROCm GPU device")
+    if off_device:
+        raise ValueError("packed executor requires all model parameters on the request device")
+    if True in [t.get_device() != index for i in range(len(base_cache.layers)) for t in layer_kv(base_cache, i)]:
+        raise ValueError("packed executor requires all cache layers on the request device")
     _require_gfx950(device)
     with _PLAN_LOCK:
         _QUALIFIED[base] = (fingerprint, index)
@@ -646,11 +647,19 @@ def _launcher(device_plan: DeviceIndexedPlan, config, key: torch.Tensor) -> _Lau
                      positions_ptr=device_plan.positions.data_ptr())
 
 
-def _check_backends(attention_backend, writeback_backend):
-    if attention_backend not in _BACKENDS:
-        raise ValueError("attention_backend must be 'hip'")
-    if writeback_backend not in _BACKENDS:
-        raise ValueError("writeback_backend must be 'hip'")
+def _check_backends(attention_backend, writeback_backend) -> tuple[str, str]:
+    """The backends that run: always the HIP kernels. The reference's default
+    names ("sdpa" attention, "torch" writeback, packed_cache.py:225-231) are
+    accepted so callers that pass them explicitly keep working; they select the
+    same kernels as "hip" (the receipt names what ran). The reference's
+    experimental "triton"/"flex" backends and unknown names are rejected."""
+    if attention_backend not in _BACKENDS + ("sdpa",):
+        raise ValueError("attention_backend must be 'hip' (or the reference default 'sdpa', served by the same "
+                         "HIP kernel)")
+    if writeback_backend not in _BACKENDS + ("torch",):
+        raise ValueError("writeback_backend must be 'hip' (or the reference default 'torch', served by the same "
+                         "HIP kernel)")
+    return "hip", "hip"
 
 
 def _check_ids(edited_ids_t):
@@ -848,15 +857,16 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
 
 @torch.no_grad()
 def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
-                           intervals: Sequence[tuple[int, int]], *, attention_backend: str = "hip",
-                           writeback_backend: str = "hip", plan: Any = None, fused_epilogue: bool = True,
+                           intervals: Sequence[tuple[int, int]], *, attention_backend: str = "sdpa",
+                           writeback_backend: str = "torch", plan: Any = None, fused_epilogue: bool = True,
                            fused_layers: bool | None = None, fused_projections: bool | None = None,
                            native_layers: bool | None = None) -> tuple[Any, dict[str, Any]]:
     """Recompute sorted selected rows in one native layer-major forward.
 
     Same signature, validation order, receipt and ownership contract as the
-    reference executor (packed_cache.py:225-298); the backends are the gfx950
-    HIP kernels. ``plan`` optionally supplies a reusable host IndexedPlan for
+    reference executor (packed_cache.py:225-298), including its default backend
+    names; every accepted backend name runs the gfx950 HIP kernels (the receipt
+    records "hip"). ``plan`` optionally supplies a reusable host IndexedPlan for
     exactly these intervals and length. The borrowed ``base_cache`` is never
     mutated: a nonempty repair returns an independently owned cache (one
     libkvrepair copy launch), an empty one returns ``base_cache`` itself.
@@ -876,7 +886,7 @@ def packed_interval_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tenso
     the same arguments, bit-identical to the Python-dispatched fused shells);
     the default (None) does so whenever the three fusions above are active.
     """
-    _check_backends(attention_backend, writeback_backend)
+    attention_backend, writeback_backend = _check_backends(attention_backend, writeback_backend)
     _check_ids(edited_ids_t)
     length = int(edited_ids_t.shape[1])
     layer_count = _validate_cache(base_cache, length)

@@ -355,9 +355,11 @@ int kvr_copy_kv_interval(void* out_k, void* out_v, const void* in_k, const void*
  * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`
  * is the HOST copy of the strictly increasing selected positions (the
  * reference IndexedPlan.positions, indexed_attention.py:56-83).
- * chunk_keys <= 0 selects a size from the geometry. Writes at most `capacity`
+ * chunk_keys == 0 selects a size from the geometry; a positive value must be
+ * a multiple of 64; a negative value is rejected. Writes at most `capacity`
  * int32 entries to `schedule` and returns the entry count, or a negative
  * status. With schedule == NULL it returns the required entry count.
+ * n_sel == 0 gives a header-only schedule (no work).
  */
 int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_sel, int64_t n_keys, int32_t n_q_heads,
                                int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys,

@@ -1,0 +1,234 @@
+"""The public repair API end to end on the GPU (tiny fp32 models, in-memory
+tokenizer), against the oracle's restatement of the reference's schedules.
+
+Vectors follow the reference's public-contract tests (tests/test_api.py:
+152-273): 0% and 100% budgets agree with the sequential interval recurrence,
+the full suffix reproduces a clean prefill, trailing and whole-prompt
+deletions leave an empty suffix, boundary retokenization is recomputed outside
+the budget, a cache of the wrong length is refused, and the input cache is
+never modified. Also the packed attention plugin on K = 0 / V = arange, where
+every row's output is exactly position / 2 (tests/test_packed_cache.py:207-224).
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+SUFFIX = "alpha beta gamma . " * 25
+
+
+@pytest.fixture
+def tokenizer():
+    from tokenizers import Tokenizer
+    from tokenizers.models import WordLevel
+    from tokenizers.pre_tokenizers import WhitespaceSplit
+    from transformers import PreTrainedTokenizerFast
+
+    words = ["[UNK]", "prefix", "obsolete", "discard", "alpha", "beta", "gamma", ".", "red", "blue", "redblue"]
+    backend = Tokenizer(WordLevel({w: i for i, w in enumerate(words)}, unk_token="[UNK]"))
+    backend.pre_tokenizer = WhitespaceSplit()
+    return PreTrainedTokenizerFast(tokenizer_object=backend, unk_token="[UNK]")
+
+
+@pytest.fixture(params=["llama", "qwen3"])
+def model(request, gpu_device):
+    from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM
+
+    options = dict(vocab_size=32, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=4,
+                   num_key_value_heads=2, head_dim=8, max_position_embeddings=256, attention_dropout=0.0)
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(23)
+        if request.param == "llama":
+            instance = LlamaForCausalLM(LlamaConfig(**options))
+        else:
+            instance = Qwen3ForCausalLM(Qwen3Config(**options, layer_types=["full_attention"] * 2))
+    instance.to(gpu_device).eval()
+    instance.set_attn_implementation("eager")
+    return instance
+
+
+def prefill(model, tokenizer, text):
+    ids = tokenizer(text, add_special_tokens=False, return_tensors="pt")["input_ids"].to(model.device)
+    with torch.no_grad():
+        return model.base_model(input_ids=ids, use_cache=True).past_key_values
+
+
+def snapshot(cache):
+    return [(l.keys.clone(), l.values.clone()) for l in cache.layers]
+
+
+def assert_unchanged(cache, snap):
+    for layer, (k, v) in zip(cache.layers, snap):
+        assert torch.equal(layer.keys.view(torch.int32), k.view(torch.int32))
+        assert torch.equal(layer.values.view(torch.int32), v.view(torch.int32))
+
+
+def assert_caches_close(actual, expected, *, rows=None):
+    assert len(actual.layers) == len(expected.layers)
+    for a, e in zip(actual.layers, expected.layers):
+        for x, y in ((a.keys, e.keys), (a.values, e.values)):
+            if rows is not None:
+                x, y = x[:, :, rows], y[:, :, rows]
+            assert x.shape == y.shape
+            torch.testing.assert_close(x, y, rtol=1e-5, atol=2e-6)
+
+
+def request(model, tokenizer):
+    prefix, obsolete = "prefix ", "obsolete discard "
+    original = prefix + obsolete + SUFFIX
+    return dict(model=model, tokenizer=tokenizer, old_cache=prefill(model, tokenizer, original),
+                original_text=original, delete_span=(len(prefix), len(prefix) + len(obsolete)), query="alpha")
+
+
+@pytest.mark.parametrize("budget", [0, 100])
+def test_budget_edges_match_the_sequential_recurrence_and_keep_the_input(model, tokenizer, budget):
+    from kv_cache_repair_amd import repair_after_deletion
+
+    req = request(model, tokenizer)
+    snap = snapshot(req["old_cache"])
+    result = repair_after_deletion(**req, budget_percent=budget)
+    assert result.edited_text == "prefix " + SUFFIX
+    assert tuple(result.input_ids.shape) == (1, 101)
+    assert result.selection.budget_tokens == budget and result.selection.suffix_start == 1
+    assert result.selection.positions == (() if budget == 0 else tuple(range(1, 101)))
+    assert result.metadata["executor"] == "packed"
+    assert result.metadata["alignment"]["mandatory_changed_tokens"] == 0
+    assert result.metadata["alignment"]["position_shift"] == -2
+    old_ids = tokenizer(req["original_text"], add_special_tokens=False, return_tensors="pt")["input_ids"]
+    shifted, _ = ref.build_halo_cache(model, req["old_cache"], old_ids.to(model.device), result.input_ids, 0)
+    expected = ref.sequential_repair(model, shifted, result.input_ids, list(result.selection.intervals))
+    assert_caches_close(result.cache, expected)
+    assert_unchanged(req["old_cache"], snap)
+    for new, old in zip(result.cache.layers, req["old_cache"].layers):
+        assert new.keys.data_ptr() != old.keys.data_ptr() and new.values.data_ptr() != old.values.data_ptr()
+
+
+def test_full_suffix_repair_reproduces_a_clean_prefill(model, tokenizer):
+    from kv_cache_repair_amd import repair_after_deletion
+
+    result = repair_after_deletion(**request(model, tokenizer), budget_percent=100)
+    assert result.selection.positions == tuple(range(1, 101))
+    assert_caches_close(result.cache, prefill(model, tokenizer, result.edited_text))
+
+
+@pytest.mark.parametrize("span,edited", [((7, 21), "prefix "), ((0, 21), "")])
+def test_trailing_and_whole_prompt_deletions_leave_an_empty_suffix(model, tokenizer, span, edited):
+    from kv_cache_repair_amd import repair_after_deletion
+
+    original = "prefix obsolete alpha"
+    old = prefill(model, tokenizer, original)
+    snap = snapshot(old)
+    result = repair_after_deletion(model, tokenizer, old, original, delete_span=span, query="", budget_percent=5)
+    assert result.edited_text == edited
+    assert result.selection.suffix_tokens == result.selection.budget_tokens == 0
+    assert result.selection.positions == result.selection.intervals == ()
+    kept = 1 if edited else 0
+    assert result.cache.get_seq_length() == kept
+    assert_unchanged(old, snap)
+    for new, src in zip(result.cache.layers, old.layers):
+        assert torch.equal(new.keys, src.keys[:, :, :kept]) and torch.equal(new.values, src.values[:, :, :kept])
+
+
+def test_boundary_retokenization_is_recomputed_outside_the_budget(model, tokenizer):
+    from kv_cache_repair_amd import repair_after_deletion
+
+    original = "prefix red blue alpha beta"
+    join = original.index(" blue")
+    old = prefill(model, tokenizer, original)
+    result = repair_after_deletion(model, tokenizer, old, original, delete_span=(join, join + 1), query="alpha",
+                                   budget_percent=0)
+    assert result.edited_text == "prefix redblue alpha beta"
+    assert result.input_ids.tolist() == [[1, 10, 4, 5]]
+    assert (result.selection.suffix_start, result.selection.suffix_tokens, result.selection.budget_tokens) == (2, 2, 0)
+    assert result.metadata["alignment"]["mandatory_changed_tokens"] == 1
+    assert result.metadata["alignment"]["recomputed_tokens"] == 1
+    assert_caches_close(result.cache, prefill(model, tokenizer, result.edited_text), rows=slice(0, 2))
+
+
+def test_repair_with_caller_positions_matches_the_reference_packed_path(model, tokenizer):
+    from kv_cache_repair_amd import repair_with_positions
+
+    req = request(model, tokenizer)
+    req.pop("query")
+    snap = snapshot(req["old_cache"])
+    positions = [3, 4, 5, 40, 41, 99, 100]
+    result = repair_with_positions(**req, positions=positions)
+    assert result.selection.intervals == ((3, 6), (40, 42), (99, 101))
+    assert result.selection.metadata["selection"] == "caller"
+    old_ids = tokenizer(req["original_text"], add_special_tokens=False, return_tensors="pt")["input_ids"]
+    shifted, _ = ref.build_halo_cache(model, req["old_cache"], old_ids.to(model.device), result.input_ids, 0)
+    assert_caches_close(result.cache, ref.packed_sdpa_repair(model, shifted, result.input_ids,
+                                                             list(result.selection.intervals)))
+    assert_caches_close(result.cache, ref.sequential_repair(model, shifted, result.input_ids,
+                                                            list(result.selection.intervals)))
+    assert_unchanged(req["old_cache"], snap)
+    with pytest.raises(RuntimeError, match="suffix budget"):
+        repair_with_positions(**req, positions=[0, 3])  # position 0 is in the unchanged prefix
+
+
+def test_cache_of_the_wrong_length_is_refused(model, tokenizer):
+    from kv_cache_repair_amd import repair_after_deletion
+
+    req = request(model, tokenizer)
+    req["old_cache"] = ref.clone_cache(req["old_cache"], 5)
+    with pytest.raises(ValueError, match="old_cache shape"):
+        repair_after_deletion(**req)
+
+
+@pytest.mark.parametrize("budget", [2, 5])
+def test_partial_budgets_are_refused_before_any_device_work(model, tokenizer, monkeypatch, budget):
+    """The suffix start (hence the budget) is known from the host alignment, so a
+    budget this build cannot select is refused before the shift-cache build."""
+    from kv_cache_repair_amd import api, repair_after_deletion
+
+    def forbidden(*args, **kwargs):
+        raise AssertionError("no device work may run for a refused request")
+
+    monkeypatch.setattr(api, "build_halo_cache", forbidden)
+    monkeypatch.setattr(api, "packed_refresh_owned_", forbidden)
+    req = request(model, tokenizer)
+    snap = snapshot(req["old_cache"])
+    with pytest.raises(NotImplementedError, match=rf"\({budget} of 100 suffix tokens\)"):
+        repair_after_deletion(**req, budget_percent=budget)
+    assert_unchanged(req["old_cache"], snap)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_packed_attention_plugin_on_zero_keys_and_arange_values(gpu_device, dtype):
+    """K = 0 makes every visible key equally likely, so row r's output is the mean
+    of V[0..pos_r] = pos_r / 2 exactly; future keys cannot change it and a larger
+    legal unselected past value raises it."""
+    from kv_cache_repair_amd.kernels.indexed_attention import IndexedPlan
+    from kv_cache_repair_amd.kernels.packed_cache import _launcher, _packed_attention, _PackedContext
+
+    dim = 8 if dtype == torch.float32 else 64
+    plan = IndexedPlan((3, 4, 8, 9), 12).to(gpu_device)
+    query = torch.zeros(1, 4, 4, dim, dtype=dtype, device=gpu_device)
+    key = torch.zeros(1, 2, 12, dim, dtype=dtype, device=gpu_device)
+    value = torch.arange(12, dtype=torch.float32, device=gpu_device).reshape(1, 1, 12, 1).expand(1, 2, 12, dim)
+    value = value.to(dtype).contiguous()
+    launcher = _launcher(plan, SimpleNamespace(num_attention_heads=4), key)
+    context = _PackedContext(plan.positions, 12, "hip", plan, launcher)
+    module = SimpleNamespace(num_key_value_groups=2, is_causal=True)
+
+    def attend(v):
+        out, weights = _packed_attention(module, query, key, v, None, sur_packed_context=context)
+        assert weights is None and out.shape == (1, 4, 4, dim)
+        return out
+
+    base = attend(value)
+    for row, position in enumerate(plan.host_plan.positions):
+        assert torch.equal(base[0, row].float(), torch.full((4, dim), position / 2, device=gpu_device))
+    future = value.clone()
+    future[:, :, 10:] = 10000
+    assert torch.equal(attend(future), base)
+    past = value.clone()
+    past[:, :, 1] += 100
+    assert torch.all(attend(past) > base)

@@ -286,3 +286,20 @@ def test_decoder_layer_descriptors_validate_before_any_launch():
     assert lib.kvr_decoder_forward(None, 0, C.byref(d), None, None) == 0
     assert lib.kvr_decoder_forward(None, 2, C.byref(d), None, None) == -5
     assert lib.kvr_decoder_forward(C.byref(layer), -1, C.byref(d), None, None) == -1
+
+
+def test_empty_selection_gives_a_header_only_schedule():
+    """n_sel == 0 is valid (an empty support): a schedule with no groups and no
+    work, whose workspace is zero bytes, whatever chunk size is asked for."""
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    empty = _native.i64_array([0])
+    for chunk in (0, 64, 256):
+        need = lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, chunk, None, 0)
+        assert need == 17
+        buf = (ctypes.c_int32 * need)()
+        assert lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, chunk, buf, need) == need
+        assert (buf[2], buf[3], buf[5]) == (0, 0, 0)  # rows, groups, work items
+        assert lib.kvr_attention_workspace_bytes(buf, need, 32, 128) == 0
+    assert lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, -64, None, 0) == -1  # negative chunk
