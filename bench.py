@@ -227,6 +227,7 @@ def time_steps(fn, steps, warmup):
 
 
 # ----------------------------------------------------------------------------- reference stage (same GPU)
+@torch.no_grad()
 def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
     """The reference's eager path on this GPU: build_halo_cache with the per-layer
     rotate chain and cats (cache.py:103-144), clone_cache, boolean mask and

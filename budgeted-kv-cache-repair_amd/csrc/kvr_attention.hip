@@ -30,14 +30,15 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace kvr {
 namespace {
 
 constexpr int32_t kMagic = 0x4B565253;  // "KVRS"
-constexpr int32_t kVersion = 4;
-constexpr int kHeader = 17;
+constexpr int32_t kVersion = 5;
+constexpr int kHeader = 18;
 constexpr int kWorkInts = 4;               // (group, chunk, key_begin, key_end)
 constexpr int kRowTile = 16;               // rows per MFMA tile
 constexpr int kTilesPerGroup = 4;
@@ -50,6 +51,9 @@ constexpr int kMaxChunksPerGroup = 1024;   // merge weights fit in LDS
 #endif
 #ifndef KVR_ATTN_MAX_QT
 #define KVR_ATTN_MAX_QT 4
+#endif
+#ifndef KVR_ATTN_PAIR
+#define KVR_ATTN_PAIR 1
 #endif
 constexpr int kTargetBlocks = KVR_ATTN_TARGET_BLOCKS;  // one block per CU (MI355X: 256 CUs)
 constexpr float kLazyLog2 = 8.f;           // lazy-rescale headroom (log2 units): p <= 256
@@ -71,7 +75,8 @@ enum Header {
     H_NKEYS,
     H_DTYPE,
     H_MAXCHUNKS,
-    H_GROUP_ROWS
+    H_GROUP_ROWS,
+    H_PROB  // 0: probabilities enter PV as a hi + lo pair; 1: rounded to the input dtype (as SDPA rounds them)
 };
 enum Kind { KIND_GENERIC = 0, KIND_MFMA = 1 };
 
@@ -100,6 +105,7 @@ struct AttnArgs {
     int32_t group_rows;  // rows per group: kGroupRows, or kTileGroupRows (tile kernel)
     int32_t head_dim;
     int32_t out_vec;  // output rows take 8-byte stores (unit dim stride, aligned)
+    int32_t p_rounded;  // the schedule permits probabilities rounded to the input dtype (H_PROB)
     float scale_log2;  // scale * log2(e)
 };
 
@@ -129,6 +135,11 @@ template <> struct mma_t<bf16_t> {
     }
     // bf16 head = the upper half of the fp32 bits (truncation); p - head is exact
     // in fp32 and its RNE bf16 rounding leaves an error below 2^-16 |p|.
+    // two probabilities rounded to bf16 (RNE), packed
+    __device__ static inline uint32_t round2(float p0, float p1) {
+        const f32x2 r = {p0, p1};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+    }
     __device__ static inline void split(float p0, float p1, uint32_t& hi, uint32_t& lo) {
         const uint32_t b0 = __float_as_uint(p0), b1 = __float_as_uint(p1);
         hi = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
@@ -140,6 +151,10 @@ template <> struct mma_t<f16_t> {
     typedef _Float16 v8 __attribute__((ext_vector_type(8)));
     __device__ static inline f32x4 mma(v8 a, v8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    __device__ static inline uint32_t round2(float p0, float p1) {
+        return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(p0))) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(p1))) << 16);
     }
     __device__ static inline void split(float p0, float p1, uint32_t& hi, uint32_t& lo) {
         const _Float16 h0 = static_cast<_Float16>(p0), h1 = static_cast<_Float16>(p1);
@@ -718,6 +733,501 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
 }
 
 // ===========================================================================
+// Head-pair kernel (bf16 / fp16, head_dim 64 or 128, four query heads per KV
+// head group). Block = (KV head, head group, row group of RT row tiles,
+// chunk), 8 waves. A wave owns two query heads of one 16-row tile -- the two
+// MFMA column tiles share every K and V fragment it reads from LDS, so one
+// fragment read feeds two MFMAs -- and one of X = 8 / (2 RT) key classes.
+// Keys are staged 128 per step (four 32-key sub-tiles) by direct global->LDS
+// loads (no register staging), double-buffered; the wave of key class x
+// attends the step's sub-tiles x, x + X, ... With RT = 1 (16-row groups, few
+// selected rows) the four key classes of a head pair take one sub-tile each
+// per step and are combined through LDS at the end; with RT = 4 (64-row
+// groups) every wave takes all four sub-tiles of a step.
+//
+// LDS holds K and V row-major, 16-byte pieces XOR-swizzled by row (piece c of
+// key row r at c ^ (r mod D/8)), so every fragment read below is free of bank
+// conflicts. QK^T reads K fragments with 16-byte reads; the PV operand V^T is
+// read with gfx950's transposing ds_read_b64_tr_b16: within each 16-lane
+// group, lane i receives element i & 3 of the 8-byte pieces addressed by
+// lanes (i >> 2) + 4j, j = 0..3. Pointing lane s of group lj at key row
+// 16h + 4 lj + (s >> 2), dims 16 dt + 4 (s & 3) .. + 4 makes lane i receive
+// keys 16h + 4 lj .. + 4 of dim 16 dt + i: the V^T fragment whose k order
+// matches the score layout of the QK^T MFMA (lane (row, lj) holds keys
+// 16 kt + 4 lj + i), so P^T needs no permutation.
+// ===========================================================================
+constexpr int kPairSub = 32;                 // keys per sub-tile
+constexpr int kPairSubs = 4;                 // sub-tiles staged per step
+constexpr int kPairStepKeys = kPairSub * kPairSubs;
+constexpr int kPairThreads = 512;
+
+template <int D>
+struct PairCfg {
+    static constexpr int c8 = D / 8;                              // 16-byte pieces per row
+    static constexpr int tensor_bytes = kPairStepKeys * D * 2;    // K or V of one step
+    static constexpr int stage_bytes = 2 * tensor_bytes;          // K then V
+    static constexpr int bytes = 2 * stage_bytes;                 // double-buffered
+    static constexpr int pieces_per_wave = tensor_bytes / 16 / 8; // 16-byte pieces one wave loads per tensor
+    static constexpr int loads = pieces_per_wave / 64;            // load instructions per wave per tensor
+    static_assert(pieces_per_wave % 64 == 0, "whole load instructions");
+    // Piece swizzles (XOR on the 16-byte piece index; rows are keys). K: 8
+    // consecutive rows at one piece hit 8 distinct bank groups (a 16-byte read
+    // serves 8 lanes per cycle). V: the transposing read serves 16 lanes per
+    // cycle, 4 consecutive rows x 2 adjacent pieces, which 2 r spreads over 8
+    // distinct bank groups.
+    __host__ __device__ static constexpr int kswz(int r) { return r & (c8 - 1); }
+    __host__ __device__ static constexpr int vswz(int r) { return (2 * r) & (c8 - 1); }
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// 16 bytes per lane from `src` (per-lane global address) to LDS at `dst` + 16 *
+// lane (`dst` wave-uniform): global_load_lds_dwordx4, the LDS base in M0. Issued
+// as inline assembly so the compiler's wait-count pass, which cannot tell these
+// LDS writes from the stage being read, adds no vmcnt waits before LDS reads;
+// the kernel waits for them itself (vmcnt(0), then a barrier) before reading.
+__device__ inline void lds_dma16(const char* src, char* dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)dst)));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
+// HILO: probabilities enter PV as a hi + lo pair of 16-bit values (fp32-class,
+// the reference Triton kernel's precision); otherwise each is rounded to the
+// input dtype before PV, as the SDPA path the packed executor replaces rounds it.
+template <typename T, int D, bool HILO>
+struct PairWave {
+    using M = mma_t<T>;
+    using v8 = typename M::v8;
+    using C = PairCfg<D>;
+    static constexpr int DS = D / 32;  // k-steps of the QK^T MFMA
+    static constexpr int DT = D / 16;  // d tiles of the PV MFMA
+
+    v8 qf[2][DS];
+    f32x4 o[2][DT];
+    f32x4 lsum[2];    // row sums of P as a 17th output tile: row 0 of O^T += ones . P^T
+    float m_run[2];
+    int32_t pos;      // this lane's row position; -1 past the selected rows
+    v8 ones;          // A operand of the row-sum tile: row 0 all ones, rows 1..15 zero
+    // Per-lane byte offsets of this lane's fragment reads within a staged tile,
+    // for sub-tile row 0 (every sub-tile starts at a multiple of 16 rows, so the
+    // swizzle of a lane's rows does not depend on the sub-tile or key tile; those
+    // add compile-time offsets). K: row lq, piece 4 ds + lj. V (transposing
+    // reads): row 4 lj + (lq >> 2), dims 16 dt + 4 (lq & 3).
+    int32_t koff[DS];
+    int32_t voff[DT];
+
+    // byte offsets of piece c of row r in the swizzled K and V tiles
+    __device__ static inline int kpiece(int r, int c) { return (r * C::c8 + (c ^ C::kswz(r))) * 16; }
+    __device__ static inline int vpiece(int r, int c) { return (r * C::c8 + (c ^ C::vswz(r))) * 16; }
+
+    __device__ inline void init(int lq, int lj) {
+        offsets(lq, lj);
+        const uint16_t one = elem<T>::from_float(1.f);
+        const uint32_t w = lq == 0 ? (static_cast<uint32_t>(one) | (static_cast<uint32_t>(one) << 16)) : 0u;
+        ones = __builtin_bit_cast(v8, u32x4{w, w, w, w});
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            m_run[t] = -INFINITY;
+            lsum[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    __device__ inline void offsets(int lq, int lj) {
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) koff[ds] = kpiece(lq, 4 * ds + lj);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int d0 = 16 * dt + 4 * (lq & 3);
+            voff[dt] = vpiece(4 * lj + (lq >> 2), d0 >> 3) + (d0 & 4) * 2;
+        }
+    }
+
+    // K fragments of the sub-tile: [ds][kt], rows 16 kt + lq, pieces 4 ds + lj.
+    __device__ inline void read_k(const char* Ks, v8 (&kf)[DS][2]) {
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                kf[ds][kt] =
+                    __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(Ks + koff[ds] + 16 * kt * D * 2));
+    }
+
+    // S^T = K Q_t^T for head t: keys on the M axis, lane (lq, lj) gets keys
+    // 16 kt + 4 lj + i of row lq.
+    __device__ inline void qk(int t, const v8 (&kf)[DS][2], f32x4 (&st)[2]) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) st[kt] = M::mma(kf[ds][kt], qf[t][ds], st[kt]);
+    }
+
+    // Scores past a row's position become -inf (the causal mask; only sub-tiles
+    // that reach past the tile's first position need it).
+    __device__ inline void apply_mask(f32x4 (&st)[2], int32_t key0, int lj) {
+        const int32_t lim = pos - key0 - 4 * lj;  // key 16 kt + 4 lj + i is visible iff 16 kt + i <= lim
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st[kt][i] = (16 * kt + i <= lim) ? st[kt][i] : -INFINITY;
+    }
+
+    // Row maximum of head t's scores over this lane's keys, scaled.
+    __device__ inline float row_max(const f32x4 (&st)[2], float scale_log2, float (&x)[2][4]) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[kt][i] = st[kt][i];
+                mx = fmaxf(mx, x[kt][i]);
+            }
+        return mx * scale_log2;  // scale_log2 > 0: the scaled maximum is the raw maximum scaled
+    }
+
+    // Lazy move of head t's reference maximum: it moves only when a score
+    // exceeds it by more than kLazyLog2 (so p <= 2^8 and the fp32 accumulators
+    // cannot overflow); O and the row sums are rescaled then (rare).
+    __device__ inline void rescale_if(int t, float mx) {
+        if (__any(mx > m_run[t] + kLazyLog2)) {
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = (mx > m_run[t] + kLazyLog2) ? mx : m_run[t];
+            // 1 if unmoved, 0 from -inf; a row with no visible key keeps m = -inf
+            const float alpha = __builtin_amdgcn_exp2f(m_run[t] - (m_new == -INFINITY ? 0.f : m_new));
+            m_run[t] = m_new;
+            lsum[t] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[t][dt] *= alpha;
+        }
+    }
+
+    // two probabilities as B-operand halves: hi (+ lo) or the rounded pair
+    __device__ static inline void pack(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+        if (HILO)
+            M::split(p0, p1, hi, lo);
+        else
+            hi = M::round2(p0, p1);
+    }
+
+    // P = exp2(scale x - m) of head t as the B operand(s) of the PV MFMA:
+    // element 4h + i of lane (lq, lj) is key 16h + 4 lj + i.
+    __device__ inline void probs(int t, float (&x)[2][4], float scale_log2, u32x4& phi, u32x4& plo) {
+        const float m_use = (m_run[t] == -INFINITY) ? 0.f : m_run[t];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], scale_log2, -m_use));
+        uint32_t hv[4], lv[4] = {0u, 0u, 0u, 0u};
+        pack(x[0][0], x[0][1], hv[0], lv[0]);
+        pack(x[0][2], x[0][3], hv[1], lv[1]);
+        pack(x[1][0], x[1][1], hv[2], lv[2]);
+        pack(x[1][2], x[1][3], hv[3], lv[3]);
+        phi = u32x4{hv[0], hv[1], hv[2], hv[3]};
+        plo = u32x4{lv[0], lv[1], lv[2], lv[3]};
+    }
+
+    // V^T fragments of the sub-tile: per d tile two transposing reads give keys
+    // 4 lj .. + 4 and 16 + 4 lj .. + 4 of dim 16 dt + lq.
+    __device__ inline void read_v(const char* Vs, v8 (&vf)[DT]) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vs + voff[dt]));
+            const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vs + voff[dt] + 16 * D * 2));
+            vf[dt] = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    }
+
+    // O_t^T += V^T P_t^T and the row sums.
+    __device__ inline void pv(int t, const v8 (&vf)[DT], const u32x4& phi, const u32x4& plo) {
+        const v8 bh = __builtin_bit_cast(v8, phi), bl = __builtin_bit_cast(v8, plo);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            o[t][dt] = M::mma(vf[dt], bh, o[t][dt]);
+            if (HILO) o[t][dt] = M::mma(vf[dt], bl, o[t][dt]);
+        }
+        lsum[t] = M::mma(ones, bh, lsum[t]);
+        if (HILO) lsum[t] = M::mma(ones, bl, lsum[t]);
+    }
+
+    // PV(0) with P(1) interleaved in source order: after the two MFMAs of each
+    // d tile one probability of head 1 is computed (and, every other tile, a
+    // pair is split), so the VALU work issues while the MFMAs execute.
+    __device__ inline void pv0_probs1(const v8 (&vf)[DT], const u32x4& h0, const u32x4& l0, float (&x1)[2][4],
+                                      float scale_log2, u32x4& h1, u32x4& l1) {
+        const v8 bh = __builtin_bit_cast(v8, h0), bl = __builtin_bit_cast(v8, l0);
+        const float m_use = (m_run[1] == -INFINITY) ? 0.f : m_run[1];
+        float p[8];
+        uint32_t hv[4], lv[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            o[0][dt] = M::mma(vf[dt], bh, o[0][dt]);
+            if (HILO) o[0][dt] = M::mma(vf[dt], bl, o[0][dt]);
+            if (dt < 8) {
+                p[dt] = __builtin_amdgcn_exp2f(__builtin_fmaf(x1[dt >> 2][dt & 3], scale_log2, -m_use));
+                if (dt & 1) pack(p[dt - 1], p[dt], hv[dt >> 1], lv[dt >> 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (DT < 8) {  // head_dim 64: the remaining probabilities
+#pragma unroll
+            for (int e = DT; e < 8; ++e) {
+                p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x1[e >> 2][e & 3], scale_log2, -m_use));
+                if (e & 1) pack(p[e - 1], p[e], hv[e >> 1], lv[e >> 1]);
+            }
+        }
+        lsum[0] = M::mma(ones, bh, lsum[0]);
+        if (HILO) lsum[0] = M::mma(ones, bl, lsum[0]);
+        h1 = u32x4{hv[0], hv[1], hv[2], hv[3]};
+        l1 = u32x4{lv[0], lv[1], lv[2], lv[3]};
+    }
+
+    // One 32-key sub-tile (Ks / Vs: its first staged K / V row) for both heads,
+    // software-pipelined over the two heads so the MFMA work of one overlaps the
+    // softmax of the other, each K and V fragment read once for both:
+    //   read V, K;  QK(0);  QK(1);  [mask];  max, rescale (0, 1);  P(0);
+    //   PV(0) || P(1);  PV(1)
+    // MFMAs run asynchronously, so VALU work issued between them overlaps them;
+    // the scheduling barriers keep this order.
+    // mask: some key may lie beyond some row's position (wave-uniform).
+    __device__ inline void step(const char* Ks, const char* Vs, bool mask, int32_t key0, int lj, float scale_log2) {
+        f32x4 s0[2], s1[2];
+        float x0[2][4], x1[2][4];
+        u32x4 h0, l0, h1, l1;
+        v8 vf[DT];
+        {
+            v8 kf[DS][2];
+            read_v(Vs, vf);
+            read_k(Ks, kf);
+            __builtin_amdgcn_sched_barrier(0);
+            qk(0, kf, s0);
+            qk(1, kf, s1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (mask) {
+            apply_mask(s0, key0, lj);
+            apply_mask(s1, key0, lj);
+        }
+        rescale_if(0, row_max(s0, scale_log2, x0));
+        rescale_if(1, row_max(s1, scale_log2, x1));
+        probs(0, x0, scale_log2, h0, l0);
+        __builtin_amdgcn_sched_barrier(0);
+        pv0_probs1(vf, h0, l0, x1, scale_log2, h1, l1);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(1, vf, h1, l1);
+    }
+};
+
+template <typename T, int D, int RT, bool HILO>
+__global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
+    using C = PairCfg<D>;
+    using W = PairWave<T, D, HILO>;
+    using v8 = typename W::v8;
+    constexpr int X = 8 / (2 * RT);  // key classes per head pair
+    constexpr int GR = kRowTile * RT;
+    extern __shared__ __align__(16) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lq = lane & 15;
+    const int lj = lane >> 4;
+    const int hp = wave & 1;              // head pair of the block's four query heads
+    const int rt = (wave >> 1) % RT;      // row tile within the group
+    const int kq = (wave >> 1) / RT;      // key class
+
+    const int work = blockIdx.y;
+    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int grp = wk[0];
+    const int32_t key_begin = wk[2];
+    const int32_t key_end = wk[3];
+    const int n_chunks = group_table(a.sched)[2 * grp + 1];
+    const int kv_head = blockIdx.x / a.n_head_groups;
+    const int hg = blockIdx.x - kv_head * a.n_head_groups;
+    const int head0 = kv_head * a.group + hg * 4 + 2 * hp;
+    const int64_t row0 = static_cast<int64_t>(grp) * GR + kRowTile * rt;
+
+    const char* kbase = a.k + (static_cast<int64_t>(kv_head) * a.ks[0] + static_cast<int64_t>(key_begin) * a.ks[1]) * 2;
+    const char* vbase = a.v + (static_cast<int64_t>(kv_head) * a.vs[0] + static_cast<int64_t>(key_begin) * a.vs[1]) * 2;
+    const int32_t n_keys_chunk = key_end - key_begin;
+    const int n_sub = (n_keys_chunk + kPairSub - 1) / kPairSub;
+    const int n_it = (n_keys_chunk + kPairStepKeys - 1) / kPairStepKeys;
+
+    // Direct global -> LDS loads of step i into stage buffer `stage`: each load
+    // instruction of a wave fills 1 KB of LDS (64 lanes x 16 bytes, lane order);
+    // lane L of block b writes swizzled position (row, c') = divmod(64 b + L, D/8)
+    // and so loads piece c' ^ (row mod D/8) of that key row. Rows past the chunk
+    // end re-read its last row (in bounds); they are masked or zeroed later.
+    auto load = [&](int i, char* stage) {
+        const int32_t base = kPairStepKeys * i;
+#pragma unroll
+        for (int p = 0; p < C::loads; ++p) {
+            const int b = p * 8 + wave;                    // 1 KB block of the tensor
+            const int idx = 64 * b + lane;
+            const int row = idx / C::c8;
+            const int32_t key = min(base + row, n_keys_chunk - 1);
+            const int64_t koff = static_cast<int64_t>(key) * a.ks[1] + 8 * ((idx % C::c8) ^ C::kswz(row));
+            const int64_t voff = static_cast<int64_t>(key) * a.vs[1] + 8 * ((idx % C::c8) ^ C::vswz(row));
+            lds_dma16(kbase + koff * 2, stage + b * 1024);
+            lds_dma16(vbase + voff * 2, stage + C::tensor_bytes + b * 1024);
+        }
+    };
+
+    W w;
+    int32_t kmax, nomask_end;
+    {
+        const int64_t row = row0 + lq;
+        kmax = rows_kmax(a, row0, kRowTile);
+        nomask_end = (row0 + kRowTile <= a.n_sel) ? static_cast<int32_t>(a.positions[row0] + 1) : 0;
+        w.pos = (row < a.n_sel) ? static_cast<int32_t>(a.positions[row]) : -1;
+        w.init(lq, lj);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int ds = 0; ds < W::DS; ++ds) {
+                u32x4 raw = {0u, 0u, 0u, 0u};
+                if (row < a.n_sel) {
+                    const int64_t off = (head0 + t) * a.qs[0] + row * a.qs[1] + (32 * ds + 8 * lj);
+                    raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
+                }
+                // consume the loaded fragment here: the wait for it then sits in
+                // the prologue, not inside the loop, where a vmcnt wait would
+                // also stall on the next stage's loads
+                asm volatile("" : "+v"(raw));
+                w.qf[t][ds] = __builtin_bit_cast(v8, raw);
+            }
+        }
+    }
+
+    if (n_it > 0) load(0, smem);
+    for (int i = 0; i < n_it; ++i) {
+        char* stage = smem + (i & 1) * C::stage_bytes;
+        // stage i has landed (this wave's loads) and every wave is past step i - 1,
+        // so stage (i + 1) & 1 is free for the next loads
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int32_t left = n_keys_chunk - kPairStepKeys * i;
+        if (left < kPairStepKeys) {
+            // the chunk ends inside this step: zero the V rows past its end (their
+            // probabilities are 0, and 0 * V must stay 0 whatever V holds there)
+            for (int e = tid; e < (kPairStepKeys - left) * C::c8; e += kPairThreads)
+                *reinterpret_cast<u32x4*>(stage + C::tensor_bytes + left * D * 2 + 16 * e) = u32x4{0u, 0u, 0u, 0u};
+            __syncthreads();
+        }
+        if (i + 1 < n_it) load(i + 1, smem + ((i + 1) & 1) * C::stage_bytes);
+        const char* Ks = stage;
+        const char* Vs = stage + C::tensor_bytes;
+#pragma unroll 1
+        for (int j = kq; j < kPairSubs; j += X) {
+            const int s = kPairSubs * i + j;
+            const int32_t key0 = key_begin + kPairSub * s;
+            if (s < n_sub && key0 < kmax)
+                w.step(Ks + kPairSub * j * D * 2, Vs + kPairSub * j * D * 2, key0 + kPairSub > nomask_end, key0, lj,
+                       a.scale_log2);
+        }
+    }
+
+    // ---- row sums: row 0 of the sum tile, i.e. element 0 of lane lq (lj = 0);
+    // the other lanes hold zeros, so the sum over the lane groups broadcasts it ----
+    float l_run[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        float l = w.lsum[t][0];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        l_run[t] = l;
+    }
+    // ---- combine the X key classes of each (head pair, row tile) in LDS ----
+    if (X > 1) {
+        constexpr int kX = 2 * (W::DT * 4 + 2);  // exchanged floats per lane: O, m, l of both heads
+        __syncthreads();  // every wave is done with the K/V stages
+        if (kq > 0) {
+            float* xch = reinterpret_cast<float*>(smem) + ((hp * RT + rt) * (X - 1) + kq - 1) * kX * 64;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int dt = 0; dt < W::DT; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xch[((t * W::DT + dt) * 4 + e) * 64 + lane] = w.o[t][dt][e];
+                xch[(2 * W::DT * 4 + 2 * t) * 64 + lane] = w.m_run[t];
+                xch[(2 * W::DT * 4 + 2 * t + 1) * 64 + lane] = l_run[t];
+            }
+        }
+        __syncthreads();
+        if (kq > 0) return;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float mb[X > 1 ? X - 1 : 1], lb[X > 1 ? X - 1 : 1];
+            float m = w.m_run[t];
+#pragma unroll
+            for (int c = 0; c < X - 1; ++c) {
+                const float* xch = reinterpret_cast<const float*>(smem) + ((hp * RT + rt) * (X - 1) + c) * kX * 64;
+                mb[c] = xch[(2 * W::DT * 4 + 2 * t) * 64 + lane];
+                lb[c] = xch[(2 * W::DT * 4 + 2 * t + 1) * 64 + lane];
+                m = fmaxf(m, mb[c]);
+            }
+            if (m == -INFINITY) continue;  // no key of the chunk is visible to this row
+            const float fa = __builtin_amdgcn_exp2f(w.m_run[t] - m);  // exp2(-inf) = 0 for an empty class
+            float l = l_run[t] * fa;
+#pragma unroll
+            for (int dt = 0; dt < W::DT; ++dt) w.o[t][dt] *= fa;
+#pragma unroll
+            for (int c = 0; c < X - 1; ++c) {
+                const float* xch = reinterpret_cast<const float*>(smem) + ((hp * RT + rt) * (X - 1) + c) * kX * 64;
+                const float fb = __builtin_amdgcn_exp2f(mb[c] - m);
+                l += lb[c] * fb;
+#pragma unroll
+                for (int dt = 0; dt < W::DT; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w.o[t][dt][e] += xch[((t * W::DT + dt) * 4 + e) * 64 + lane] * fb;
+            }
+            w.m_run[t] = m;
+            l_run[t] = l;
+        }
+    }
+
+    // ---- output (one chunk) or the chunk's partial ----
+    const int r = kRowTile * rt + lq;  // row within the group
+    const int64_t row = row0 + lq;
+    if (kmax <= key_begin || row >= a.n_sel) return;  // the tile does not attend into this chunk
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int q_head = head0 + t;
+        if (n_chunks == 1) {
+            const float inv = 1.f / l_run[t];
+            uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + q_head * a.os[0] + row * a.os[1];
+#pragma unroll
+            for (int dt = 0; dt < W::DT; ++dt) {
+                uint16_t e[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) e[i] = elem<T>::from_float(w.o[t][dt][i] * inv);
+                if (a.out_vec) {
+                    *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * lj) =
+                        uint2{e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16)};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dst[(16 * dt + 4 * lj + i) * a.os[2]] = e[i];
+                }
+            }
+        } else {
+            const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * GR + r;
+            float* po = a.ws_o + slot * D;
+#pragma unroll
+            for (int dt = 0; dt < W::DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lj) = w.o[t][dt];
+            if (lj == 0) {
+                a.ws_ml[slot * 2 + 0] = w.m_run[t];
+                a.ws_ml[slot * 2 + 1] = l_run[t];
+            }
+        }
+    }
+}
+
+// ===========================================================================
 // Generic kernel (vector ALU; fp32 / fp16 / bf16, any head_dim <= 256).
 // Same work items as the MFMA kernel. 256 threads: thread t owns query
 // (tile t/64, head (t%64)/16, row t%16); K/V staged in LDS as fp32.
@@ -1036,8 +1546,28 @@ int launch_tile_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
     return launch_status();
 }
 
+template <typename T, int D, int RT, bool HILO>
+int launch_pair_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
+    constexpr size_t bytes = PairCfg<D>::bytes;
+    constexpr int X = 8 / (2 * RT);
+    static_assert(X == 1 || bytes >= static_cast<size_t>(2 * RT * (X - 1)) * 2 * (D / 16 * 4 + 2) * 64 * 4,
+                  "key-class exchange fits the stages");
+    static const bool ok = allow_lds(attn_pair_kernel<T, D, RT, HILO>, bytes);
+    if (!ok) return KVR_E_LAUNCH_FAILED;
+    attn_pair_kernel<T, D, RT, HILO><<<grid, kPairThreads, bytes, s>>>(a);
+    return launch_status();
+}
+
 template <typename T, int D>
 int launch_mfma(const AttnArgs& a, int qt, dim3 grid, hipStream_t s) {
+    if (qt == 4 && KVR_ATTN_PAIR) {
+        if (a.p_rounded) {
+            if (a.group_rows == kTileGroupRows) return launch_pair_inst<T, D, 1, false>(a, grid, s);
+            return launch_pair_inst<T, D, 4, false>(a, grid, s);
+        }
+        if (a.group_rows == kTileGroupRows) return launch_pair_inst<T, D, 1, true>(a, grid, s);
+        return launch_pair_inst<T, D, 4, true>(a, grid, s);
+    }
     if (a.group_rows == kTileGroupRows) {
         if (qt == 4) return launch_tile_inst<T, D, 4>(a, grid, s);
         if (qt == 2) return launch_tile_inst<T, D, 2>(a, grid, s);
@@ -1167,9 +1697,11 @@ void* scratch_address(void* stream) {
 
 using namespace kvr;
 
-extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_sel, int64_t n_keys, int32_t n_q_heads,
-                                          int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys,
-                                          int32_t* schedule, int64_t capacity) {
+extern "C" int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n_sel, int64_t n_keys,
+                                             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
+                                             int32_t chunk_keys, int32_t flags, int32_t* schedule, int64_t capacity) {
+    if (flags & ~KVR_ATTN_ROUNDED_PROBABILITIES) return KVR_E_INVALID_ARGUMENT;
+    const int32_t p_rounded = (flags & KVR_ATTN_ROUNDED_PROBABILITIES) ? 1 : 0;
     if (dtype_size(dtype) == 0) return KVR_E_UNSUPPORTED_DTYPE;
     if (n_sel < 0 || n_keys < 0 || n_sel > n_keys) return KVR_E_INVALID_ARGUMENT;
     if (n_keys >= (int64_t(1) << 31) - kSub || n_sel >= (int64_t(1) << 31)) return KVR_E_UNSUPPORTED_SHAPE;
@@ -1210,6 +1742,7 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
         schedule[H_NKEYS] = static_cast<int32_t>(n_keys);
         schedule[H_DTYPE] = dtype;
         schedule[H_GROUP_ROWS] = group_rows;
+        schedule[H_PROB] = p_rounded;
         return need;
     }
 
@@ -1262,7 +1795,9 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
         // every group is one chunk; the wide kernel runs two blocks per CU.
         int64_t cap = (total + per_head - 1) / per_head;
         const int64_t max_cost = *std::max_element(group_cost.begin(), group_cost.end());
-        while (group_rows == kTileGroupRows) {
+        // (The head-pair kernel also runs one block per CU in 64-row groups.)
+        const bool one_block_per_cu = group_rows == kTileGroupRows || (mfma && qt == 4 && KVR_ATTN_PAIR);
+        while (one_block_per_cu) {
             int64_t sum = 0;
             for (int64_t g = 0; g < n_groups; ++g) sum += chunks_of(g, cap);
             if (sum <= per_head || cap >= max_cost) break;
@@ -1327,6 +1862,7 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
     h[H_DTYPE] = dtype;
     h[H_MAXCHUNKS] = static_cast<int32_t>(max_chunks);
     h[H_GROUP_ROWS] = group_rows;
+    h[H_PROB] = p_rounded;
     int32_t* groups = h + kHeader;
     int32_t* works = groups + 2 * n_groups;
     for (int64_t g = 0; g < n_groups; ++g) {
@@ -1340,6 +1876,13 @@ extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_se
         works[kWorkInts * w + 3] = chunks[w].end;
     }
     return need;
+}
+
+extern "C" int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_sel, int64_t n_keys, int32_t n_q_heads,
+                                          int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys,
+                                          int32_t* schedule, int64_t capacity) {
+    return kvr_attention_schedule_ex(positions, n_sel, n_keys, n_q_heads, n_kv_heads, head_dim, dtype, chunk_keys, 0,
+                                     schedule, capacity);
 }
 
 extern "C" int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_t schedule_len, int32_t n_q_heads,
@@ -1381,6 +1924,7 @@ int attention_call(const void* q, const void* k, const void* v, void* out, const
     if (schedule_len != kHeader + 2 * static_cast<int64_t>(hs[H_NGROUPS]) + kWorkInts * static_cast<int64_t>(hs[H_NWORK]))
         return KVR_E_BAD_SCHEDULE;
     if (hs[H_MAXCHUNKS] > kMaxChunksPerGroup || hs[H_NWORK] <= 0 || hs[H_NWORK] > 65535) return KVR_E_BAD_SCHEDULE;
+    if (hs[H_PROB] != 0 && hs[H_PROB] != 1) return KVR_E_BAD_SCHEDULE;
     const int64_t ws_need = kvr_attention_workspace_bytes(hs, schedule_len, n_q_heads, head_dim);
     if (ws_need < 0) return KVR_E_BAD_SCHEDULE;
     if (scratch_limit > 0) {
@@ -1416,6 +1960,7 @@ int attention_call(const void* q, const void* k, const void* v, void* out, const
     a.n_groups = hs[H_NGROUPS];
     a.n_work = hs[H_NWORK];
     a.group_rows = hs[H_GROUP_ROWS];
+    a.p_rounded = hs[H_PROB];
     a.head_dim = head_dim;
     a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
     if (ws_need > 0) {

@@ -17,6 +17,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libkvrepair.so"
 ABI_VERSION = 1
 
+ATTN_ROUNDED_PROBABILITIES = 1  # kvr_attention_schedule_ex flag (include/kvrepair.h)
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
@@ -118,6 +119,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.kvr_attention_schedule.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _i32p, ctypes.c_int64]
     lib.kvr_attention_schedule.restype = ctypes.c_int64
+    lib.kvr_attention_schedule_ex.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                              ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _i32p,
+                                              ctypes.c_int64]
+    lib.kvr_attention_schedule_ex.restype = ctypes.c_int64
     lib.kvr_attention_workspace_bytes.argtypes = [_i32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]
     lib.kvr_attention_workspace_bytes.restype = ctypes.c_int64
     lib.kvr_packed_causal_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32,

@@ -152,9 +152,14 @@ class DeviceIndexedPlan:
         return self.positions.device
 
     def attention_schedule(self, n_q_heads: int, n_kv_heads: int, head_dim: int, dtype: torch.dtype,
-                           chunk_keys: int = 0):
-        """(host int32 array, device int32 tensor) work schedule for these shapes."""
-        key = (int(n_q_heads), int(n_kv_heads), int(head_dim), dtype, int(chunk_keys))
+                           chunk_keys: int = 0, rounded: bool = False):
+        """(host int32 array, device int32 tensor) work schedule for these shapes.
+
+        rounded=True permits the kernel to round each softmax probability to
+        the input dtype before the PV product (the SDPA precision the packed
+        executor replaces); the default keeps them as a hi + lo pair.
+        """
+        key = (int(n_q_heads), int(n_kv_heads), int(head_dim), dtype, int(chunk_keys), bool(rounded))
         cached = self._schedules.get(key)
         if cached is not None:
             host, dev, version = cached
@@ -164,11 +169,12 @@ class DeviceIndexedPlan:
         lib = _native.lib()
         pos = _native.i64_array(self.host_plan.positions)
         args = (pos, self.selected_count, self.logical_length, int(n_q_heads), int(n_kv_heads), int(head_dim),
-                _native.DTYPE_CODES[dtype], int(chunk_keys))
-        need = lib.kvr_attention_schedule(*args, None, 0)
-        _native.check(int(need), "kvr_attention_schedule")
+                _native.DTYPE_CODES[dtype], int(chunk_keys),
+                _native.ATTN_ROUNDED_PROBABILITIES if rounded else 0)
+        need = lib.kvr_attention_schedule_ex(*args, None, 0)
+        _native.check(int(need), "kvr_attention_schedule_ex")
         host = (ctypes.c_int32 * int(need))()
-        _native.check(int(lib.kvr_attention_schedule(*args, host, int(need))), "kvr_attention_schedule")
+        _native.check(int(lib.kvr_attention_schedule_ex(*args, host, int(need))), "kvr_attention_schedule_ex")
         with torch.cuda.device(self.device), torch.inference_mode(False):
             dev = _upload(torch.frombuffer(host, dtype=torch.int32), self.device)
         self._schedules[key] = (host, dev, dev._version)

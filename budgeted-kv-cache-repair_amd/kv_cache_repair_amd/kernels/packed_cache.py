@@ -637,7 +637,10 @@ class _PackedLayer(DynamicLayer):
 
 def _launcher(device_plan: DeviceIndexedPlan, config, key: torch.Tensor) -> _Launcher:
     q_heads, kv_heads, dim = int(config.num_attention_heads), int(key.shape[1]), int(key.shape[3])
-    host, dev = device_plan.attention_schedule(q_heads, kv_heads, dim, key.dtype)
+    # the reference executor's SDPA rounds probabilities to the 16-bit input
+    # dtype before PV (packed_cache.py:60-67); this path keeps that precision
+    rounded = key.dtype in (torch.bfloat16, torch.float16)
+    host, dev = device_plan.attention_schedule(q_heads, kv_heads, dim, key.dtype, rounded=rounded)
     ws_bytes = int(_native.lib().kvr_attention_workspace_bytes(host, len(host), q_heads, dim))
     _native.check(ws_bytes, "kvr_attention_workspace_bytes")
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=key.device) if ws_bytes else None

@@ -365,6 +365,22 @@ int64_t kvr_attention_schedule(const int64_t* positions, int64_t n_sel, int64_t 
                                int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys,
                                int32_t* schedule, int64_t capacity);
 
+/*
+ * kvr_attention_schedule with flags. KVR_ATTN_ROUNDED_PROBABILITIES lets the
+ * attention round each softmax probability to the input dtype before the PV
+ * product, as the SDPA path of the reference packed executor
+ * (packed_cache.py:60-67, transformers' sdpa_attention_forward) rounds it; the
+ * packed executor builds its schedules this way. Without it (flags 0, what
+ * kvr_attention_schedule builds) probabilities enter PV as a hi + lo pair of
+ * 16-bit values, the fp32-class precision of the reference Triton operator
+ * (_indexed_triton.py:54-58). The flag permits rounding; kernels that do not
+ * implement it keep the pair.
+ */
+#define KVR_ATTN_ROUNDED_PROBABILITIES 1
+int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n_sel, int64_t n_keys, int32_t n_q_heads,
+                                  int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t chunk_keys, int32_t flags,
+                                  int32_t* schedule, int64_t capacity);
+
 /* Workspace bytes kvr_packed_causal_attention needs for a schedule (host-only). */
 int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_t schedule_len, int32_t n_q_heads,
                                       int32_t head_dim);

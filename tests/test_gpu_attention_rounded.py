@@ -1,0 +1,138 @@
+"""The packed executor's attention, which rounds each softmax probability to the
+16-bit input dtype before the PV product as the SDPA call it replaces does
+(reference packed_cache.py:60-67 -> transformers sdpa_attention_forward).
+
+Three results on the same seeded inputs: the executor's kernel (schedule built
+with KVR_ATTN_ROUNDED_PROBABILITIES), the reference path (HF sdpa with the
+reference's boolean packed mask, in the same 16-bit dtype) and a float64
+control (the same SDPA on the inputs upcast exactly). The gate is the
+reference's precision floor (tests/test_packed_cache.py:291-315): our max-abs
+and RMSE error against the control at most twice the reference path's, with
+an epsilon floor. Independently of SDPA, a bound the rounding fixes: a
+probability rounded to nearest carries relative error <= u (unit roundoff,
+2^-8 bf16, 2^-11 fp16), so the normalised output sum p v / sum p moves by at
+most u max|v - o| / (1 - u) <= 2u max|v| per row; in fp16 a probability below
+2^-14 is subnormal and rounds with absolute error <= 2^-25 against a sum of at
+least 1, adding n 2^-25 max|v|; plus the output's own rounding. The kernel must
+stay inside that bound against the fp64 oracle where the oracle finishes in
+seconds.
+"""
+
+from __future__ import annotations
+
+import random
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+UNIT = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+SUBNORMAL_HALF_STEP = {torch.bfloat16: 0.0, torch.float16: 2.0 ** -25}  # bf16's, 2^-134, is negligible
+CODE = {torch.float16: orc.F16, torch.bfloat16: orc.BF16}
+
+
+def c3_support():
+    slots = random.Random(2).sample(range(5632 // 8), 16)
+    return sorted(p for s in slots for p in range(2048 + 8 * s, 2048 + 8 * s + 4))
+
+
+def c4_support():
+    rng = random.Random(4)
+    starts = sorted(rng.sample(range(2048, 32768 - 64, 64), 32))
+    rows = set()
+    for s in starts:
+        rows.update(range(s, s + rng.randint(24, 60)))
+    return sorted(rows)
+
+
+# (name, q heads, kv heads, head_dim, keys, positions)
+CASES = [
+    ("c2", 32, 8, 128, 1920, list(range(928, 992))),
+    ("c3", 32, 8, 128, 7680, c3_support()),
+    ("wide-64", 16, 4, 64, 6000, sorted(random.Random(7).sample(range(6000), 300))),
+    ("c4-rows64", 32, 8, 128, 32768, c4_support()),
+]
+
+
+def executor_attention(q, k, v, positions):
+    """q [1, Hq, R, D]; returns [1, R, Hq, D] from the packed executor's path."""
+    from kv_cache_repair_amd.kernels.indexed_attention import IndexedPlan
+    from kv_cache_repair_amd.kernels.packed_cache import _launcher, _packed_attention, _PackedContext
+
+    plan = IndexedPlan(positions, k.shape[2]).to(q.device)
+    launcher = _launcher(plan, SimpleNamespace(num_attention_heads=q.shape[1]), k)
+    assert launcher.host_schedule[17] == 1  # the executor asked for rounded probabilities
+    context = _PackedContext(plan.positions, k.shape[2], "hip", plan, launcher)
+    module = SimpleNamespace(num_key_value_groups=q.shape[1] // k.shape[1], is_causal=True)
+    out, weights = _packed_attention(module, q, k, v, None, sur_packed_context=context)
+    assert weights is None
+    return out
+
+
+def sdpa(q, k, v, positions, scale):
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+    pos = torch.tensor(positions, device=q.device)
+    mask = (torch.arange(k.shape[2], device=q.device)[None, :] <= pos[:, None])[None, None]
+    module = SimpleNamespace(num_key_value_groups=q.shape[1] // k.shape[1], is_causal=True)
+    out, _ = sdpa_attention_forward(module, q, k, v, mask, dropout=0.0, scaling=scale, is_causal=False)
+    return out
+
+
+def errors(actual, control):
+    d = actual.double() - control
+    return d.abs().max().item(), d.pow(2).mean().sqrt().item()
+
+
+def inputs(device, hq, hkv, dim, n, rows, dtype, seed):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(1, hq, rows, dim, device=device, generator=gen).to(dtype)
+    k = torch.randn(1, hkv, n, dim, device=device, generator=gen).to(dtype)
+    v = torch.randn(1, hkv, n, dim, device=device, generator=gen).to(dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_executor_attention_within_the_sdpa_precision_floor(gpu_device, case, dtype):
+    name, hq, hkv, dim, n, positions = case
+    print(f"rounded attention {name} {dtype} rows={len(positions)} keys={n}", flush=True)
+    q, k, v = inputs(gpu_device, hq, hkv, dim, n, len(positions), dtype, seed=11)
+    scale = dim ** -0.5
+    ours = executor_attention(q, k, v, positions)
+    theirs = sdpa(q, k, v, positions, scale)
+    control = sdpa(q.double(), k.double(), v.double(), positions, scale)
+    assert ours.shape == theirs.shape == (1, len(positions), hq, dim) and torch.isfinite(ours).all()
+    ours_max, ours_rmse = errors(ours, control)
+    ref_max, ref_rmse = errors(theirs, control)
+    floor = UNIT[dtype] / 8
+    print(f"  ours max {ours_max:.3e} rmse {ours_rmse:.3e} | sdpa max {ref_max:.3e} rmse {ref_rmse:.3e}", flush=True)
+    assert ours_max <= 2.0 * max(ref_max, floor)
+    assert ours_rmse <= 2.0 * max(ref_rmse, floor / 8)
+    del control
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", CASES[:3], ids=[c[0] for c in CASES[:3]])
+def test_executor_attention_within_the_rounding_bound_of_the_fp64_oracle(gpu_device, case, dtype):
+    name, hq, hkv, dim, n, positions = case
+    q, k, v = inputs(gpu_device, hq, hkv, dim, n, len(positions), dtype, seed=5)
+    ours = executor_attention(q, k, v, positions)[0].transpose(0, 1).double().cpu()  # [Hq, R, D]
+
+    def bits(t):
+        return t[0].detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    exact = torch.from_numpy(orc.attention_f64(bits(q), bits(k), bits(v), positions, CODE[dtype], dim ** -0.5))
+    u = UNIT[dtype]
+    vmax = v.abs().amax(dim=(2, 3)).double().cpu().repeat_interleave(hq // hkv)[:, None, None]  # per query head
+    # probabilities as above; QK^T and the exponent in fp32 add a few fp32 ulp of
+    # the scores, far below u; the output's rounding to the dtype adds u |out|
+    bound = (2 * u + n * SUBNORMAL_HALF_STEP[dtype]) * vmax + u * exact.abs() + 1e-6
+    excess = (ours - exact).abs() - bound
+    assert excess.max().item() <= 0, f"{name}: worst excess {excess.max().item():.3e}"

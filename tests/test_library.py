@@ -23,8 +23,8 @@ def declared_symbols() -> list[str]:
 def test_header_declares_the_entry_points():
     assert declared_symbols() == sorted([
         "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
-        "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_workspace_bytes",
-        "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
+        "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_attention_schedule", "kvr_attention_schedule_ex",
+        "kvr_attention_workspace_bytes", "kvr_packed_causal_attention", "kvr_rms_norm", "kvr_silu_mul", "kvr_linear", "kvr_linear_splits",
         "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
         "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance", "kvr_packed_causal_attention_noalloc",
@@ -166,14 +166,14 @@ def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
     (list(range(0, 40000, 37)), 40000, 0), ([7], 8, 0)])
 def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_keys, chunk):
     s = schedule(positions, n_keys, 32, 8, 128, chunk=chunk)
-    header, n_groups, longest, n_work, rows = s[:17], s[3], s[4], s[5], s[16]
-    assert header[0] == 0x4B565253 and header[1] == 4 and header[2] == len(positions)
+    header, n_groups, longest, n_work, rows = s[:18], s[3], s[4], s[5], s[16]
+    assert header[0] == 0x4B565253 and header[1] == 5 and header[17] == 0 and header[2] == len(positions)
     # 16-row groups (tile kernel) while 64-row groups x 8 heads would fill at most half of 256 blocks
     assert rows == (16 if 2 * 8 * ((len(positions) + 63) // 64) <= 256 else 64)
     assert n_groups == (len(positions) + rows - 1) // rows
-    assert len(s) == 17 + 2 * n_groups + 4 * n_work
-    groups = [(s[17 + 2 * g], s[18 + 2 * g]) for g in range(n_groups)]
-    work = [tuple(s[17 + 2 * n_groups + 4 * w:21 + 2 * n_groups + 4 * w]) for w in range(n_work)]
+    assert len(s) == 18 + 2 * n_groups + 4 * n_work
+    groups = [(s[18 + 2 * g], s[19 + 2 * g]) for g in range(n_groups)]
+    work = [tuple(s[18 + 2 * n_groups + 4 * w:22 + 2 * n_groups + 4 * w]) for w in range(n_work)]
     assert len(work) == n_work == sum(c for _, c in groups) and header[15] == max(c for _, c in groups)
     assert longest == max(e - b for _, _, b, e in work)
     for g, (base, count) in enumerate(groups):
@@ -206,8 +206,8 @@ def test_default_chunking_keeps_one_block_per_cu_for_the_c3_support():
     assert 24 * 8 <= n_work * 8 <= 256
     # chunks are cost balanced: one row tile per group, so every chunk carries about
     # the same number of keys (whole 64-key sub-tiles, the group's last one shorter)
-    work = [tuple(s[17 + 2 * n_groups + 4 * w:21 + 2 * n_groups + 4 * w]) for w in range(n_work)]
-    lengths = [e - b for g, c, b, e in work if c + 1 < s[18 + 2 * g]]  # all but each group's last chunk
+    work = [tuple(s[18 + 2 * n_groups + 4 * w:22 + 2 * n_groups + 4 * w]) for w in range(n_work)]
+    lengths = [e - b for g, c, b, e in work if c + 1 < s[19 + 2 * g]]  # all but each group's last chunk
     assert max(lengths) - min(lengths) <= 64
     # a group that fits one block's share is never split
     s = schedule(list(range(15104)), 16128, 32, 8, 128)
@@ -288,6 +288,29 @@ def test_decoder_layer_descriptors_validate_before_any_launch():
     assert lib.kvr_decoder_forward(C.byref(layer), -1, C.byref(d), None, None) == -1
 
 
+def test_schedule_flags_record_the_probability_precision():
+    """kvr_attention_schedule_ex writes the rounded-probability permission into
+    the header and is otherwise the same schedule; unknown flags are refused."""
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    positions = list(range(100, 228))
+    pos = _native.i64_array(positions)
+    plain = schedule(positions, 300, 32, 8, 128)
+    for flags, expected in ((0, 0), (_native.ATTN_ROUNDED_PROBABILITIES, 1)):
+        need = lib.kvr_attention_schedule_ex(pos, len(positions), 300, 32, 8, 128, 2, 0, flags, None, 0)
+        assert need == len(plain)
+        buf = (ctypes.c_int32 * need)()
+        assert lib.kvr_attention_schedule_ex(pos, len(positions), 300, 32, 8, 128, 2, 0, flags, buf, need) == need
+        assert buf[17] == expected
+        assert list(buf[:17]) + list(buf[18:]) == plain[:17] + plain[18:]
+    for bad in (2, -1, 1 << 30):
+        assert lib.kvr_attention_schedule_ex(pos, len(positions), 300, 32, 8, 128, 2, 0, bad, None, 0) == -1
+    empty = _native.i64_array([0])
+    buf = (ctypes.c_int32 * 18)()
+    assert lib.kvr_attention_schedule_ex(empty, 0, 100, 32, 8, 128, 2, 0, 1, buf, 18) == 18 and buf[17] == 1
+
+
 def test_empty_selection_gives_a_header_only_schedule():
     """n_sel == 0 is valid (an empty support): a schedule with no groups and no
     work, whose workspace is zero bytes, whatever chunk size is asked for."""
@@ -297,7 +320,7 @@ def test_empty_selection_gives_a_header_only_schedule():
     empty = _native.i64_array([0])
     for chunk in (0, 64, 256):
         need = lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, chunk, None, 0)
-        assert need == 17
+        assert need == 18
         buf = (ctypes.c_int32 * need)()
         assert lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, chunk, buf, need) == need
         assert (buf[2], buf[3], buf[5]) == (0, 0, 0)  # rows, groups, work items
