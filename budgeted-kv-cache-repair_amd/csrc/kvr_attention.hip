@@ -1078,33 +1078,51 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
         }
     };
 
+    // Prologue, one round trip: the row positions and Q fragments are loaded
+    // (unconditionally, from rows clamped into range; n_sel >= 1 whenever a
+    // work item exists), then the first stage's K/V loads are issued, then all
+    // of them are waited for at once. Consuming the values through the empty
+    // asm below keeps the compiler's waits for them here, not inside the loop,
+    // where a vmcnt wait would also stall on the next stage's loads.
     W w;
     int32_t kmax, nomask_end;
     {
         const int64_t row = row0 + lq;
-        kmax = rows_kmax(a, row0, kRowTile);
-        nomask_end = (row0 + kRowTile <= a.n_sel) ? static_cast<int32_t>(a.positions[row0] + 1) : 0;
-        w.pos = (row < a.n_sel) ? static_cast<int32_t>(a.positions[row]) : -1;
-        w.init(lq, lj);
+        const int64_t last_sel = a.n_sel - 1;
+        const int64_t row_c = row < last_sel ? row : last_sel;
+        const int64_t tile_last = row0 + kRowTile - 1 < last_sel ? row0 + kRowTile - 1 : last_sel;
+        const int64_t tile_first = row0 < last_sel ? row0 : last_sel;
+        // positions are below n_keys < 2^31: their low words (little-endian)
+        const int32_t* pos32 = reinterpret_cast<const int32_t*>(a.positions);
+        int32_t pos_raw = pos32[2 * row_c];
+        int32_t kmax_raw = pos32[2 * tile_last];
+        int32_t first_raw = pos32[2 * tile_first];
+        u32x4 raw[2][W::DS];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int ds = 0; ds < W::DS; ++ds) {
-                u32x4 raw = {0u, 0u, 0u, 0u};
-                if (row < a.n_sel) {
-                    const int64_t off = (head0 + t) * a.qs[0] + row * a.qs[1] + (32 * ds + 8 * lj);
-                    raw = *reinterpret_cast<const u32x4*>(a.q + off * 2);
-                }
-                // consume the loaded fragment here: the wait for it then sits in
-                // the prologue, not inside the loop, where a vmcnt wait would
-                // also stall on the next stage's loads
-                asm volatile("" : "+v"(raw));
-                w.qf[t][ds] = __builtin_bit_cast(v8, raw);
+                const int64_t off = (head0 + t) * a.qs[0] + row_c * a.qs[1] + (32 * ds + 8 * lj);
+                raw[t][ds] = *reinterpret_cast<const u32x4*>(a.q + off * 2);
             }
-        }
+        if (n_it > 0) load(0, smem);
+        asm volatile("" : "+v"(pos_raw), "+v"(kmax_raw), "+v"(first_raw));
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ds = 0; ds < W::DS; ++ds) asm volatile("" : "+v"(raw[t][ds]));
+        const bool live_row = row < a.n_sel;
+        kmax = row0 < a.n_sel ? kmax_raw + 1 : 0;
+        nomask_end = (row0 + kRowTile <= a.n_sel) ? first_raw + 1 : 0;
+        w.pos = live_row ? pos_raw : -1;
+        w.init(lq, lj);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ds = 0; ds < W::DS; ++ds)
+                w.qf[t][ds] = __builtin_bit_cast(v8, live_row ? raw[t][ds] : u32x4{0u, 0u, 0u, 0u});
     }
 
-    if (n_it > 0) load(0, smem);
     for (int i = 0; i < n_it; ++i) {
         char* stage = smem + (i & 1) * C::stage_bytes;
         // stage i has landed (this wave's loads) and every wave is past step i - 1,
