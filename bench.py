@@ -500,7 +500,8 @@ def kernel_launchers(model, workload: Workload, old, old_ids, new_ids, device):
     out["kvr_indexed_scatter_kv"] = (_checked(lib.kvr_indexed_scatter_kv, *args),
                                      2 * 2 * w.hkv * b * w.dim * esz, 0, 0)
 
-    host, dev = plan.attention_schedule(w.hq, w.hkv, w.dim, torch.bfloat16)
+    # the packed executor's schedule: probabilities rounded to bf16 before PV, as its SDPA counterpart
+    host, dev = plan.attention_schedule(w.hq, w.hkv, w.dim, torch.bfloat16, rounded=True)
     ws_bytes = int(lib.kvr_attention_workspace_bytes(host, len(host), w.hq, w.dim))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     attn_out = torch.empty(1, b, w.hq, w.dim, device=device, dtype=torch.bfloat16).permute(0, 2, 1, 3)
@@ -571,7 +572,7 @@ def measure_kernels(model, workload, old, old_ids, new_ids, device) -> dict:
     return kernels
 
 
-TRAFFIC_SUMMARIES = tuple(sorted((ROOT / "profiles").glob("*hbm_traffic*.md")))
+TRAFFIC_SUMMARIES = tuple(sorted((ROOT / "profiles").glob("*.md")))
 KERNEL_SOURCES = {"kvr_packed_causal_attention": "kvr_attention.hip", "kvr_shift_cache_build": "kvr_rotate.hip",
                   "kvr_rope_delta_rotate": "kvr_rotate.hip", "kvr_indexed_scatter_kv": "kvr_scatter.hip",
                   "kvr_rope_scatter_kv": "kvr_fresh.hip", "kvr_linear_multi": "kvr_gemm.hip"}
@@ -881,6 +882,28 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
 
 
 # ----------------------------------------------------------------------------- main
+def profile_kernels(args, workload: Workload, device) -> dict:
+    """Launch the named libkvrepair calls (kernel_launchers' names, or "all")
+    with the stage's shapes, eagerly and synchronised one by one: a short
+    program for rocprofv3 counter passes, without the stage or its checks."""
+    from kv_cache_repair_amd import _native
+
+    _native.lib()
+    model = make_model(device, workload)
+    old, old_ids, new_ids = make_request(device, workload)
+    launchers, keep = kernel_launchers(model, workload, old, old_ids, new_ids, device)
+    names = sorted(launchers) if args.profile_kernels == "all" else args.profile_kernels.split(",")
+    unknown = [n for n in names if n not in launchers]
+    if unknown:
+        raise SystemExit(f"unknown kernel(s) {unknown}; choose from {sorted(launchers)}")
+    for name in names:
+        for _ in range(args.profile_launches):
+            launchers[name][0]()
+            torch.cuda.synchronize()
+    del keep
+    return {"profiled": names, "launches_each": args.profile_launches, "workload": workload.name}
+
+
 def run_workload(args, workload: Workload, device) -> dict:
     from kv_cache_repair_amd import _native
     from kv_cache_repair_amd.cache import OperatorShim
@@ -959,6 +982,10 @@ def main(argv=None) -> int:
     parser.add_argument("--calibration-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB three times with a plain device-to-device "
                              "copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
+    parser.add_argument("--profile-kernels", default="",
+                        help="comma-separated libkvrepair calls (or 'all') to launch --profile-launches times each "
+                             "with the workload's shapes, for rocprofv3 counter passes; no stage timing")
+    parser.add_argument("--profile-launches", type=int, default=5)
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build runs on a single GPU (--gpus {args.gpus} requested). "
@@ -980,7 +1007,10 @@ def main(argv=None) -> int:
                 print(json.dumps(grid_case(model, length, count, 64, args.grid_warmups, args.grid_repeats, 71)),
                       flush=True)
         return 0
-    line = run_workload(args, WORKLOADS[args.workload], device)
+    if args.profile_kernels:
+        line = profile_kernels(args, WORKLOADS[args.workload], device)
+    else:
+        line = run_workload(args, WORKLOADS[args.workload], device)
     print(json.dumps(line), flush=True)
     if args.calibration_copy_mib > 0:
         src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=device)
