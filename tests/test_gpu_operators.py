@@ -1,9 +1,12 @@
 """GPU parity of the indexed scatter and the packed causal attention operators.
 
-Mirrors the reference operator tests (tests/test_indexed_attention.py) with
-the HIP library in place of Triton, and checks against the C oracle: the
-scatter bit for bit, attention against the fp64 dense oracle with the
-reference's frozen tolerances (bf16 atol 0.002 rtol 0.02; fp16 2.5e-4/3e-3).
+The scatter is checked bit for bit: whole storages against an expected storage
+computed through storage-index maps (see strided_views.py), against
+``index_copy_`` and against the C oracle. Attention is checked against the
+fp64 dense oracle with the reference's frozen tolerances (bf16 atol 0.002 rtol
+0.02; fp16 2.5e-4/3e-3). Vectors (positions, shapes, payload bits, the
+cancelling value channels, rejected inputs) follow the reference's
+tests/test_indexed_attention.py; the test code is this build's own.
 """
 
 from __future__ import annotations
@@ -15,10 +18,12 @@ import pytest
 import torch
 
 from oracle import oracle as orc
+from strided_views import host_bits, payload_rows, same_bits, storage_index, strided_over_storage
 
 pytestmark = pytest.mark.gpu
 
 CODE = {torch.float32: orc.F32, torch.float16: orc.F16, torch.bfloat16: orc.BF16}
+TOLERANCE = {torch.bfloat16: (0.002, 0.02), torch.float16: (0.00025, 0.003)}  # (atol, rtol), frozen
 
 
 def ops():
@@ -27,75 +32,64 @@ def ops():
     return ia
 
 
-def host_bits(t: torch.Tensor) -> np.ndarray:
-    t = t.detach().cpu()
-    if t.dtype == torch.float32:
-        return t.numpy()
-    return t.view(torch.int16).numpy().view(np.uint16)
-
-
 def oracle_attention(q, k, v, positions, scale=None):
     return orc.attention_f64(host_bits(q[0]), host_bits(k[0]), host_bits(v[0]), positions, CODE[q.dtype], scale)
 
 
 def assert_attention_close(actual, expected):
-    atol, rtol = (0.002, 0.02) if actual.dtype == torch.bfloat16 else (0.00025, 0.003)
+    atol, rtol = TOLERANCE[actual.dtype]
     assert torch.isfinite(actual).all()
     torch.testing.assert_close(actual[0].double().cpu(), torch.from_numpy(expected), atol=atol, rtol=rtol)
 
 
-def bits_equal(a, b):
-    return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
+bits_equal = same_bits
 
 
-def view(shape, dtype, layout, device):
-    _, heads, tokens, dim = shape
-    if layout == "native":
-        storage = torch.randn((1, tokens, heads, dim), device=device, dtype=dtype) * 0.5
-        return storage, storage.transpose(1, 2)
-    if layout == "holes":
-        storage = torch.randn((1, heads, 2 * tokens + 3, 2 * dim + 5), device=device, dtype=dtype) * 0.5
-        return storage, storage[:, :, 1:1 + 2 * tokens:2, 2:2 + 2 * dim:2]
-    storage = torch.randn(shape, device=device, dtype=dtype) * 0.5
-    return storage, storage
-
-
-def spread(count, length):
-    return [length - 1] if count == 1 else [i * (length - 1) // (count - 1) for i in range(count)]
+def evenly_spaced(count, length):
+    """``count`` sorted positions from 0 to length - 1 (just the last one for count 1)."""
+    if count == 1:
+        return [length - 1]
+    return [i * (length - 1) // (count - 1) for i in range(count)]
 
 
 # --------------------------------------------------------------------------- scatter
+@pytest.mark.parametrize("arrangement", [("sparse", "token_major", "token_major", "sparse"),
+                                         ("padded", "dense", "sparse", "padded")])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_scatter_preserves_entire_backings_including_holes(gpu_device, dtype):
+def test_scatter_writes_only_the_plan_rows_of_each_storage(gpu_device, dtype, arrangement):
     ia = ops()
     positions = [0, 3, 4, 8, 9, 63, 64, 129]
     plan = ia.IndexedPlan(positions, 130).to(gpu_device)
-    pairs = [view((1, 3, 130, 128), dtype, "holes", gpu_device), view((1, 3, 130, 128), dtype, "native", gpu_device),
-             view((1, 3, len(positions), 128), dtype, "native", gpu_device),
-             view((1, 3, len(positions), 128), dtype, "holes", gpu_device)]
-    snapshots = [backing.clone() for backing, _ in pairs]
-    views = [s.as_strided(v.shape, v.stride(), v.storage_offset()) for s, (_, v) in zip(snapshots, pairs)]
-    for target, source in zip(views[:2], views[2:]):
-        target.index_copy_(2, plan.positions, source)
-    ia.indexed_kv_scatter_(*(v for _, v in pairs), plan)
+    gen = torch.Generator(device=gpu_device).manual_seed(130)
+    shapes = [(1, 3, 130, 128)] * 2 + [(1, 3, len(positions), 128)] * 2
+    made = [strided_over_storage(shape, dtype, gpu_device, layout, gen) for shape, layout in zip(shapes, arrangement)]
+    storages, views = [m[0] for m in made], [m[1] for m in made]
+    expected = [st.clone() for st in storages]
+    rows = torch.tensor(positions, device=gpu_device)
+    for out, fresh in ((0, 2), (1, 3)):
+        expected[out][storage_index(views[out]).index_select(2, rows).reshape(-1)] = \
+            storages[fresh][storage_index(views[fresh]).reshape(-1)]
+    ia.indexed_kv_scatter_(*views, plan)
     torch.cuda.synchronize()
-    assert all(bits_equal(backing, expect) for (backing, _), expect in zip(pairs, snapshots))
+    assert all(same_bits(actual, want) for actual, want in zip(storages, expected))
 
 
-@pytest.mark.parametrize("dtype,payload", [(torch.float16, [0, -32768, 31744, -1024, 32257, 1]),
-                                           (torch.bfloat16, [0, -32768, 32640, -128, 32705, 1])])
-def test_scatter_is_bitwise_copy_including_nan_payloads(gpu_device, dtype, payload):
+@pytest.mark.parametrize("heads", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_scatter_moves_special_values_bit_for_bit(gpu_device, dtype, heads):
+    """Signed zeros, infinities, a NaN payload and a subnormal land unchanged at
+    rows 0, 3 and 8 of a 9-row cache; the other rows keep their zeros."""
     ia = ops()
     plan = ia.IndexedPlan([0, 3, 8], 9).to(gpu_device)
-    raw = torch.tensor(payload, dtype=torch.int16, device=gpu_device).repeat(32).reshape(1, 1, 3, 64)
-    fresh_k = raw.view(dtype)
-    fresh_v = fresh_k.clone()
-    key = torch.zeros((1, 1, 9, 64), device=gpu_device, dtype=dtype)
-    value = key.clone()
-    ia.indexed_kv_scatter_(key, value, fresh_k, fresh_v, plan)
-    assert bits_equal(key.index_select(2, plan.positions), fresh_k)
-    assert bits_equal(value.index_select(2, plan.positions), fresh_v)
-    assert torch.count_nonzero(key[:, :, [1, 2, 4, 5, 6, 7]].view(torch.int16)) == 0
+    bits = payload_rows(dtype, heads, 3, 64, gpu_device)
+    cache_k = torch.zeros(1, heads, 9, 64, device=gpu_device, dtype=dtype)
+    cache_v = torch.zeros_like(cache_k)
+    ia.indexed_kv_scatter_(cache_k, cache_v, bits.view(dtype), bits.flip(3).contiguous().view(dtype), plan)
+    torch.cuda.synchronize()
+    for cache, want in ((cache_k, bits), (cache_v, bits.flip(3))):
+        as_bits = cache.view(torch.int16)
+        assert torch.equal(as_bits[:, :, [0, 3, 8]], want)
+        assert torch.count_nonzero(as_bits[:, :, [1, 2, 4, 5, 6, 7]]) == 0
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
@@ -120,17 +114,17 @@ def test_native_scatter_matches_oracle_for_all_dtypes(gpu_device, dtype, dim):
 
 
 @pytest.mark.parametrize("length", [0, 17])
-def test_empty_plan_has_no_writes_and_empty_attention_result(gpu_device, length):
+def test_an_empty_plan_writes_nothing_and_attends_nothing(gpu_device, length):
     ia = ops()
     plan = ia.IndexedPlan([], length).to(gpu_device)
-    key = torch.randn((1, 2, length, 64), device=gpu_device, dtype=torch.float16)
-    value, saved = key.clone(), key.clone()
-    fresh = torch.empty((1, 2, 0, 64), device=gpu_device, dtype=torch.float16)
-    ia.indexed_kv_scatter_(key, value, fresh, fresh, plan)
-    result = ia.indexed_causal_attention(torch.empty((1, 4, 0, 64), device=gpu_device, dtype=key.dtype), key, value,
-                                         plan)
-    assert result.shape == (1, 4, 0, 64)
-    assert bits_equal(key, saved) and bits_equal(value, saved)
+    gen = torch.Generator(device=gpu_device).manual_seed(length)
+    cache = [torch.randn(1, 2, length, 64, device=gpu_device, generator=gen).half() for _ in range(2)]
+    kept = [c.clone() for c in cache]
+    no_rows = torch.empty(1, 2, 0, 64, device=gpu_device, dtype=torch.float16)
+    ia.indexed_kv_scatter_(*cache, no_rows, no_rows, plan)
+    out = ia.indexed_causal_attention(torch.empty(1, 4, 0, 64, device=gpu_device, dtype=torch.float16), *cache, plan)
+    assert tuple(out.shape) == (1, 4, 0, 64)
+    assert all(same_bits(c, k) for c, k in zip(cache, kept))
 
 
 # --------------------------------------------------------------------------- fused fresh-row epilogue
@@ -146,7 +140,7 @@ def rotary_tables(positions, dim, dtype, device, theta=10000.0):
     return rotary(probe, pos)
 
 
-@pytest.mark.parametrize("layout", ["contiguous", "native", "holes"])
+@pytest.mark.parametrize("layout", ["dense", "token_major", "sparse"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dim", [64, 128])
 def test_rope_scatter_matches_native_rotary_then_index_copy(gpu_device, dtype, dim, layout):
@@ -157,13 +151,13 @@ def test_rope_scatter_matches_native_rotary_then_index_copy(gpu_device, dtype, d
     positions = [0, 3, 4, 8, 9, 63, 64, 129, 200, 4000]
     n = 4001
     plan = ia.IndexedPlan(positions, n).to(gpu_device)
-    q = view((1, 8, len(positions), dim), dtype, layout, gpu_device)[1]
-    fk = view((1, 2, len(positions), dim), dtype, layout, gpu_device)[1]
-    fv = view((1, 2, len(positions), dim), dtype, layout, gpu_device)[1]
-    q.mul_(4)  # in place: the views keep their layouts
-    fk.mul_(4)
-    out_k_backing, out_k = view((1, 2, n, dim), dtype, "holes" if layout == "holes" else "contiguous", gpu_device)
-    out_v_backing, out_v = view((1, 2, n, dim), dtype, "contiguous", gpu_device)
+    gen = torch.Generator(device=gpu_device).manual_seed(dim + len(layout))
+    q = strided_over_storage((1, 8, len(positions), dim), dtype, gpu_device, layout, gen, scale=2.0)[1]
+    fk = strided_over_storage((1, 2, len(positions), dim), dtype, gpu_device, layout, gen, scale=2.0)[1]
+    fv = strided_over_storage((1, 2, len(positions), dim), dtype, gpu_device, layout, gen, scale=0.5)[1]
+    out_k_backing, out_k = strided_over_storage((1, 2, n, dim), dtype, gpu_device,
+                                                "sparse" if layout == "sparse" else "dense", gen, scale=0.5)
+    out_v_backing, out_v = strided_over_storage((1, 2, n, dim), dtype, gpu_device, "dense", gen, scale=0.5)
     ref_k_backing, ref_v_backing = out_k_backing.clone(), out_v_backing.clone()
     ref_k = ref_k_backing.as_strided(out_k.shape, out_k.stride(), out_k.storage_offset())
     ref_v = ref_v_backing.as_strided(out_v.shape, out_v.stride(), out_v.storage_offset())
@@ -407,45 +401,71 @@ def test_projection_plans_reject_what_they_cannot_serve(gpu_device):
 
 
 # --------------------------------------------------------------------------- attention
+def attention_problem(device, dtype, heads, kv_heads, rows, length, dim, layouts=("dense",) * 3, seed=0,
+                      scale=0.5):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = strided_over_storage((1, heads, rows, dim), dtype, device, layouts[0], gen, scale)[1]
+    k = strided_over_storage((1, kv_heads, length, dim), dtype, device, layouts[1], gen, scale)[1]
+    v = strided_over_storage((1, kv_heads, length, dim), dtype, device, layouts[2], gen, scale)[1]
+    return q, k, v
+
+
+# (rows, head_dim, length, heads, kv heads, layouts of q / k / v, scale or None for 1/sqrt(D))
+ORACLE_CASES = {
+    **{f"{rows}x{dim}": (rows, dim, 1025, 4, 2, ("dense",) * 3, None) for rows in (1, 15, 16, 17, 64)
+       for dim in (64, 128)},
+    "token-major, scale 0.17": (17, 128, 259, 6, 3, ("token_major", "token_major", "sparse"), 0.17),
+    "sparse, scale 0.17": (17, 128, 259, 6, 3, ("sparse", "sparse", "sparse"), 0.17),
+    "padded heads": (33, 64, 700, 8, 2, ("padded", "sparse", "padded"), None),
+}
+CUSTOM_POSITIONS = [0, 1, 63, 64, 65, 66, 71, 99, 111, 127, 128, 193, 249, 250, 255, 256, 258]
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("dim", [64, 128])
-@pytest.mark.parametrize("count", [1, 15, 16, 17, 64])
-def test_attention_matches_independent_fp64_oracle(gpu_device, count, dim, dtype):
+@pytest.mark.parametrize("case", list(ORACLE_CASES))
+def test_attention_agrees_with_the_fp64_oracle(gpu_device, case, dtype):
+    """Any layout of q/k/v (strides, storage offsets), custom scales; the inputs
+    are left untouched."""
     ia = ops()
-    torch.manual_seed(8200 + count + dim)
-    length = 1025
-    positions = spread(count, length)
+    rows, dim, length, heads, kv_heads, layouts, scale = ORACLE_CASES[case]
+    positions = CUSTOM_POSITIONS if length == 259 else evenly_spaced(rows, length)
+    q, k, v = attention_problem(gpu_device, dtype, heads, kv_heads, len(positions), length, dim, layouts,
+                                seed=8200 + rows + dim)
+    kept = [t.clone() for t in (q, k, v)]
     plan = ia.IndexedPlan(positions, length).to(gpu_device)
-    q = torch.randn((1, 4, count, dim), device=gpu_device, dtype=dtype) * 0.5
-    k = torch.randn((1, 2, length, dim), device=gpu_device, dtype=dtype) * 0.5
-    v = torch.randn_like(k) * 0.5
-    before = [t.clone() for t in (q, k, v)]
-    actual = ia.indexed_causal_attention(q, k, v, plan)
-    assert actual.shape == q.shape and actual.dtype == dtype
-    assert_attention_close(actual, oracle_attention(q, k, v, positions))
-    assert all(bits_equal(t, s) for t, s in zip((q, k, v), before))
+    actual = ia.indexed_causal_attention(q, k, v, plan, scale)
+    assert tuple(actual.shape) == tuple(q.shape) and actual.dtype == dtype
+    assert_attention_close(actual, oracle_attention(q, k, v, positions, scale))
+    assert all(same_bits(t, s) for t, s in zip((q, k, v), kept))
+
+
+def cancelling_channels(device, dtype, positions, length):
+    """Scores from two coordinates (exact in 16 bits) give nonuniform weights;
+    values alternate in sign along the keys with magnitudes 64 / 1 / 1/32 per
+    channel block, so P @ V cancels large terms (KV head 1 scaled by 1.5)."""
+    rows = torch.arange(len(positions), device=device, dtype=torch.float32)
+    keys = torch.arange(length, device=device)
+    q = torch.zeros(1, 4, len(positions), 64, device=device)
+    q[0, :, :, 0] = (1 + torch.arange(4, device=device) / 4)[:, None]
+    q[0, :, :, 1] = rows / 16 - 0.5
+    k = torch.zeros(1, 2, length, 64, device=device)
+    k[0, :, :, 0] = torch.linspace(-3, 3, length, device=device)
+    k[0, :, :, 1] = ((keys % 9).float() - 4) / 8
+    sign = 1.0 - 2.0 * (keys % 2).float()
+    magnitude = torch.cat([torch.full((16,), 64.0), torch.ones(16), torch.full((32,), 2.0 ** -5)]).to(device)
+    v = torch.outer(sign, magnitude)[None, None] * torch.tensor([1.0, 1.5], device=device)[None, :, None, None]
+    return q.to(dtype), k.to(dtype), v.to(dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_attention_with_cancelling_large_value_channels(gpu_device, dtype):
-    """Reference tests/test_indexed_attention.py:127-155: alternating +-64 value
-    channels stress P@V; probabilities must not be rounded to 16 bits."""
+    """Probabilities must not be rounded to 16 bits before P @ V (the public
+    operator's contract, as the reference Triton kernel keeps P in fp32)."""
     ia = ops()
     positions = [0, 1, 3, 7, 16, 31, 63, 64, 95, 127, 191, 255, 256]
-    plan = ia.IndexedPlan(positions, 257).to(gpu_device)
-    query = torch.zeros((1, 4, len(positions), 64), device=gpu_device, dtype=dtype)
-    key = torch.zeros((1, 2, 257, 64), device=gpu_device, dtype=dtype)
-    for head in range(4):
-        query[:, head, :, 0] = 1 + head / 4
-        query[:, head, :, 1] = torch.arange(len(positions), device=gpu_device, dtype=torch.float32) / 16 - 0.5
-    key[:, :, :, 0] = torch.linspace(-3, 3, 257, device=gpu_device, dtype=torch.float32)
-    key[:, :, :, 1] = ((torch.arange(257, device=gpu_device) % 9).float() - 4) / 8
-    signs = torch.where(torch.arange(257, device=gpu_device) % 2 == 0, 1.0, -1.0)
-    magnitude = torch.tensor([64.0] * 16 + [1.0] * 16 + [0.03125] * 32, device=gpu_device)
-    value = (signs[:, None] * magnitude[None, :]).to(dtype)[None, None].repeat(1, 2, 1, 1)
-    value[:, 1].mul_(1.5)
-    actual = ia.indexed_causal_attention(query, key, value, plan, scale=1.0)
-    assert_attention_close(actual, oracle_attention(query, key, value, positions, 1.0))
+    q, k, v = cancelling_channels(gpu_device, dtype, positions, 257)
+    actual = ia.indexed_causal_attention(q, k, v, ia.IndexedPlan(positions, 257).to(gpu_device), scale=1.0)
+    assert_attention_close(actual, oracle_attention(q, k, v, positions, 1.0))
 
 
 @pytest.mark.parametrize("direction", [1.0, -1.0])
@@ -469,67 +489,57 @@ def test_attention_scores_drifting_along_the_key_axis(gpu_device, dtype, directi
     assert_attention_close(actual, oracle_attention(q, k, v, positions, 0.125))
 
 
-@pytest.mark.parametrize("layout", ["native", "holes"])
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_attention_accepts_native_transposes_storage_offsets_and_custom_scale(gpu_device, layout, dtype):
-    ia = ops()
-    positions = [0, 1, 63, 64, 65, 66, 71, 99, 111, 127, 128, 193, 249, 250, 255, 256, 258]
-    plan = ia.IndexedPlan(positions, 259).to(gpu_device)
-    q = view((1, 6, len(positions), 128), dtype, layout, gpu_device)[1]
-    k = view((1, 3, 259, 128), dtype, layout, gpu_device)[1]
-    v = view((1, 3, 259, 128), dtype, "holes", gpu_device)[1]
-    actual = ia.indexed_causal_attention(q, k, v, plan, scale=0.17)
-    assert_attention_close(actual, oracle_attention(q, k, v, positions, 0.17))
-
-
 @pytest.mark.parametrize("heads,kv_heads", [(1, 1), (4, 1), (4, 4), (8, 2), (6, 2), (32, 8)])
-def test_grouped_query_head_mapping(gpu_device, heads, kv_heads):
+def test_each_query_head_reads_its_own_kv_head(gpu_device, heads, kv_heads):
+    """With K = 0 every visible key weighs the same; V constant per KV head
+    (head j holds j + 1) makes query head h return h // (heads / kv_heads) + 1."""
     ia = ops()
     positions = [0, 64, 130]
-    plan = ia.IndexedPlan(positions, 131).to(gpu_device)
-    q = torch.zeros((1, heads, 3, 64), device=gpu_device, dtype=torch.bfloat16)
-    k = torch.zeros((1, kv_heads, 131, 64), device=gpu_device, dtype=torch.bfloat16)
-    v = torch.empty_like(k)
-    for head in range(kv_heads):
-        v[:, head].fill_(head + 1)
-    actual = ia.indexed_causal_attention(q, k, v, plan)
+    q = torch.zeros(1, heads, 3, 64, device=gpu_device, dtype=torch.bfloat16)
+    k = torch.zeros(1, kv_heads, 131, 64, device=gpu_device, dtype=torch.bfloat16)
+    v = (torch.arange(1, kv_heads + 1, device=gpu_device, dtype=torch.float32)[None, :, None, None]
+         .expand(1, kv_heads, 131, 64).to(torch.bfloat16).contiguous())
+    actual = ia.indexed_causal_attention(q, k, v, ia.IndexedPlan(positions, 131).to(gpu_device))
     assert_attention_close(actual, oracle_attention(q, k, v, positions))
-    for head in range(heads):
-        expect = torch.full_like(actual[:, head].float(), head // (heads // kv_heads) + 1)
-        torch.testing.assert_close(actual[:, head].float(), expect, atol=0.02, rtol=0.01)
+    owner = torch.arange(heads, device=gpu_device) // (heads // kv_heads) + 1
+    assert torch.equal(actual.float(), owner.float()[None, :, None, None].expand_as(actual))
 
 
-def test_fresh_selected_visibility_and_future_exclusion(gpu_device):
+def test_fresh_rows_are_visible_and_later_keys_are_not(gpu_device):
+    """Scattered fresh rows are attended by every selected row at or after them;
+    rewriting keys and values past position 8 leaves the outputs of rows at
+    positions <= 8 bit-identical and changes the row at 9."""
     ia = ops()
     positions = [3, 4, 8, 9]
     plan = ia.IndexedPlan(positions, 131).to(gpu_device)
-    key = torch.zeros((1, 2, 131, 64), device=gpu_device, dtype=torch.bfloat16)
-    value = torch.zeros_like(key)
-    fresh_key = torch.zeros((1, 2, 4, 64), device=gpu_device, dtype=torch.bfloat16)
-    fresh_value = torch.empty_like(fresh_key)
-    for row in range(4):
-        fresh_value[:, :, row].fill_(10 + row)
-    query = torch.zeros((1, 4, 4, 64), device=gpu_device, dtype=torch.bfloat16)
-    ia.indexed_kv_scatter_(key, value, fresh_key, fresh_value, plan)
-    output = ia.indexed_causal_attention(query, key, value, plan)
-    assert_attention_close(output, oracle_attention(query, key, value, positions))
-    assert float(output[0, 0, 2, 0]) > 3.5
-    preserved = output.clone()
-    key[:, :, 9:].fill_(50)
-    value[:, :, 9:].fill_(500)
-    changed = ia.indexed_causal_attention(query, key, value, plan)
-    assert bits_equal(changed[:, :, :3], preserved[:, :, :3])
-    assert not bits_equal(changed[:, :, 3:], preserved[:, :, 3:])
+    cache_k = torch.zeros(1, 2, 131, 64, device=gpu_device, dtype=torch.bfloat16)
+    cache_v = torch.zeros_like(cache_k)
+    fresh_v = (10 + torch.arange(4, device=gpu_device, dtype=torch.float32))[None, None, :, None]
+    fresh_v = fresh_v.expand(1, 2, 4, 64).to(torch.bfloat16).contiguous()
+    ia.indexed_kv_scatter_(cache_k, cache_v, torch.zeros_like(fresh_v), fresh_v, plan)
+    q = torch.zeros(1, 4, 4, 64, device=gpu_device, dtype=torch.bfloat16)
+    first = ia.indexed_causal_attention(q, cache_k, cache_v, plan)
+    assert_attention_close(first, oracle_attention(q, cache_k, cache_v, positions))
+    # row at position 8 averages 9 keys, three of them fresh (10, 11, 12): 33 / 9
+    assert abs(float(first[0, 0, 2, 0]) - 33 / 9) < 0.02
+    cache_k[:, :, 9:] = 50
+    cache_v[:, :, 9:] = 500
+    second = ia.indexed_causal_attention(q, cache_k, cache_v, plan)
+    assert same_bits(second[:, :, :3], first[:, :, :3])
+    assert not same_bits(second[:, :, 3:], first[:, :, 3:])
 
 
-def test_query_at_zero_reads_only_itself(gpu_device):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_a_row_at_position_zero_returns_the_first_value(gpu_device, dtype):
+    """Position 0 sees one key: its softmax weight is exactly 1, so the output
+    is V[0] of its KV head bit for bit."""
     ia = ops()
-    plan = ia.IndexedPlan([0], 130).to(gpu_device)
-    q = torch.randn((1, 4, 1, 64), device=gpu_device, dtype=torch.float16)
-    k = torch.randn((1, 2, 130, 64), device=gpu_device, dtype=torch.float16)
-    v = torch.randn_like(k)
-    output = ia.indexed_causal_attention(q, k, v, plan)
-    assert bits_equal(output, v[:, :, :1].repeat_interleave(2, dim=1))
+    gen = torch.Generator(device=gpu_device).manual_seed(0)
+    q = torch.randn(1, 4, 1, 64, device=gpu_device, generator=gen).to(dtype)
+    k = torch.randn(1, 2, 130, 64, device=gpu_device, generator=gen).to(dtype)
+    v = torch.randn(1, 2, 130, 64, device=gpu_device, generator=gen).to(dtype)
+    out = ia.indexed_causal_attention(q, k, v, ia.IndexedPlan([0], 130).to(gpu_device))
+    assert same_bits(out, v[:, [0, 0, 1, 1], :1])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -551,100 +561,100 @@ def test_generic_kernel_shapes_match_oracle(gpu_device, dtype, dim):
     torch.testing.assert_close(out[0].double().cpu(), expect, atol=atol, rtol=1e-3 if dtype == torch.float32 else 0.02)
 
 
-def test_upload_scatter_attention_use_the_callers_nondefault_stream(gpu_device):
+def test_plan_upload_scatter_and_attention_run_on_the_callers_stream(gpu_device):
+    """Everything is enqueued on the current stream: on a side stream held back
+    by a long kernel, the upload, scatter and attention still see their inputs
+    in order and the result is right once the side stream is joined."""
     ia = ops()
     host = ia.IndexedPlan([0, 3, 4, 8, 9], 130)
-    plan = host.to(gpu_device)
-    q = torch.zeros((1, 4, 5, 64), device=gpu_device, dtype=torch.bfloat16)
-    k = torch.zeros((1, 2, 130, 64), device=gpu_device, dtype=torch.bfloat16)
-    v = k.clone()
-    fresh = torch.zeros((1, 2, 5, 64), device=gpu_device, dtype=torch.bfloat16)
-    ia.indexed_kv_scatter_(k, v, fresh, fresh, plan)
-    ia.indexed_causal_attention(q, k, v, plan)
-    torch.cuda.synchronize()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        torch.cuda._sleep(2_000_000)
+    side = torch.cuda.Stream(device=gpu_device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(2_000_000)  # the side stream's work starts ~ms later than the host's calls return
+        gen = torch.Generator(device=gpu_device).manual_seed(11)
+        q = (torch.randn(1, 4, 5, 64, device=gpu_device, generator=gen) * 0.5).to(torch.bfloat16)
+        k = (torch.randn(1, 2, 130, 64, device=gpu_device, generator=gen) * 0.5).to(torch.bfloat16)
+        v = (torch.randn(1, 2, 130, 64, device=gpu_device, generator=gen) * 0.5).to(torch.bfloat16)
+        fresh = [(torch.randn(1, 2, 5, 64, device=gpu_device, generator=gen)).to(torch.bfloat16) for _ in range(2)]
         plan = host.to(gpu_device)
-        q = torch.randn_like(q) * 0.5
-        k, v = torch.randn_like(k) * 0.5, torch.randn_like(v) * 0.5
-        fresh_k, fresh_v = torch.randn_like(fresh), torch.randn_like(fresh)
-        ia.indexed_kv_scatter_(k, v, fresh_k, fresh_v, plan)
-        output = ia.indexed_causal_attention(q, k, v, plan)
-    torch.cuda.current_stream().wait_stream(stream)
+        ia.indexed_kv_scatter_(k, v, *fresh, plan)
+        out = ia.indexed_causal_attention(q, k, v, plan)
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    assert_attention_close(output, oracle_attention(q, k, v, host.positions))
+    assert_attention_close(out, oracle_attention(q, k, v, host.positions))
 
 
-@pytest.mark.parametrize("problem", ["dtype", "batch", "dimension", "gqa", "overlap", "length", "plan", "scale",
-                                     "grad"])
-def test_attention_public_contract_rejects_unsupported_inputs(gpu_device, problem):
+def _contract_case(kind, device):
+    """(q, k, v, plan, scale) for indexed_causal_attention with one violation."""
     ia = ops()
-    plan = ia.IndexedPlan([0, 3, 8], 9).to(gpu_device)
-    q = torch.zeros((1, 4, 3, 64), device=gpu_device, dtype=torch.float16)
-    k = torch.zeros((1, 2, 9, 64), device=gpu_device, dtype=torch.float16)
-    v = k.clone()
-    scale = None
-    if problem == "dtype":
-        q, k, v = q.float(), k.float(), v.float()
-    elif problem == "batch":
-        q = q.repeat(2, 1, 1, 1)
-    elif problem == "dimension":
-        q, k, v = q[:, :, :, :32], k[:, :, :, :32], v[:, :, :, :32]
-    elif problem == "gqa":
-        q = q[:, :3]
-    elif problem == "overlap":
-        q = q.as_strided(q.shape, (768, 1, 1, 1))
-    elif problem == "length":
-        q = q[:, :, :2]
-    elif problem == "plan":
-        plan = replace(plan, positions=plan.positions.to(torch.int32))
-    elif problem == "scale":
-        scale = float("nan")
-    elif problem == "grad":
-        q.requires_grad_(True)
+    plan = ia.IndexedPlan([0, 3, 8], 9).to(device)
+    q = torch.zeros(1, 4, 3, 64, device=device, dtype=torch.float16)
+    kv = torch.zeros(1, 2, 9, 64, device=device, dtype=torch.float16)
+    cases = {
+        "dtype": lambda: (q.float(), kv.float(), kv.float(), plan, None),
+        "batch": lambda: (q.expand(2, 4, 3, 64), kv, kv, plan, None),
+        "dimension": lambda: (q[..., :32], kv[..., :32], kv[..., :32], plan, None),
+        "gqa": lambda: (q[:, :3], kv, kv, plan, None),
+        "overlap": lambda: (q.as_strided(q.shape, (768, 1, 1, 1)), kv, kv, plan, None),
+        "length": lambda: (q[:, :, :2], kv, kv, plan, None),
+        "plan": lambda: (q, kv, kv, replace(plan, positions=plan.positions.int()), None),
+        "scale": lambda: (q, kv, kv, plan, float("nan")),
+        "grad": lambda: (q.clone().requires_grad_(True), kv, kv, plan, None),
+    }
+    return cases[kind]()
+
+
+@pytest.mark.parametrize("kind", ["dtype", "batch", "dimension", "gqa", "overlap", "length", "plan", "scale", "grad"])
+def test_attention_refuses_inputs_outside_its_contract(gpu_device, kind):
+    ia = ops()
     with pytest.raises(ValueError):
-        ia.indexed_causal_attention(q, k, v, plan, scale)
+        ia.indexed_causal_attention(*_contract_case(kind, gpu_device))
 
 
-@pytest.mark.parametrize("alias", ["outputs", "source"])
-def test_scatter_rejects_aliasing_storage(gpu_device, alias):
+@pytest.mark.parametrize("shared", ["the two outputs", "an output and a source"])
+def test_scatter_refuses_storage_shared_between_tensors(gpu_device, shared):
     ia = ops()
     plan = ia.IndexedPlan([0, 3, 8], 9).to(gpu_device)
-    key = torch.zeros((1, 2, 9, 64), device=gpu_device, dtype=torch.float16)
-    value = key if alias == "outputs" else key.clone()
-    fresh_key = key[:, :, :3] if alias == "source" else torch.zeros((1, 2, 3, 64), device=gpu_device, dtype=key.dtype)
-    with pytest.raises(ValueError, match="independent"):
-        ia.indexed_kv_scatter_(key, value, fresh_key, fresh_key.clone(), plan)
-
-
-@pytest.mark.parametrize("change", ["positions", "full_prefix_tiles", "total_tiles", "replacement", "manufactured"])
-def test_device_plan_rejects_mutated_or_manufactured_metadata(gpu_device, change):
-    ia = ops()
-    plan = ia.IndexedPlan([0, 3, 8], 9).to(gpu_device)
-    q = torch.zeros((1, 4, 3, 64), device=gpu_device, dtype=torch.float16)
-    k = torch.zeros((1, 2, 9, 64), device=gpu_device, dtype=torch.float16)
-    if change in ("positions", "full_prefix_tiles", "total_tiles"):
-        getattr(plan, change).fill_(-1)
-    elif change == "replacement":
-        plan = replace(plan, positions=plan.positions.clone())
+    cache_k = torch.zeros(1, 2, 9, 64, device=gpu_device, dtype=torch.float16)
+    if shared == "the two outputs":
+        args = (cache_k, cache_k, torch.zeros(1, 2, 3, 64, device=gpu_device, dtype=torch.float16))
     else:
-        plan = ia.DeviceIndexedPlan(plan.host_plan, plan.positions, plan.full_prefix_tiles, plan.total_tiles)
+        args = (cache_k, cache_k.clone(), cache_k[:, :, :3])
+    with pytest.raises(ValueError, match="independent"):
+        ia.indexed_kv_scatter_(*args, args[2].clone(), plan)
+
+
+def _tampered(plan, how):
+    ia = ops()
+    if how in ("positions", "full_prefix_tiles", "total_tiles"):
+        getattr(plan, how).fill_(-1)  # in place on the sealed device tensors
+        return plan
+    if how == "replacement":
+        return replace(plan, positions=plan.positions.clone())
+    return ia.DeviceIndexedPlan(plan.host_plan, plan.positions, plan.full_prefix_tiles, plan.total_tiles)
+
+
+@pytest.mark.parametrize("how", ["positions", "full_prefix_tiles", "total_tiles", "replacement", "manufactured"])
+def test_a_tampered_device_plan_is_refused(gpu_device, how):
+    ia = ops()
+    plan = _tampered(ia.IndexedPlan([0, 3, 8], 9).to(gpu_device), how)
+    q = torch.zeros(1, 4, 3, 64, device=gpu_device, dtype=torch.float16)
+    kv = torch.zeros(1, 2, 9, 64, device=gpu_device, dtype=torch.float16)
     with pytest.raises(ValueError, match="metadata"):
-        ia.indexed_causal_attention(q, k, k, plan)
+        ia.indexed_causal_attention(q, kv, kv, plan)
 
 
-def test_plan_upload_under_inference_mode_still_tracks_mutations(gpu_device):
+def test_a_plan_uploaded_in_inference_mode_still_detects_mutation(gpu_device):
+    """Tensors created under inference_mode have no version counter; the plan
+    seal must still see an in-place change."""
     ia = ops()
     with torch.inference_mode():
         plan = ia.IndexedPlan([0], 1).to(gpu_device)
-        q = torch.ones((1, 1, 1, 64), device=gpu_device, dtype=torch.float16)
-        actual = ia.indexed_causal_attention(q, q, q, plan)
-        assert bits_equal(actual, q)
+        ones = torch.ones(1, 1, 1, 64, device=gpu_device, dtype=torch.float16)
+        assert same_bits(ia.indexed_causal_attention(ones, ones, ones, plan), ones)
         plan.positions.add_(0)
         with pytest.raises(ValueError, match="mutated"):
-            ia.indexed_causal_attention(q, q, q, plan)
+            ia.indexed_causal_attention(ones, ones, ones, plan)
 
 
 # --------------------------------------------------------------------------- full-size shapes

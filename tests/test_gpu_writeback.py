@@ -1,9 +1,17 @@
 """GPU parity of the interval writeback (kvr_copy_kv_interval).
 
-Mirrors the reference's tests/test_writeback.py with the HIP library in place
-of Triton: bit-exact against torch's slice copy AND the C oracle over whole
-backings (holes, permuted, batch/head holes, storage offsets), raw NaN payload
-bits, and the validation contract (same ValueError classes and messages).
+Every tensor here is a view made with ``as_strided`` over a flat random
+storage, so the expected storage after a copy can be computed independently of
+the kernel: a storage-index map (``arange`` viewed with the tensor's strides)
+says which storage element each view element is, and the interval rows are
+assigned through those maps. The whole storages (holes, padding, rows outside
+the interval, the sources) must then match bit for bit, and the copied views
+must equal the C oracle's ``orc_copy_interval``.
+
+Vectors from the reference's tests/test_writeback.py: the four layouts (dense,
+every other row and dim with offsets, token-major, padded batch and head axes),
+the shapes and intervals, the rejected intervals and tensor contracts, and the
+fp16/bf16 payloads (signed zeros, infinities, a NaN with payload, a subnormal).
 """
 
 from __future__ import annotations
@@ -13,62 +21,43 @@ import pytest
 import torch
 
 from oracle import oracle as orc
+from strided_views import PAYLOADS, host_bits, payload_rows, same_bits, storage_index, strided_over_storage
 
 pytestmark = pytest.mark.gpu
 
 CODE = {torch.float32: orc.F32, torch.float16: orc.F16, torch.bfloat16: orc.BF16}
 
 
-def _view(shape, dtype, layout, device):
-    batch, heads, tokens, dim = shape
-    if layout == "contiguous":
-        backing = torch.randn(shape, device=device).to(dtype)
-        return backing, backing
-    if layout == "holes":
-        backing = torch.randn((batch, heads, 2 * tokens + 3, 2 * dim + 5), device=device).to(dtype)
-        return backing, backing[:, :, 1:1 + 2 * tokens:2, 2:2 + 2 * dim:2]
-    if layout == "transposed":
-        backing = torch.randn((batch, tokens, heads, dim), device=device).to(dtype)
-        return backing, backing.permute(0, 2, 1, 3)
-    if layout == "batch_head_holes":
-        backing = torch.randn((2 * batch + 1, 2 * heads + 1, tokens + 2, dim + 4), device=device).to(dtype)
-        return backing, backing[1:1 + 2 * batch:2, 1:1 + 2 * heads:2, 1:1 + tokens, 2:2 + dim]
-    raise AssertionError(layout)
+CASES = [((1, 8, 37, 128), 3, 4), ((2, 3, 71, 37), 5, 22), ((2, 5, 33, 7), 0, 33), ((1, 1, 9, 13), 0, 0),
+         ((1, 8, 300, 128), 17, 289)]
+ARRANGEMENTS = {"dense": ("dense",) * 4, "mixed": ("sparse", "token_major", "padded", "sparse")}
 
 
-def host(t):
-    t = t.detach().cpu()
-    return t.numpy() if t.dtype == torch.float32 else t.view(torch.int16).numpy().view(np.uint16)
-
-
+@pytest.mark.parametrize("layouts", list(ARRANGEMENTS))
+@pytest.mark.parametrize("shape,start,end", CASES)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("shape,start,end", [((1, 8, 37, 128), 3, 4), ((2, 3, 71, 37), 5, 22),
-                                             ((2, 5, 33, 7), 0, 33), ((1, 1, 9, 13), 0, 0),
-                                             ((1, 8, 300, 128), 17, 289)])
-@pytest.mark.parametrize("strided", [False, True])
-def test_writeback_matches_slice_copy_oracle_and_preserves_storage(gpu_device, shape, start, end, dtype, strided):
+def test_interval_copy_writes_exactly_the_interval(gpu_device, shape, start, end, dtype, layouts):
     from kv_cache_repair_amd.kernels.writeback import copy_kv_interval_
 
-    torch.manual_seed(701 + end)
-    source_shape = (shape[0], shape[1], max(1, end), shape[3])
-    layouts = ("holes", "transposed", "batch_head_holes", "holes") if strided else ("contiguous",) * 4
-    pairs = [_view(s, dtype, layout, gpu_device)
-             for s, layout in zip((shape, shape, source_shape, source_shape), layouts)]
-    backings = [p[0] for p in pairs]
-    tensors = [p[1] for p in pairs]
-    snapshots = [b.clone() for b in backings]
-    views = [b.as_strided(t.shape, t.stride(), t.storage_offset()) for b, t in zip(snapshots, tensors)]
-    oracle_k = orc.copy_interval(host(views[0]), host(views[2]), start, start, end - start, CODE[dtype])
-    oracle_v = orc.copy_interval(host(views[1]), host(views[3]), start, start, end - start, CODE[dtype])
-    views[0][:, :, start:end, :].copy_(views[2][:, :, start:end, :])
-    views[1][:, :, start:end, :].copy_(views[3][:, :, start:end, :])
+    gen = torch.Generator(device=gpu_device).manual_seed(5000 + 7 * end + shape[3])
+    src_shape = shape[:2] + (max(1, end), shape[3])
+    made = [strided_over_storage(s, dtype, gpu_device, layout, gen)
+            for s, layout in zip((shape, shape, src_shape, src_shape), ARRANGEMENTS[layouts])]
+    storages, views = [m[0] for m in made], [m[1] for m in made]
+    before = [s.clone() for s in storages]
+    expected = [s.clone() for s in storages]
+    for out, src in ((0, 2), (1, 3)):
+        dst_idx = storage_index(views[out])[:, :, start:end, :]
+        src_idx = storage_index(views[src])[:, :, start:end, :]
+        expected[out][dst_idx.reshape(-1)] = before[src][src_idx.reshape(-1)]
+    oracle = [orc.copy_interval(host_bits(views[out]), host_bits(views[src]), start, start, end - start,
+                                CODE[dtype]) for out, src in ((0, 2), (1, 3))]
 
-    copy_kv_interval_(*tensors, start, end)
+    copy_kv_interval_(*views, start, end)
     torch.cuda.synchronize()
-    # whole backings: unselected rows, holes, storage offsets and the sources are untouched
-    for actual, expected in zip(backings, snapshots):
-        assert torch.equal(actual.contiguous().view(torch.uint8), expected.contiguous().view(torch.uint8))
-    assert np.array_equal(host(tensors[0]), oracle_k) and np.array_equal(host(tensors[1]), oracle_v)
+    for actual, want in zip(storages, expected):
+        assert same_bits(actual, want)
+    assert np.array_equal(host_bits(views[0]), oracle[0]) and np.array_equal(host_bits(views[1]), oracle[1])
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -90,50 +79,63 @@ def test_scatter_fresh_kv_writes_fresh_rows_at_the_interval(gpu_device, dtype):
         scatter_fresh_kv(out_k, out_v, fresh_k, fresh_v, 40, 46)
 
 
-@pytest.mark.parametrize("start,end", [(-1, 2), (2, 1), (0, 5), (True, 2), (0, 1.0)])
-def test_invalid_interval_is_rejected(gpu_device, start, end):
+def four(device, shape=(1, 2, 4, 8)):
+    return [torch.zeros(shape, device=device) for _ in range(4)]
+
+
+BAD_INTERVALS = {"negative start": (-1, 2), "reversed": (2, 1), "past the end": (0, 5), "bool start": (True, 2),
+                 "float end": (0, 1.0)}
+
+
+@pytest.mark.parametrize("why", list(BAD_INTERVALS))
+def test_intervals_outside_the_contract_are_refused(gpu_device, why):
     from kv_cache_repair_amd.kernels.writeback import copy_kv_interval_
 
-    tensors = [torch.zeros((1, 2, 4, 8), device=gpu_device) for _ in range(4)]
+    tensors = four(gpu_device)
+    start, end = BAD_INTERVALS[why]
     with pytest.raises(ValueError, match="interval"):
         copy_kv_interval_(*tensors, start, end)
+    assert all(torch.count_nonzero(t) == 0 for t in tensors)
+
+
+def _spoil(kind, tensors, device):
+    """The four copy_kv_interval_ tensors with one contract violation."""
+    out_k, out_v, src_k, src_v = tensors
+    spoiled = {
+        "source_alias": lambda: (out_k, out_v, out_k.view_as(out_k), src_v),   # a source shares out_k's storage
+        "output_alias": lambda: (out_k, out_k.view_as(out_k), src_k, src_v),   # the two outputs share storage
+        "dtype": lambda: (out_k, out_v, src_k.double(), src_v),
+        "shape": lambda: (out_k, out_v, torch.zeros(1, 3, 4, 8, device=device), src_v),
+        "zero_stride": lambda: (torch.zeros(1, 1, 4, 8, device=device).expand(1, 2, 4, 8), out_v, src_k, src_v),
+        "overlap": lambda: (out_k.as_strided((1, 2, 4, 8), (64, 1, 1, 1)), out_v, src_k, src_v),
+    }
+    return spoiled[kind]()
 
 
 @pytest.mark.parametrize("kind", ["source_alias", "output_alias", "dtype", "shape", "zero_stride", "overlap"])
-def test_invalid_tensor_contract_is_rejected(gpu_device, kind):
+def test_tensors_outside_the_contract_are_refused(gpu_device, kind):
     from kv_cache_repair_amd.kernels.writeback import copy_kv_interval_
 
-    tensors = [torch.zeros((1, 2, 4, 8), device=gpu_device) for _ in range(4)]
-    if kind == "source_alias":
-        tensors[2] = tensors[0][:, :, :, :]
-    elif kind == "output_alias":
-        tensors[1] = tensors[0][:, :, :, :]
-    elif kind == "dtype":
-        tensors[2] = tensors[2].to(torch.float64)
-    elif kind == "shape":
-        tensors[2] = torch.zeros((1, 3, 4, 8), device=gpu_device)
-    elif kind == "zero_stride":
-        tensors[0] = torch.zeros((1, 1, 4, 8), device=gpu_device).expand(1, 2, 4, 8)
-    elif kind == "overlap":
-        tensors[0] = tensors[0].as_strided((1, 2, 4, 8), (64, 1, 1, 1))
     with pytest.raises(ValueError):
-        copy_kv_interval_(*tensors, 0, 2)
+        copy_kv_interval_(*_spoil(kind, four(gpu_device), gpu_device), 0, 2)
 
 
-@pytest.mark.parametrize("dtype,bits", [
-    (torch.float16, [0, -32768, 31744, -1024, 32257, 1]),
-    (torch.bfloat16, [0, -32768, 32640, -128, 32705, 1]),
-])
-def test_writeback_preserves_raw_bits_including_nan_payloads(gpu_device, dtype, bits):
+@pytest.mark.parametrize("dtype", list(PAYLOADS))
+@pytest.mark.parametrize("heads,rows", [(1, 2), (3, 5)])
+def test_copied_rows_keep_their_exact_bits(gpu_device, dtype, heads, rows):
+    """Special values and NaN payloads survive the copy unchanged (no
+    arithmetic, no canonicalisation), in K and V, and rows past the interval
+    stay untouched."""
     from kv_cache_repair_amd.kernels.writeback import copy_kv_interval_
 
-    raw = torch.tensor(bits, dtype=torch.int16, device=gpu_device).reshape(1, 1, 2, 3)
-    source_key = raw.view(dtype)
-    source_value = source_key.clone()
-    target_key = torch.zeros((1, 1, 4, 3), device=gpu_device, dtype=dtype)
-    target_value = target_key.clone()
-    copy_kv_interval_(target_key, target_value, source_key, source_value, 0, 2)
+    bits = payload_rows(dtype, heads, rows, 3, gpu_device)
+    src_k = bits.view(dtype)
+    src_v = bits.flip(2).contiguous().view(dtype)
+    out_k = torch.zeros(1, heads, rows + 2, 3, device=gpu_device, dtype=dtype)
+    out_v = torch.zeros_like(out_k)
+    copy_kv_interval_(out_k, out_v, src_k, src_v, 0, rows)
     torch.cuda.synchronize()
-    for target in (target_key, target_value):
-        assert torch.equal(target[:, :, :2, :].view(torch.int16), raw)
-        assert torch.count_nonzero(target[:, :, 2:, :].view(torch.int16)) == 0
+    assert torch.equal(out_k[:, :, :rows].view(torch.int16), bits)
+    assert torch.equal(out_v[:, :, :rows].view(torch.int16), bits.flip(2))
+    assert torch.count_nonzero(out_k[:, :, rows:].view(torch.int16)) == 0
+    assert torch.count_nonzero(out_v[:, :, rows:].view(torch.int16)) == 0
