@@ -147,13 +147,15 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
     const PartialSums gemm_partials{static_cast<const float*>(gws), 0};
     const bool norm_partials = rms_norm_partials_ok(h, dt);
 
-    // q/k/v projections (+ Qwen3's per-head norms)
+    // q/k/v projections (+ Qwen3's per-head norms: inside the fresh-row
+    // epilogue, except for fp16, whose epilogue takes its scalar kernel)
     const char* qp;
     const char* kp;
     const char* vp;
     int64_t q_ld, k_ld, v_ld;
     int32_t qkv_splits = 1;
-    if (!qk_norm) {
+    const bool norms_in_epilogue = qk_norm && dt != KVR_DTYPE_F16;
+    if (!qk_norm || norms_in_epilogue) {
         const void* w[3] = {L->w_q, L->w_k, L->w_v};
         const int32_t rows[3] = {qd, kd, kd};
         const int64_t ldw[3] = {L->ld_q, L->ld_k, L->ld_v};
@@ -195,7 +197,13 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
         PartialSums p = gemm_partials;
         p.splits = qkv_splits;
         KVR_TRY(rope_scatter_partials(p, part_col, q_rot, L->cache_k, L->cache_v, d->cos, d->sin, d->positions, m,
-                                      d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, dt, stream));
+                                      d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, dt, stream,
+                                      norms_in_epilogue ? L->q_norm : nullptr,
+                                      norms_in_epilogue ? L->k_norm : nullptr, L->eps_q, L->eps_k));
+    } else if (norms_in_epilogue) {
+        KVR_TRY(kvr_rope_scatter_kv_norm(qp, q_rot, kp, vp, L->cache_k, L->cache_v, d->cos, d->sin, d->positions, m,
+                                         d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, L->q_norm,
+                                         L->k_norm, L->eps_q, L->eps_k, dt, stream));
     } else {
         KVR_TRY(kvr_rope_scatter_kv(qp, q_rot, kp, vp, L->cache_k, L->cache_v, d->cos, d->sin, d->positions, m,
                                     d->q_heads, d->kv_heads, d->n_keys, dim, rs, d->cs_strides, dt, stream));

@@ -12,6 +12,14 @@
 // Each multiply and the add round to the storage type exactly as the eager
 // elementwise ops do, so the outputs are bit-identical to that op sequence.
 // A position outside [0, n_keys) writes no K/V row (as the scatter).
+//
+// With per-head norm weights (Qwen3's q_norm / k_norm, transformers 5.15.0
+// models/qwen3/modeling_qwen3.py:252-257 apply them to the projected q and k
+// before RoPE) each q / k row is first RMS-normalised over head_dim:
+//   x' = w * dtype(x * rsqrt(mean(x^2) + eps))
+// with kvr_rms_norm's fp32 summation order (per 16-byte vector, then the
+// butterfly over vectors), so the result is bit-identical to kvr_rms_norm
+// followed by the plain epilogue.
 #include "kvr_internal.h"
 
 #include <type_traits>
@@ -38,6 +46,8 @@ struct FreshArgs {
     int32_t head_dim;
     PartialSums src;      // src.base != nullptr: q / fresh K / fresh V come from split-K partial sums
     int64_t part_col[3];  // their first column in the concatenated projection
+    const char* norm_w[2];  // per-head RMSNorm weights [head_dim] of q and k, or null (no norm)
+    float norm_eps[2];
 };
 
 // One rotated pair with distinct cos/sin for the two halves (the rotary
@@ -72,6 +82,44 @@ __device__ inline void decode_row(const FreshArgs& a, int64_t g, int& part, int6
         r = g / a.n_kv_heads;
         h = g - r * a.n_kv_heads;
     }
+}
+
+// RMSNorm of one row held by TPR lanes, lane c holding 16-byte vector c of the
+// first half (lo) and vector c of the second half (hi), in place. The sum of
+// squares follows kvr_rms_norm, whose lane j holds vector j of 2 TPR: each
+// vector's squares summed in order, then a butterfly over the vectors; its
+// first step pairs vectors c and c + TPR, i.e. lo + hi here, and the rest of
+// the butterfly runs over the TPR lanes.
+template <typename T>
+__device__ inline void norm_row(u32x4& lo, u32x4& hi, const u32x4& w_lo, const u32x4& w_hi, int tpr, int dim,
+                                float eps) {
+#pragma clang fp contract(off)
+    using E = elem<T>;
+    using bits = typename E::bits;
+    constexpr int EPV = 16 / E::size;
+    bits xl[EPV], xh[EPV], wl[EPV], wh[EPV];
+    __builtin_memcpy(xl, &lo, 16);
+    __builtin_memcpy(xh, &hi, 16);
+    __builtin_memcpy(wl, &w_lo, 16);
+    __builtin_memcpy(wh, &w_hi, 16);
+    float vl[EPV], vh[EPV], s_lo = 0.f, s_hi = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+        vl[e] = E::to_float(xl[e]);
+        vh[e] = E::to_float(xh[e]);
+        s_lo += vl[e] * vl[e];
+        s_hi += vh[e] * vh[e];
+    }
+    float ss = s_lo + s_hi;
+    for (int off = tpr >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, tpr);
+    const float inv = rsqrtf(ss * (1.f / static_cast<float>(dim)) + eps);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+        xl[e] = E::from_float(E::to_float(wl[e]) * round_through<T>(vl[e] * inv));
+        xh[e] = E::from_float(E::to_float(wh[e]) * round_through<T>(vh[e] * inv));
+    }
+    __builtin_memcpy(&lo, xl, 16);
+    __builtin_memcpy(&hi, xh, 16);
 }
 
 // Vector path: unit dim strides, 16-byte aligned rows. TPR threads share a
@@ -129,6 +177,14 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
             for (int e = 0; e < EPV; ++e) b[e] = E::from_float(sh8[e]);
             __builtin_memcpy(&hi, b, 16);
         }
+    }
+    // per-head RMSNorm of a q or k row (uniform over the row's TPR lanes, so
+    // the butterfly below runs on whole lane groups)
+    if (part < 2 && a.norm_w[part]) {
+        const char* wrow = a.norm_w[part];
+        const u32x4 w_lo = *reinterpret_cast<const u32x4*>(wrow + lo_off * E::size);
+        const u32x4 w_hi = *reinterpret_cast<const u32x4*>(wrow + hi_off * E::size);
+        norm_row<T>(lo, hi, w_lo, w_hi, tpr, a.head_dim, a.norm_eps[part]);
     }
     char* dst;
     if (part == 0) {
@@ -248,7 +304,8 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
                       const void* cos, const void* sin, const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
                       int32_t n_kv_heads, int64_t n_keys, int32_t head_dim, const int64_t strides[18],
                       const int64_t cs_strides[4], int32_t dtype, void* stream, const PartialSums* partial,
-                      const int64_t* part_col) {
+                      const int64_t* part_col, const void* q_norm = nullptr, const void* k_norm = nullptr,
+                      float eps_q = 0.f, float eps_k = 0.f) {
     using namespace kvr;
     const int esize = dtype_size(dtype);
     if (esize == 0) return KVR_E_UNSUPPORTED_DTYPE;
@@ -267,6 +324,10 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
         return KVR_E_NULL_POINTER;
     }
     if (!q_out || !out_k || !out_v || !cos || !sin || !positions) return KVR_E_NULL_POINTER;
+    const bool norms = q_norm || k_norm;
+    if (norms && (!q_norm || !k_norm)) return KVR_E_NULL_POINTER;
+    if (norms && (!(eps_q >= 0.f) || !(eps_k >= 0.f) || eps_q == INFINITY || eps_k == INFINITY))
+        return KVR_E_INVALID_ARGUMENT;
 
     FreshArgs a;
     a.q = static_cast<const char*>(q);
@@ -297,6 +358,10 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
     a.head_dim = head_dim;
     a.src = partial ? *partial : PartialSums{};
     for (int i = 0; i < 3; ++i) a.part_col[i] = part_col ? part_col[i] : 0;
+    a.norm_w[0] = static_cast<const char*>(q_norm);
+    a.norm_w[1] = static_cast<const char*>(k_norm);
+    a.norm_eps[0] = eps_q;
+    a.norm_eps[1] = eps_k;
 
     // Vector path: each half splits into a power-of-two number of 16-byte chunks.
     const int64_t half_bytes = static_cast<int64_t>(head_dim / 2) * esize;
@@ -315,6 +380,10 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
           (cs_strides[2] * esize) % 16 == 0;
     vec = vec && aligned16(q) && aligned16(q_out) && aligned16(fresh_k) && aligned16(fresh_v) && aligned16(out_k) &&
           aligned16(out_v) && aligned16(cos) && aligned16(sin);
+    // the norms run on the vector path only (their butterfly is over its lane
+    // groups), which fp16 does not take (see launch)
+    if (norms && (!vec || dtype == KVR_DTYPE_F16 || !aligned16(q_norm) || !aligned16(k_norm)))
+        return KVR_E_UNSUPPORTED_SHAPE;
 
     hipStream_t s = as_stream(stream);
     switch (dtype) {
@@ -329,9 +398,11 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
 int rope_scatter_partials(const PartialSums& src, const int64_t part_col[3], void* q_out, void* out_k, void* out_v,
                           const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,
                           int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
-                          const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream) {
+                          const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream,
+                          const void* q_norm, const void* k_norm, float eps_q, float eps_k) {
     return rope_scatter_impl(nullptr, q_out, nullptr, nullptr, out_k, out_v, cos, sin, positions, n_sel, n_q_heads,
-                             n_kv_heads, n_keys, head_dim, strides, cs_strides, dtype, stream, &src, part_col);
+                             n_kv_heads, n_keys, head_dim, strides, cs_strides, dtype, stream, &src, part_col,
+                             q_norm, k_norm, eps_q, eps_k);
 }
 
 }  // namespace kvr
@@ -343,4 +414,15 @@ extern "C" int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh
                                    int32_t dtype, void* stream) {
     return kvr::rope_scatter_impl(q, q_out, fresh_k, fresh_v, out_k, out_v, cos, sin, positions, n_sel, n_q_heads,
                                   n_kv_heads, n_keys, head_dim, strides, cs_strides, dtype, stream, nullptr, nullptr);
+}
+
+extern "C" int kvr_rope_scatter_kv_norm(const void* q, void* q_out, const void* fresh_k, const void* fresh_v,
+                                        void* out_k, void* out_v, const void* cos, const void* sin,
+                                        const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
+                                        int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
+                                        const int64_t strides[18], const int64_t cs_strides[4], const void* q_norm,
+                                        const void* k_norm, float eps_q, float eps_k, int32_t dtype, void* stream) {
+    return kvr::rope_scatter_impl(q, q_out, fresh_k, fresh_v, out_k, out_v, cos, sin, positions, n_sel, n_q_heads,
+                                  n_kv_heads, n_keys, head_dim, strides, cs_strides, dtype, stream, nullptr, nullptr,
+                                  q_norm, k_norm, eps_q, eps_k);
 }

@@ -146,14 +146,16 @@ int rms_norm_partials(const PartialSums& x, const void* residual, void* residual
                       int64_t rows, int32_t hidden, const int64_t row_strides[4], float eps, int32_t dtype,
                       void* stream);
 
-// kvr_rope_scatter_kv with q, fresh K and fresh V given as split-K partial sums
-// of one concatenated projection (columns part_col[0] + h*head_dim + i for
+// kvr_rope_scatter_kv_norm with q, fresh K and fresh V given as split-K partial
+// sums of one concatenated projection (columns part_col[0] + h*head_dim + i for
 // query head h, part_col[1] + ... for K, part_col[2] + ... for V). The q /
-// fresh-K / fresh-V strides of `strides` are ignored.
+// fresh-K / fresh-V strides of `strides` are ignored; q_norm / k_norm null: no
+// per-head norm.
 int rope_scatter_partials(const PartialSums& src, const int64_t part_col[3], void* q_out, void* out_k, void* out_v,
                           const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,
                           int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
-                          const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream);
+                          const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream,
+                          const void* q_norm, const void* k_norm, float eps_q, float eps_k);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

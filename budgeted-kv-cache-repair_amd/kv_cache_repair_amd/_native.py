@@ -78,6 +78,10 @@ def _declare(lib: ctypes.CDLL) -> None:
                                         ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, _i64p, _i64p, ctypes.c_int32,
                                         _vp]
     lib.kvr_rope_scatter_kv.restype = ctypes.c_int
+    lib.kvr_rope_scatter_kv_norm.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64,
+                                             ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, _i64p,
+                                             _i64p, _vp, _vp, ctypes.c_float, ctypes.c_float, ctypes.c_int32, _vp]
+    lib.kvr_rope_scatter_kv_norm.restype = ctypes.c_int
     lib.kvr_rms_norm.argtypes = [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, _i64p, ctypes.c_float,
                                  ctypes.c_int32, _vp]
     lib.kvr_rms_norm.restype = ctypes.c_int

@@ -86,15 +86,25 @@ class _Launcher:
             _native.stream_handle(self.device))
         _native.check(status, "kvr_indexed_scatter_kv")
 
-    def rope_scatter(self, q, q_out, fresh_k, fresh_v, keys, values, cos, sin) -> None:
-        status = _native.lib().kvr_rope_scatter_kv(
-            q.data_ptr(), q_out.data_ptr(), fresh_k.data_ptr(), fresh_v.data_ptr(), keys.data_ptr(),
-            values.data_ptr(), cos.data_ptr(), sin.data_ptr(), self.positions_ptr, self.n_sel, self.q_heads,
-            self.kv_heads, self.n_keys, self.head_dim,
-            self._stride_array((q, q_out, fresh_k, fresh_v, keys, values)),
-            _native.i64_array([int(cos.stride(-2)), int(cos.stride(-1)), int(sin.stride(-2)), int(sin.stride(-1))]),
-            self.dtype_code, _native.stream_handle(self.device))
-        _native.check(status, "kvr_rope_scatter_kv")
+    def rope_scatter(self, q, q_out, fresh_k, fresh_v, keys, values, cos, sin, norms=None) -> None:
+        """The fresh-row epilogue; ``norms`` = (q_norm, k_norm) modules folds
+        their per-head RMSNorm in front of RoPE (kvr_rope_scatter_kv_norm)."""
+        lib = _native.lib()
+        args = (q.data_ptr(), q_out.data_ptr(), fresh_k.data_ptr(), fresh_v.data_ptr(), keys.data_ptr(),
+                values.data_ptr(), cos.data_ptr(), sin.data_ptr(), self.positions_ptr, self.n_sel, self.q_heads,
+                self.kv_heads, self.n_keys, self.head_dim,
+                self._stride_array((q, q_out, fresh_k, fresh_v, keys, values)),
+                _native.i64_array([int(cos.stride(-2)), int(cos.stride(-1)), int(sin.stride(-2)),
+                                   int(sin.stride(-1))]))
+        if norms is None:
+            status = lib.kvr_rope_scatter_kv(*args, self.dtype_code, _native.stream_handle(self.device))
+            _native.check(status, "kvr_rope_scatter_kv")
+            return
+        q_norm, k_norm = norms
+        status = lib.kvr_rope_scatter_kv_norm(*args, q_norm.weight.data_ptr(), k_norm.weight.data_ptr(),
+                                              float(q_norm.variance_epsilon), float(k_norm.variance_epsilon),
+                                              self.dtype_code, _native.stream_handle(self.device))
+        _native.check(status, "kvr_rope_scatter_kv_norm")
 
     def attention(self, q, k, v, out_view, scale: float) -> None:
         status = _native.lib().kvr_packed_causal_attention(
@@ -154,6 +164,21 @@ def _silu_activations() -> tuple[type, ...]:
 _SILU_ACTIVATIONS = _silu_activations()
 
 
+def _norms_in_epilogue(dtype) -> bool:
+    """Qwen3's per-head q/k norms run inside the fresh-row epilogue
+    (kvr_rope_scatter_kv_norm) for bf16 / fp32 rows; fp16 rows take the epilogue's
+    scalar kernel, which has no norm, so they keep separate kvr_rms_norm launches."""
+    return dtype in (torch.bfloat16, torch.float32)
+
+
+def _checked_head_norm(module, x: torch.Tensor):
+    weight = module.weight
+    if weight.dtype != x.dtype or weight.numel() != x.shape[-1] or not weight.is_contiguous() \
+            or not isinstance(getattr(module, "variance_epsilon", None), float):
+        raise RuntimeError("packed fused per-head RMSNorm geometry/dtype drifted")
+    return module
+
+
 def _rms_norm(module, x: torch.Tensor, residual: torch.Tensor | None = None):
     """One kvr_rms_norm launch with ``module``'s weight and epsilon over the last
     dim of contiguous ``x``; with ``residual`` also returns s = residual + x."""
@@ -188,8 +213,8 @@ def _silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 @dataclass
 class _LayerPlans:
     """kvr_linear_multi plans of one decoder layer's projections: q/k/v in one
-    launch (separate launches when the layer normalises q/k per head), o, the
-    SiLU-gated gate/up pair in one launch, down."""
+    launch (separate launches for fp16 layers that normalise q/k per head), o,
+    the SiLU-gated gate/up pair in one launch, down."""
 
     pointers: tuple
     qkv: Any
@@ -270,7 +295,9 @@ def _layer_plans(layer) -> _LayerPlans | None:
         return None
     q, k, v, o, gate, up, down = weights
     plan = _projection.ProjectionPlan
-    separate = len(norms) > 2
+    # q/k/v in one launch, unless per-head norms must run as separate launches
+    # on contiguous q and k (fp16: the epilogue cannot fold them in)
+    separate = len(norms) > 2 and not _norms_in_epilogue(q.dtype)
     plans = _LayerPlans(
         pointers=key, qkv=None if separate else plan([q, k, v]), q=plan([q]) if separate else None,
         k=plan([k]) if separate else None, v=plan([v]) if separate else None, o=plan([o]),
@@ -429,8 +456,11 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
         key = plans.k(hidden_states).view(hidden_shape)
         value = plans.v(hidden_states).view(hidden_shape)
     q_norm = getattr(self, "q_norm", None)
+    norms = None
     if q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
-        if getattr(self, "_kvr_fused_norms", False):
+        if getattr(self, "_kvr_fused_norms", False) and _norms_in_epilogue(query.dtype):
+            norms = (_checked_head_norm(q_norm, query), _checked_head_norm(self.k_norm, key))
+        elif getattr(self, "_kvr_fused_norms", False):
             query = _rms_norm(q_norm, query)
             key = _rms_norm(self.k_norm, key)
         else:
@@ -440,7 +470,7 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     layer = past_key_values.layers[self.layer_idx]
     rotated = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     layer.fused_update(query.transpose(1, 2), rotated.transpose(1, 2), key.transpose(1, 2), value.transpose(1, 2),
-                       cos, sin)
+                       cos, sin, norms)
     launcher = context.launcher
     out = torch.empty(query.shape, dtype=query.dtype, device=query.device)  # [1, B, Hq, D]
     launcher.attention(rotated.transpose(1, 2), layer.keys, layer.values, out.transpose(1, 2), float(self.scaling))
@@ -610,9 +640,10 @@ class _PackedLayer(DynamicLayer):
         self.updated = True
         return self.keys, self.values
 
-    def fused_update(self, query, query_out, key_states, value_states, cos, sin):
+    def fused_update(self, query, query_out, key_states, value_states, cos, sin, norms=None):
         """Fresh-row epilogue: rotate queries (into ``query_out``) and keys at the
-        context positions, scatter the keys and values into this layer."""
+        context positions, scatter the keys and values into this layer; with
+        ``norms`` = (q_norm, k_norm), RMS-normalise q and k per head first."""
         if self.updated:
             raise RuntimeError("packed native forward updated one layer more than once")
         positions = self._context.positions
@@ -631,7 +662,7 @@ class _PackedLayer(DynamicLayer):
         if self._backend != "hip":
             raise RuntimeError("unknown packed writeback backend")
         self._context.launcher.rope_scatter(query, query_out, key_states, value_states, self.keys, self.values,
-                                            cos, sin)
+                                            cos, sin, norms)
         self.updated = True
 
 

@@ -191,6 +191,25 @@ int kvr_rope_scatter_kv(const void* q, void* q_out, const void* fresh_k, const v
                         const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream);
 
 /*
+ * kvr_rope_scatter_kv with Qwen3's per-head RMSNorm of the fresh queries and
+ * keys before RoPE (transformers 5.15.0 models/qwen3/modeling_qwen3.py:252-257,
+ * q_norm / k_norm of the attention module): each q row uses `q_norm`, each K
+ * row `k_norm` ([head_dim] weights in `dtype`, 16-byte aligned), with epsilons
+ * eps_q / eps_k; values are not normalised. The norm is HF's
+ * w * dtype(x * rsqrt(mean(x^2) + eps)) with kvr_rms_norm's fp32 summation
+ * order, so the result is bit-identical to kvr_rms_norm of q and k followed by
+ * kvr_rope_scatter_kv. Runs on bf16 / fp32 rows with unit dim strides and
+ * 16-byte aligned rows (KVR_E_UNSUPPORTED_SHAPE otherwise: take the two steps
+ * separately). Both weights or neither (neither = kvr_rope_scatter_kv). No
+ * reference counterpart of its own (the reference runs these as eager ops).
+ */
+int kvr_rope_scatter_kv_norm(const void* q, void* q_out, const void* fresh_k, const void* fresh_v, void* out_k,
+                             void* out_v, const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,
+                             int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys, int32_t head_dim,
+                             const int64_t strides[18], const int64_t cs_strides[4], const void* q_norm,
+                             const void* k_norm, float eps_q, float eps_k, int32_t dtype, void* stream);
+
+/*
  * RMSNorm of `rows` rows of `hidden` elements, with an optional residual add
  * in front (one launch):
  *   s   = residual == NULL ? x : dtype(residual + x)      (s written to residual_out)

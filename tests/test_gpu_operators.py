@@ -201,6 +201,105 @@ def test_rope_scatter_rejects_aliasing_and_bad_tables(gpu_device):
     assert not ck.any() and not cv.any()
 
 
+def _epilogue_problem(device, dtype, dim, layout, positions, n, seed):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = strided_over_storage((1, 8, len(positions), dim), dtype, device, layout, gen, scale=2.0)[1]
+    fk = strided_over_storage((1, 2, len(positions), dim), dtype, device, layout, gen, scale=2.0)[1]
+    fv = strided_over_storage((1, 2, len(positions), dim), dtype, device, layout, gen, scale=0.5)[1]
+    cache = [torch.randn(1, 2, n, dim, device=device, generator=gen).to(dtype) for _ in range(2)]
+    weights = [(1 + 0.25 * torch.randn(dim, device=device, generator=gen)).to(dtype) for _ in range(2)]
+    return q, fk, fv, cache, weights
+
+
+def _norm_epilogue(q, q_out, fk, fv, cache, cos, sin, plan, weights, eps):
+    from kv_cache_repair_amd import _native
+
+    st = _native.i64_array(sum((_native.strides3(t) for t in (q, q_out, fk, fv, *cache)), []))
+    cs = _native.i64_array([int(cos.stride(-2)), int(cos.stride(-1)), int(sin.stride(-2)), int(sin.stride(-1))])
+    return _native.lib().kvr_rope_scatter_kv_norm(
+        q.data_ptr(), q_out.data_ptr(), fk.data_ptr(), fv.data_ptr(), cache[0].data_ptr(), cache[1].data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), plan.positions.data_ptr(), q.shape[2], q.shape[1], fk.shape[1],
+        cache[0].shape[2], q.shape[3], st, cs, weights[0].data_ptr() if weights[0] is not None else None,
+        weights[1].data_ptr() if weights[1] is not None else None, eps[0], eps[1], _native.DTYPE_CODES[q.dtype],
+        _native.stream_handle(q.device))
+
+
+def _rms_rows(x, weight, eps):
+    """kvr_rms_norm over the last dim of ``x`` (made contiguous), [.., D] -> same shape."""
+    from kv_cache_repair_amd import _native
+
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    dim = x.shape[-1]
+    status = _native.lib().kvr_rms_norm(x.data_ptr(), None, None, out.data_ptr(), weight.data_ptr(),
+                                        x.numel() // dim, dim, _native.i64_array([dim] * 4), eps,
+                                        _native.DTYPE_CODES[x.dtype], _native.stream_handle(x.device))
+    assert status == 0
+    return out
+
+
+@pytest.mark.parametrize("layout", ["dense", "token_major"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dim", [64, 128])
+def test_epilogue_with_head_norms_is_rmsnorm_then_epilogue_bit_for_bit(gpu_device, dtype, dim, layout):
+    """kvr_rope_scatter_kv_norm (Qwen3's q_norm / k_norm folded into the fresh-row
+    epilogue) against the two steps it replaces, kvr_rms_norm of q and k then
+    kvr_rope_scatter_kv: identical bits in q_out and in the whole caches; and
+    against HF's Qwen3RMSNorm + apply_rotary_pos_emb + index_copy_ within the
+    2-ulp bound the norm kernel meets against the eager norm."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+    ia = ops()
+    positions = [0, 3, 4, 8, 9, 63, 64, 129, 200, 4000]
+    n = 4001
+    plan = ia.IndexedPlan(positions, n).to(gpu_device)
+    q, fk, fv, cache, weights = _epilogue_problem(gpu_device, dtype, dim, layout, positions, n, seed=dim)
+    eps = (1e-6, 1e-5)
+    cos, sin = rotary_tables(positions, dim, dtype, gpu_device, theta=1e6)
+    fused_q = torch.empty(1, 8, len(positions), dim, device=gpu_device, dtype=dtype)
+    fused_cache = [c.clone() for c in cache]
+    assert _norm_epilogue(q, fused_q, fk, fv, fused_cache, cos, sin, plan, weights, eps) == 0
+    two_step_q = torch.empty_like(fused_q)
+    two_step_cache = [c.clone() for c in cache]
+    qn, kn = _rms_rows(q, weights[0], eps[0]), _rms_rows(fk, weights[1], eps[1])
+    ia.rope_indexed_kv_scatter_(qn, two_step_q, *two_step_cache, kn, fv, cos, sin, plan)
+    torch.cuda.synchronize()
+    assert same_bits(fused_q, two_step_q)
+    assert same_bits(fused_cache[0], two_step_cache[0]) and same_bits(fused_cache[1], two_step_cache[1])
+
+    norms = []
+    for w, e in zip(weights, eps):
+        module = Qwen3RMSNorm(dim, eps=e).to(device=gpu_device, dtype=dtype)
+        with torch.no_grad():
+            module.weight.copy_(w)
+        norms.append(module)
+    with torch.no_grad():
+        hf_q, hf_k = apply_rotary_pos_emb(norms[0](q), norms[1](fk), cos, sin)
+    hf_k_cache = cache[0].clone().index_copy_(2, plan.positions, hf_k)
+    eps_ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -23
+    for ours, hf in ((fused_q, hf_q), (fused_cache[0], hf_k_cache)):
+        o, h = ours.float(), hf.float()
+        # RoPE mixes two normalised elements, each within 2 ulp of HF's: 4 ulp of the larger
+        bound = 4 * eps_ulp * torch.maximum(h.abs(), torch.tensor(2.0 ** -20, device=gpu_device)) + 1e-30
+        assert ((o - h).abs() <= bound).float().mean().item() >= 0.99
+    assert same_bits(fused_cache[1].index_select(2, plan.positions), fv.contiguous())
+
+
+def test_epilogue_with_head_norms_refuses_what_it_cannot_run(gpu_device):
+    ia = ops()
+    positions = [1, 5]
+    plan = ia.IndexedPlan(positions, 8).to(gpu_device)
+    for dtype, weights_given, status in ((torch.float16, 2, -3), (torch.bfloat16, 1, -5)):
+        q, fk, fv, cache, weights = _epilogue_problem(gpu_device, dtype, 64, "dense", positions, 8, seed=1)
+        if weights_given == 1:
+            weights = [weights[0], None]
+        cos, sin = rotary_tables(positions, 64, dtype, gpu_device)
+        kept = [c.clone() for c in cache]
+        assert _norm_epilogue(q, torch.empty_like(q), fk, fv, cache, cos, sin, plan, weights, (1e-6, 1e-6)) == status
+        assert all(same_bits(c, k) for c, k in zip(cache, kept))
+
+
 # --------------------------------------------------------------------------- fused layer elementwise ops
 def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """Units in the last place between same-dtype tensors (monotone integer view)."""

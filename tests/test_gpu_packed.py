@@ -454,8 +454,8 @@ def test_fused_layers_match_native_layer_ops(gpu_device, family, dtype):
 @pytest.mark.parametrize("family", ["llama", "qwen3"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_projection_plans_match_module_linears(gpu_device, family, dtype):
-    """kvr_linear_multi projections (q/k/v in one launch for Llama, separate for
-    Qwen3's per-head norms; gate/up with the SiLU gate in one) vs the modules'
+    """kvr_linear_multi projections (q/k/v in one launch; separate for fp16 Qwen3,
+    whose per-head norms then run on their own; gate/up with the SiLU gate in one) vs the modules'
     library GEMMs: both round fp32 accumulations once, so the refreshed caches
     agree to the bf16/fp16 floor: >= 99% of elements within two ulps, per-row
     cosine >= 0.9999. The plans are cached per layer and follow weight moves."""
@@ -479,7 +479,8 @@ def test_projection_plans_match_module_linears(gpu_device, family, dtype):
     decoder = shim._base_transformer(model)
     plans = [pc._layer_plans(layer) for layer in decoder.layers]
     assert all(p is not None for p in plans)
-    assert all((p.qkv is None) == (family == "qwen3") for p in plans)
+    # q/k/v in one launch, except fp16 Qwen3 (its per-head norms run as separate launches)
+    assert all((p.qkv is None) == (family == "qwen3" and dtype == torch.float16) for p in plans)
     assert pc._layer_plans(decoder.layers[0]) is plans[0]  # cached
     again, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_projections=True)
     assert all(torch.equal(x.keys, y.keys) and torch.equal(x.values, y.values)
