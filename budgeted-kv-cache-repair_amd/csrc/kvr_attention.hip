@@ -1515,6 +1515,91 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     }
 }
 
+// ===========================================================================
+// Single-pass merge (head_dim 64 / 128): one thread per 4 output dims of one
+// (query head, row) -- 32 or 16 threads per row -- combines the row's chunk
+// partials online, kBatch chunks at a time with all their (m, l) and O loads
+// in flight together: running max M, weights exp2(m_c - M), the sum and O
+// rescaled when M grows. No LDS, no barrier, one memory round trip per batch.
+// Grid x = KV head x head group (as the main kernel), y = (group, block of
+// rows) over multi-chunk groups; blocks of single-chunk groups return.
+// ===========================================================================
+constexpr int kFlatThreads = 256;
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kFlatThreads) attn_merge_flat_kernel(AttnArgs a) {
+    using E = elem<T>;
+    using bits = typename E::bits;
+    constexpr int kTpp = D / 4;                    // threads per (query head, row)
+    constexpr int kPpb = kFlatThreads / kTpp;      // rows (x heads) per block
+    constexpr int kBatch = 8;
+    const int GR = a.group_rows;
+    const int per_group = a.qt * GR;
+    const int blocks_per_group = (per_group + kPpb - 1) / kPpb;
+    const int grp = blockIdx.y / blocks_per_group;
+    const int item = (blockIdx.y - grp * blocks_per_group) * kPpb + threadIdx.x / kTpp;
+    const int d0 = (threadIdx.x % kTpp) * 4;
+    const int32_t* gt = group_table(a.sched);
+    const int base = gt[2 * grp];
+    const int n_chunks = gt[2 * grp + 1];
+    if (n_chunks <= 1 || item >= per_group) return;
+    const int hq = item / GR;
+    const int r = item - hq * GR;
+    const int64_t row = static_cast<int64_t>(grp) * GR + r;
+    if (row >= a.n_sel) return;
+    const int kv_head = blockIdx.x / a.n_head_groups;
+    const int hg = blockIdx.x - kv_head * a.n_head_groups;
+    const int q_head = kv_head * a.group + hg * a.qt + hq;
+    // the chunks this row's tile attended: those starting below its causal limit (a prefix)
+    const int32_t tk = rows_kmax(a, static_cast<int64_t>(grp) * GR + (r / kRowTile) * kRowTile, kRowTile);
+    const int32_t* wk = work_table(a.sched) + kWorkInts * base;
+    int nv = 0;
+    while (nv < n_chunks && wk[kWorkInts * nv + 2] < tk) ++nv;
+    const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * GR + r;
+    float m = -INFINITY, l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nv; c0 += kBatch) {
+        f32x2 ml[kBatch];
+        f32x4 o[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int64_t slot = slot0 + static_cast<int64_t>(c0 + j < nv ? c0 + j : nv - 1) * GR;
+            ml[j] = *reinterpret_cast<const f32x2*>(a.ws_ml + slot * 2);
+            o[j] = *reinterpret_cast<const f32x4*>(a.ws_o + slot * D + d0);
+        }
+        float mb = m;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            if (c0 + j < nv) mb = fmaxf(mb, ml[j][0]);
+        const float m_use = mb == -INFINITY ? 0.f : mb;
+        const float f = __builtin_amdgcn_exp2f(m - m_use);  // 0 while m is -inf
+        l *= f;
+        acc *= f;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (c0 + j >= nv) continue;
+            const float w = __builtin_amdgcn_exp2f(ml[j][0] - m_use);
+            l += w * ml[j][1];
+            acc += w * o[j];
+        }
+        m = mb;
+    }
+    const float inv = 1.f / l;
+    bits e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = E::from_float(acc[i] * inv);
+    bits* dst = reinterpret_cast<bits*>(a.out) + q_head * a.os[0] + row * a.os[1];
+    if (sizeof(bits) == 2 && a.out_vec) {
+        uint32_t w0, w1;
+        __builtin_memcpy(&w0, e, 4);
+        __builtin_memcpy(&w1, e + 2, 4);
+        *reinterpret_cast<uint2*>(dst + d0) = uint2{w0, w1};
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(d0 + i) * a.os[2]] = e[i];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host helpers
 // ---------------------------------------------------------------------------
@@ -1634,8 +1719,21 @@ int launch_merge_vec(const AttnArgs& a, int max_chunks, hipStream_t s) {
     return launch_status();
 }
 
+template <typename T, int D>
+int launch_merge_flat(const AttnArgs& a, hipStream_t s) {
+    constexpr int ppb = kFlatThreads / (D / 4);
+    const int64_t blocks_per_group = (static_cast<int64_t>(a.qt) * a.group_rows + ppb - 1) / ppb;
+    const int64_t y = static_cast<int64_t>(a.n_groups) * blocks_per_group;
+    if (y > 65535) return KVR_E_UNSUPPORTED_SHAPE;
+    const dim3 grid(static_cast<unsigned>(a.n_q_heads / a.qt), static_cast<unsigned>(y));
+    attn_merge_flat_kernel<T, D><<<grid, kFlatThreads, 0, s>>>(a);
+    return launch_status();
+}
+
 template <typename T>
 int launch_merge(const AttnArgs& a, int max_chunks, hipStream_t s) {
+    if (a.head_dim == 128) return launch_merge_flat<T, 128>(a, s);
+    if (a.head_dim == 64) return launch_merge_flat<T, 64>(a, s);
     return a.head_dim % 4 == 0 ? launch_merge_vec<T, 4>(a, max_chunks, s) : launch_merge_vec<T, 1>(a, max_chunks, s);
 }
 
@@ -1954,6 +2052,8 @@ int attention_call(const void* q, const void* k, const void* v, void* out, const
         }
     }
     if (workspace_bytes < ws_need || (ws_need > 0 && !workspace)) return KVR_E_WORKSPACE_TOO_SMALL;
+    // the partials are read and written as 16-byte vectors
+    if (ws_need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u)) return KVR_E_INVALID_ARGUMENT;
 
     AttnArgs a;
     memset(&a, 0, sizeof(a));

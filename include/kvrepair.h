@@ -418,7 +418,8 @@ int64_t kvr_attention_workspace_bytes(const int32_t* schedule, int64_t schedule_
  * kvr_attention_schedule for the same positions/heads) are read-only.
  * strides: 12 element strides {head,row,dim} for q, k, v, out (k and v share
  * n_keys rows). `workspace` holds kvr_attention_workspace_bytes() bytes of
- * scratch (no initialisation needed). n_sel == 0 enqueues nothing.
+ * scratch, 16-byte aligned (KVR_E_INVALID_ARGUMENT otherwise; no
+ * initialisation needed). n_sel == 0 enqueues nothing.
  */
 int kvr_packed_causal_attention(const void* q, const void* k, const void* v, void* out, const int64_t* positions,
                                 int64_t n_sel, int32_t n_q_heads, int32_t n_kv_heads, int64_t n_keys,

@@ -242,6 +242,25 @@ def test_workspace_is_zero_when_every_tile_fits_one_chunk():
     assert _native.lib().kvr_attention_workspace_bytes(buf, len(s), 4, 64) == 4 * s[5] * 16 * 66 * 4
 
 
+def test_attention_refuses_a_misaligned_workspace_before_any_launch():
+    """The split-K partials are 16-byte vectors: a workspace that is not 16-byte
+    aligned is refused by the host checks (no device pointer is touched)."""
+    from kv_cache_repair_amd import _native
+
+    lib = _native.lib()
+    positions = list(range(0, 8000, 100))
+    s = schedule(positions, 8000, 4, 2, 64, chunk=256)
+    host = (ctypes.c_int32 * len(s))(*s)
+    need = int(lib.kvr_attention_workspace_bytes(host, len(s), 4, 64))
+    assert need > 0
+    strides = _native.i64_array([64 * len(positions), 64, 1, 64 * 8000, 64, 1, 64 * 8000, 64, 1,
+                                 64 * len(positions), 64, 1])
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the call returns before any launch
+    args = (fake, fake, fake, fake, fake, len(positions), 4, 2, 8000, 64, 0.125, strides, fake, len(s), host)
+    assert lib.kvr_packed_causal_attention(*args, ctypes.c_void_p((1 << 20) + 8), need, 2, None) == -1
+    assert lib.kvr_packed_causal_attention(*args, fake, need - 1, 2, None) == -6  # too small
+
+
 def test_noalloc_attention_refuses_oversized_schedules_before_any_launch():
     from kv_cache_repair_amd import _native
 
