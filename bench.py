@@ -813,6 +813,37 @@ def selected_intervals(length: int, budget: int, count: int) -> list[tuple[int, 
     return intervals
 
 
+def interleaved_latency(calls: dict, warmups: int, repeats: int, seed: int) -> dict:
+    """Per-call wall time of each entry of ``calls``, each call bracketed by
+    ``torch.cuda.synchronize()``: ``warmups`` untimed rounds, then ``repeats``
+    rounds that run every entry once in a shuffled order (benchmark_refresh.py:
+    100-126). Returns {name: median/mean/p95 and the raw samples, in ms}."""
+    names = list(calls)
+    for _ in range(warmups):
+        for name in names:
+            calls[name]()
+            torch.cuda.synchronize()
+    samples = {name: [] for name in names}
+    rng = random.Random(seed)
+    for _ in range(repeats):
+        order = names.copy()
+        rng.shuffle(order)
+        for name in order:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = calls[name]()
+            torch.cuda.synchronize()
+            samples[name].append((time.perf_counter() - t0) * 1000.0)
+            del out
+
+    def summary(values):
+        ordered = sorted(values)
+        return {"median_ms": statistics.median(values), "mean_ms": statistics.mean(values),
+                "p95_ms": ordered[math.ceil(0.95 * len(ordered)) - 1], "raw_ms": values}
+
+    return {name: summary(v) for name, v in samples.items()}
+
+
 def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats: int, seed: int) -> dict:
     """One case of the reference grid: a stale cache of ``length + 8`` tokens (K/V
     ~ N(0,1)) loses 8 tokens at length // 8 and is shifted (untimed); then the
@@ -845,30 +876,7 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
                   for la, lb in zip(outputs["hip"].layers, outputs["reference_packed_sdpa"].layers)
                   for a, b in ((la.keys, lb.keys), (la.values, lb.values)))
     del outputs
-    names = list(calls)
-    for _ in range(warmups):
-        for name in names:
-            calls[name]()
-            torch.cuda.synchronize()
-    samples = {name: [] for name in names}
-    rng = random.Random(seed)
-    for _ in range(repeats):
-        order = names.copy()
-        rng.shuffle(order)
-        for name in order:
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            out = calls[name]()
-            torch.cuda.synchronize()
-            samples[name].append((time.perf_counter() - t0) * 1000.0)
-            del out
-
-    def summary(values):
-        ordered = sorted(values)
-        return {"median_ms": statistics.median(values), "mean_ms": statistics.mean(values),
-                "p95_ms": ordered[math.ceil(0.95 * len(ordered)) - 1], "raw_ms": values}
-
-    lat = {name: summary(v) for name, v in samples.items()}
+    lat = interleaved_latency(calls, warmups, repeats, seed)
     return {"metric": "refresh-only latency (ms), reference benchmark grid", "length": length,
             "interval_count": count, "token_budget": budget, "intervals": intervals,
             "causal_query_key_pairs": sum(p + 1 for p in positions), "position_shift": alignment["position_shift"],
@@ -926,12 +934,21 @@ def run_workload(args, workload: Workload, device) -> dict:
     roofline, north = rooflines(kernels, workload.name)
 
     reference = None
+    interleaved = None
     if not args.no_reference:
-        ref_ms = time_steps(lambda: reference_stage(model, old, old_ids, new_ids, intervals), args.steps,
-                            max(1, args.warmup))
+        ref_step = lambda: reference_stage(model, old, old_ids, new_ids, intervals)  # noqa: E731
+        ref_ms = time_steps(ref_step, args.steps, max(1, args.warmup))
         reference = {"ms_per_step": ref_ms, "speedup": ref_ms / ms,
                      "what": "reference eager path on the same GPU: per-layer rotate chain + cats, clone_cache, "
                              "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv"}
+        if args.interleaved_repeats > 0:
+            lat = interleaved_latency({"hip": step, "reference_same_gpu": ref_step}, args.interleaved_warmups,
+                                      args.interleaved_repeats, 71)
+            interleaved = {"warmups": args.interleaved_warmups, "repeats": args.interleaved_repeats, "seed": 71,
+                           "speedup_median": lat["reference_same_gpu"]["median_ms"] / lat["hip"]["median_ms"],
+                           "latency": lat,
+                           "method": "each call bracketed by torch.cuda.synchronize(), both paths once per round in "
+                                     "a shuffled order"}
     scoring = scoring_measurement(model, new_ids, device) if headline else None
     del old
     if args.no_cpu_baseline:
@@ -959,7 +976,7 @@ def run_workload(args, workload: Workload, device) -> dict:
         "kernel_timing": "HIP events around 5 replays of a graph of 20 back-to-back launches of each libkvrepair "
                          "call with the stage's shapes (device time only); kvr_linear_multi = one layer's four "
                          "projections, per call",
-        "reference_same_gpu": reference, "checks": checks, "selection_scoring": scoring,
+        "reference_same_gpu": reference, "interleaved": interleaved, "checks": checks, "selection_scoring": scoring,
         "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
     }
     return line
@@ -975,6 +992,10 @@ def main(argv=None) -> int:
     parser.add_argument("--grid", action="store_true", help="the reference benchmark's grid (one line per case)")
     parser.add_argument("--grid-repeats", type=int, default=20)
     parser.add_argument("--grid-warmups", type=int, default=10)
+    parser.add_argument("--interleaved-repeats", type=int, default=20,
+                        help="rounds of per-call timing, this build and the reference stage in shuffled order "
+                             "(0 skips); reported beside the bracketed value, which it does not change")
+    parser.add_argument("--interleaved-warmups", type=int, default=10)
     parser.add_argument("--cpu-layers", type=int, default=4, help="layers in the bounded CPU-baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-reference", action="store_true", help="skip the same-GPU reference stage and checks")

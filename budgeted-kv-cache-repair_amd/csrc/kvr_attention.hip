@@ -793,6 +793,68 @@ __device__ inline void lds_dma16(const char* src, char* dst) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 }
 
+// The same load from a wave-uniform base (SGPRs) plus a 32-bit per-lane byte
+// offset: no per-lane address arithmetic.
+__device__ inline void lds_dma16(const char* base, uint32_t off, char* dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)dst)));
+    // the base is wave-uniform; reading it from the first lane keeps it in
+    // SGPRs even where the compiler cannot prove that (free where it can).
+    // readfirstlane returns int: each half goes through uint32_t so the low
+    // half is zero-extended, not sign-extended, into the 64-bit address.
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b))));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b >> 32))));
+    const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(sb), "s"(m0)
+                 : "memory", "m0");
+}
+
+// A wave's share of the direct loads of one 128-key step of K or V. Load p of
+// wave w fills 1 KB block b = 8 p + w of the staged tile: lane L writes the
+// swizzled position (row, c') = divmod(64 b + L, D / 8), i.e. key row
+// p * kRows + r0 with r0 = (64 w + L) / (D / 8), and loads piece c' ^ swz(row)
+// of that row. kRows is a multiple of D / 8, so the swizzle, and with it the
+// lane's byte offset from the load's first row, is the same for every load and
+// every step: only wave-uniform bases change.
+template <int D>
+struct StepLoads {
+    using C = PairCfg<D>;
+    static constexpr int kRows = 512 / C::c8;  // key rows one load instruction of the 8 waves covers
+    static constexpr int kLoads = kPairStepKeys / kRows;
+    static_assert(kLoads == C::loads, "one load per 1 KB block");
+    int r0;
+    int c;
+
+    __device__ inline void init(int wave, int lane) {
+        r0 = (64 * wave + lane) / C::c8;
+        c = lane % C::c8;
+    }
+    __device__ inline uint32_t lane_offset(int64_t stride, bool is_v) const {
+        const int swz = is_v ? C::vswz(r0) : C::kswz(r0);
+        return static_cast<uint32_t>(r0 * stride * 2 + 16 * (c ^ swz));
+    }
+    // Step `first` (its first key row within the chunk) of a tensor whose
+    // chunk starts at `base`; rows past the chunk's n keys re-read its last
+    // row (in bounds), only in a chunk's last step.
+    __device__ inline void issue(const char* base, int64_t stride, uint32_t lane_off, int32_t first, int32_t n,
+                                 char* buf, int wave, bool is_v) const {
+        if (first + kPairStepKeys <= n) {
+            const char* step = base + static_cast<int64_t>(first) * stride * 2;
+#pragma unroll
+            for (int p = 0; p < kLoads; ++p)
+                lds_dma16(step + static_cast<int64_t>(p * kRows) * stride * 2, lane_off, buf + (8 * p + wave) * 1024);
+        } else {
+            const int swz = is_v ? C::vswz(r0) : C::kswz(r0);
+#pragma unroll
+            for (int p = 0; p < kLoads; ++p) {
+                const int32_t key = min(first + p * kRows + r0, n - 1);
+                lds_dma16(base + (static_cast<int64_t>(key) * stride + 8 * (c ^ swz)) * 2, buf + (8 * p + wave) * 1024);
+            }
+        }
+    }
+};
+
 // HILO: probabilities enter PV as a hi + lo pair of 16-bit values (fp32-class,
 // the reference Triton kernel's precision); otherwise each is rounded to the
 // input dtype before PV, as the SDPA path the packed executor replaces rounds it.
@@ -996,18 +1058,22 @@ struct PairWave {
     // the scheduling barriers keep this order.
     // mask: some key may lie beyond some row's position (wave-uniform).
     __device__ inline void step(const char* Ks, const char* Vs, bool mask, int32_t key0, int lj, float scale_log2) {
+        v8 vf[DT];
+        v8 kf[DS][2];
+        read_v(Vs, vf);
+        read_k(Ks, kf);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(kf, vf, mask, key0, lj, scale_log2);
+    }
+
+    // The sub-tile's work once its K and V fragments are in registers.
+    __device__ inline void compute(const v8 (&kf)[DS][2], const v8 (&vf)[DT], bool mask, int32_t key0, int lj,
+                                   float scale_log2) {
         f32x4 s0[2], s1[2];
         float x0[2][4], x1[2][4];
         u32x4 h0, l0, h1, l1;
-        v8 vf[DT];
-        {
-            v8 kf[DS][2];
-            read_v(Vs, vf);
-            read_k(Ks, kf);
-            __builtin_amdgcn_sched_barrier(0);
-            qk(0, kf, s0);
-            qk(1, kf, s1);
-        }
+        qk(0, kf, s0);
+        qk(1, kf, s1);
         __builtin_amdgcn_sched_barrier(0);
         if (mask) {
             apply_mask(s0, key0, lj);
@@ -1022,6 +1088,11 @@ struct PairWave {
         pv(1, vf, h1, l1);
     }
 };
+
+template <typename T, int D, int RT, bool HILO>
+__device__ inline void pair_finish(const AttnArgs& a, PairWave<T, D, HILO>& w, char* smem, int hp, int rt, int kq,
+                                   int lane, int lq, int lj, int work, int n_chunks, int head0, int64_t row0,
+                                   int32_t kmax, int32_t key_begin);
 
 template <typename T, int D, int RT, bool HILO>
 __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
@@ -1063,19 +1134,13 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
     // lane L of block b writes swizzled position (row, c') = divmod(64 b + L, D/8)
     // and so loads piece c' ^ (row mod D/8) of that key row. Rows past the chunk
     // end re-read its last row (in bounds); they are masked or zeroed later.
+    StepLoads<D> sl;
+    sl.init(wave, lane);
+    const uint32_t koff = sl.lane_offset(a.ks[1], false);
+    const uint32_t voff = sl.lane_offset(a.vs[1], true);
     auto load = [&](int i, char* stage) {
-        const int32_t base = kPairStepKeys * i;
-#pragma unroll
-        for (int p = 0; p < C::loads; ++p) {
-            const int b = p * 8 + wave;                    // 1 KB block of the tensor
-            const int idx = 64 * b + lane;
-            const int row = idx / C::c8;
-            const int32_t key = min(base + row, n_keys_chunk - 1);
-            const int64_t koff = static_cast<int64_t>(key) * a.ks[1] + 8 * ((idx % C::c8) ^ C::kswz(row));
-            const int64_t voff = static_cast<int64_t>(key) * a.vs[1] + 8 * ((idx % C::c8) ^ C::vswz(row));
-            lds_dma16(kbase + koff * 2, stage + b * 1024);
-            lds_dma16(vbase + voff * 2, stage + C::tensor_bytes + b * 1024);
-        }
+        sl.issue(kbase, a.ks[1], koff, kPairStepKeys * i, n_keys_chunk, stage, wave, false);
+        sl.issue(vbase, a.vs[1], voff, kPairStepKeys * i, n_keys_chunk, stage + C::tensor_bytes, wave, true);
     };
 
     // Prologue, one round trip: the row positions and Q fragments are loaded
@@ -1149,7 +1214,34 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
                        a.scale_log2);
         }
     }
+    pair_finish<T, D, RT, HILO>(a, w, smem, hp, rt, kq, lane, lq, lj, work, n_chunks, head0, row0, kmax, key_begin);
+}
 
+// LDS bytes of pair_finish's exchange: per (head pair, row tile), class and
+// head the D / 16 - D / 16 / X d tiles the class does not own (64 lanes x 16
+// bytes each), then (m, l) per class, head and lane.
+__host__ __device__ constexpr size_t pair_exchange_bytes(int D, int RT) {
+    return RT == 4 ? 0
+                   : static_cast<size_t>(2 * RT) * (8 / (2 * RT)) * 2 *
+                         ((D / 16 - D / 16 / (8 / (2 * RT))) * 64 * 16 + 64 * 8);
+}
+
+// Row sums, the combine of the key classes of each (head pair, row tile)
+// through LDS (every wave of the block calls it, after its last step), and the
+// output (one chunk) or the chunk's partial (m, l, O). With X key classes,
+// wave kq of a (head pair, row tile) combines and writes d tiles
+// [SL kq, SL (kq + 1)) of all X classes' O, so the combine's LDS reads and the
+// stores are spread over every wave: each wave first puts its (m, l) and the
+// d tiles it does not own into LDS (f32x4 per lane and tile).
+template <typename T, int D, int RT, bool HILO>
+__device__ inline void pair_finish(const AttnArgs& a, PairWave<T, D, HILO>& w, char* smem, int hp, int rt, int kq,
+                                   int lane, int lq, int lj, int work, int n_chunks, int head0, int64_t row0,
+                                   int32_t kmax, int32_t key_begin) {
+    using W = PairWave<T, D, HILO>;
+    constexpr int X = 8 / (2 * RT);  // key classes per head pair
+    constexpr int GR = kRowTile * RT;
+    constexpr int SL = W::DT / X;    // d tiles each wave writes
+    static_assert(SL * X == W::DT, "d tiles split evenly over the key classes");
     // ---- row sums: row 0 of the sum tile, i.e. element 0 of lane lq (lj = 0);
     // the other lanes hold zeros, so the sum over the lane groups broadcasts it ----
     float l_run[2];
@@ -1160,59 +1252,80 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
         l += __shfl_xor(l, 32);
         l_run[t] = l;
     }
-    // ---- combine the X key classes of each (head pair, row tile) in LDS ----
-    if (X > 1) {
-        constexpr int kX = 2 * (W::DT * 4 + 2);  // exchanged floats per lane: O, m, l of both heads
-        __syncthreads();  // every wave is done with the K/V stages
-        if (kq > 0) {
-            float* xch = reinterpret_cast<float*>(smem) + ((hp * RT + rt) * (X - 1) + kq - 1) * kX * 64;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int dt = 0; dt < W::DT; ++dt)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) xch[((t * W::DT + dt) * 4 + e) * 64 + lane] = w.o[t][dt][e];
-                xch[(2 * W::DT * 4 + 2 * t) * 64 + lane] = w.m_run[t];
-                xch[(2 * W::DT * 4 + 2 * t + 1) * 64 + lane] = l_run[t];
-            }
-        }
-        __syncthreads();
-        if (kq > 0) return;
+    f32x4 res[2][SL];  // this wave's d tiles [SL kq, SL (kq + 1)) of both heads
+    float m_out[2];
+    if constexpr (X == 1) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            float mb[X > 1 ? X - 1 : 1], lb[X > 1 ? X - 1 : 1];
-            float m = w.m_run[t];
+            m_out[t] = w.m_run[t];
 #pragma unroll
-            for (int c = 0; c < X - 1; ++c) {
-                const float* xch = reinterpret_cast<const float*>(smem) + ((hp * RT + rt) * (X - 1) + c) * kX * 64;
-                mb[c] = xch[(2 * W::DT * 4 + 2 * t) * 64 + lane];
-                lb[c] = xch[(2 * W::DT * 4 + 2 * t + 1) * 64 + lane];
-                m = fmaxf(m, mb[c]);
+            for (int j = 0; j < SL; ++j) res[t][j] = w.o[t][j];
+        }
+    } else {
+        // exchange layout (head pair, row tile) -> class c -> head t -> the
+        // W::DT - SL d tiles c does not own, in order -> lane; then (m, l)
+        constexpr int kTiles = W::DT - SL;
+        const int unit = hp * RT + rt;
+        f32x4* xo = reinterpret_cast<f32x4*>(smem);
+        float2* xml = reinterpret_cast<float2*>(smem + static_cast<size_t>(2 * RT) * X * 2 * kTiles * 64 * 16);
+        auto o_at = [&](int c, int t, int dt) {  // dt not owned by class c
+            const int k = dt < SL * c ? dt : dt - SL;
+            return xo + ((((unit * X + c) * 2 + t) * kTiles + k) * 64 + lane);
+        };
+        __syncthreads();  // every wave is done with the K/V stages
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int dt = 0; dt < W::DT; ++dt)
+                if (dt / SL != kq) *o_at(kq, t, dt) = w.o[t][dt];
+            xml[((unit * X + kq) * 2 + t) * 64 + lane] = float2{w.m_run[t], l_run[t]};
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float mc[X], lc[X];
+            float m = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < X; ++c) {
+                const float2 ml = c == kq ? float2{w.m_run[t], l_run[t]} : xml[((unit * X + c) * 2 + t) * 64 + lane];
+                mc[c] = ml.x;
+                lc[c] = ml.y;
+                m = fmaxf(m, mc[c]);
             }
-            if (m == -INFINITY) continue;  // no key of the chunk is visible to this row
-            const float fa = __builtin_amdgcn_exp2f(w.m_run[t] - m);  // exp2(-inf) = 0 for an empty class
-            float l = l_run[t] * fa;
+            // a row with no visible key in the chunk keeps O = 0, l = 0, m = -inf
+            const float m_use = m == -INFINITY ? 0.f : m;
+            float l = 0.f;
 #pragma unroll
-            for (int dt = 0; dt < W::DT; ++dt) w.o[t][dt] *= fa;
+            for (int j = 0; j < SL; ++j) res[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < X - 1; ++c) {
-                const float* xch = reinterpret_cast<const float*>(smem) + ((hp * RT + rt) * (X - 1) + c) * kX * 64;
-                const float fb = __builtin_amdgcn_exp2f(mb[c] - m);
-                l += lb[c] * fb;
+            for (int c = 0; c < X; ++c) {
+                const float f = __builtin_amdgcn_exp2f(mc[c] - m_use);  // 0 for an empty class
+                l += lc[c] * f;
 #pragma unroll
-                for (int dt = 0; dt < W::DT; ++dt)
+                for (int j = 0; j < SL; ++j) {
+                    f32x4 oc;
+                    if (c == kq) {
+                        // own d tiles: a select over the registers (no dynamic register indexing)
+                        oc = w.o[t][j];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) w.o[t][dt][e] += xch[((t * W::DT + dt) * 4 + e) * 64 + lane] * fb;
+                        for (int k = 1; k < X; ++k)
+                            if (k == kq) oc = w.o[t][SL * k + j];
+                    } else {
+                        oc = *o_at(c, t, SL * kq + j);
+                    }
+                    res[t][j] += oc * f;
+                }
             }
-            w.m_run[t] = m;
+            m_out[t] = m;
             l_run[t] = l;
         }
     }
 
-    // ---- output (one chunk) or the chunk's partial ----
+    // ---- output (one chunk) or the chunk's partial: d tiles [SL kq, SL (kq + 1)) ----
     const int r = kRowTile * rt + lq;  // row within the group
     const int64_t row = row0 + lq;
     if (kmax <= key_begin || row >= a.n_sel) return;  // the tile does not attend into this chunk
+    const int dt0 = X == 1 ? 0 : SL * kq;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int q_head = head0 + t;
@@ -1220,25 +1333,26 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
             const float inv = 1.f / l_run[t];
             uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + q_head * a.os[0] + row * a.os[1];
 #pragma unroll
-            for (int dt = 0; dt < W::DT; ++dt) {
+            for (int j = 0; j < SL; ++j) {
                 uint16_t e[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) e[i] = elem<T>::from_float(w.o[t][dt][i] * inv);
+                for (int i = 0; i < 4; ++i) e[i] = elem<T>::from_float(res[t][j][i] * inv);
+                const int d0 = 16 * (dt0 + j) + 4 * lj;
                 if (a.out_vec) {
-                    *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * lj) =
+                    *reinterpret_cast<uint2*>(dst + d0) =
                         uint2{e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16)};
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) dst[(16 * dt + 4 * lj + i) * a.os[2]] = e[i];
+                    for (int i = 0; i < 4; ++i) dst[(d0 + i) * a.os[2]] = e[i];
                 }
             }
         } else {
             const int64_t slot = (static_cast<int64_t>(q_head) * a.n_work + work) * GR + r;
             float* po = a.ws_o + slot * D;
 #pragma unroll
-            for (int dt = 0; dt < W::DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lj) = w.o[t][dt];
-            if (lj == 0) {
-                a.ws_ml[slot * 2 + 0] = w.m_run[t];
+            for (int j = 0; j < SL; ++j) *reinterpret_cast<f32x4*>(po + 16 * (dt0 + j) + 4 * lj) = res[t][j];
+            if (kq == 0 && lj == 0) {
+                a.ws_ml[slot * 2 + 0] = m_out[t];
                 a.ws_ml[slot * 2 + 1] = l_run[t];
             }
         }
@@ -1652,9 +1766,7 @@ int launch_tile_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
 template <typename T, int D, int RT, bool HILO>
 int launch_pair_inst(const AttnArgs& a, dim3 grid, hipStream_t s) {
     constexpr size_t bytes = PairCfg<D>::bytes;
-    constexpr int X = 8 / (2 * RT);
-    static_assert(X == 1 || bytes >= static_cast<size_t>(2 * RT * (X - 1)) * 2 * (D / 16 * 4 + 2) * 64 * 4,
-                  "key-class exchange fits the stages");
+    static_assert(bytes >= pair_exchange_bytes(D, RT), "key-class exchange fits the stages");
     static const bool ok = allow_lds(attn_pair_kernel<T, D, RT, HILO>, bytes);
     if (!ok) return KVR_E_LAUNCH_FAILED;
     attn_pair_kernel<T, D, RT, HILO><<<grid, kPairThreads, bytes, s>>>(a);
