@@ -1664,11 +1664,17 @@ __global__ void __launch_bounds__(kFlatThreads) attn_merge_flat_kernel(AttnArgs 
     const int kv_head = blockIdx.x / a.n_head_groups;
     const int hg = blockIdx.x - kv_head * a.n_head_groups;
     const int q_head = kv_head * a.group + hg * a.qt + hq;
-    // the chunks this row's tile attended: those starting below its causal limit (a prefix)
-    const int32_t tk = rows_kmax(a, static_cast<int64_t>(grp) * GR + (r / kRowTile) * kRowTile, kRowTile);
-    const int32_t* wk = work_table(a.sched) + kWorkInts * base;
-    int nv = 0;
-    while (nv < n_chunks && wk[kWorkInts * nv + 2] < tk) ++nv;
+    // The chunks this row's tile attended: those starting below its causal
+    // limit (a prefix). A one-tile group's key range ends at that limit, so
+    // its tile attends every chunk; only groups of several tiles need the
+    // (dependent) position and work-table reads.
+    int nv = n_chunks;
+    if (GR > kRowTile) {
+        const int32_t tk = rows_kmax(a, static_cast<int64_t>(grp) * GR + (r / kRowTile) * kRowTile, kRowTile);
+        const int32_t* wk = work_table(a.sched) + kWorkInts * base;
+        nv = 0;
+        while (nv < n_chunks && wk[kWorkInts * nv + 2] < tk) ++nv;
+    }
     const int64_t slot0 = (static_cast<int64_t>(q_head) * a.n_work + base) * GR + r;
     float m = -INFINITY, l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
