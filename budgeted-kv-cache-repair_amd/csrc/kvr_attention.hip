@@ -113,6 +113,11 @@ struct AttnArgs {
 __host__ __device__ inline const int32_t* group_table(const int32_t* s) { return s + kHeader; }
 __host__ __device__ inline const int32_t* work_table(const int32_t* s) { return s + kHeader + 2 * s[H_NGROUPS]; }
 
+// The device schedule's work table, located from the group count the host
+// read from the same schedule (one dependent load fewer than reading the
+// device header first).
+__device__ inline const int32_t* work_table_of(const AttnArgs& a) { return a.sched + kHeader + 2 * a.n_groups; }
+
 // Causal key limit (exclusive) of rows [first, first + count) clipped to n_sel; 0 when empty.
 __device__ inline int32_t rows_kmax(const AttnArgs& a, int64_t first, int64_t count) {
     if (first >= a.n_sel) return 0;
@@ -330,7 +335,7 @@ attn_mfma_kernel(AttnArgs a) {
     const int lj = lane >> 4;
 
     const int work = blockIdx.y;
-    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int32_t* wk = work_table_of(a) + kWorkInts * work;
     const int grp = wk[0];
     const int32_t key_begin = wk[2];
     const int32_t key_end = wk[3];
@@ -534,7 +539,7 @@ __global__ void __launch_bounds__(128 * QT) attn_tile_kernel(AttnArgs a) {
     const int kh = wave / QT;  // key half: sub-tiles 2i + kh
 
     const int work = blockIdx.y;
-    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int32_t* wk = work_table_of(a) + kWorkInts * work;
     const int grp = wk[0];
     const int32_t key_begin = wk[2];
     const int32_t key_end = wk[3];
@@ -1113,7 +1118,7 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
     const int kq = (wave >> 1) / RT;      // key class
 
     const int work = blockIdx.y;
-    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int32_t* wk = work_table_of(a) + kWorkInts * work;
     const int grp = wk[0];
     const int32_t key_begin = wk[2];
     const int32_t key_end = wk[3];
@@ -1379,7 +1384,7 @@ __global__ void __launch_bounds__(kGenThreads) attn_generic_kernel(AttnArgs a) {
 
     const int tid = threadIdx.x;
     const int work = blockIdx.y;
-    const int32_t* wk = work_table(a.sched) + kWorkInts * work;
+    const int32_t* wk = work_table_of(a) + kWorkInts * work;
     const int grp = wk[0];
     const int64_t key_begin = wk[2];
     const int64_t key_end = wk[3];
@@ -1504,7 +1509,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(AttnArgs a) {
     const int base = gt[2 * grp];
     const int n_chunks = gt[2 * grp + 1];
     if (n_chunks <= 1) return;
-    const int32_t* wk = work_table(a.sched) + kWorkInts * base;
+    const int32_t* wk = work_table_of(a) + kWorkInts * base;
     float* Red = reinterpret_cast<float*>(smem);          // [RB][kSlices][D] (16-byte aligned)
     float* W = Red + RB * kSlices * D;                     // [RB][n_chunks]
     float* Linv = W + RB * n_chunks;                       // [RB]
@@ -1671,7 +1676,7 @@ __global__ void __launch_bounds__(kFlatThreads) attn_merge_flat_kernel(AttnArgs 
     int nv = n_chunks;
     if (GR > kRowTile) {
         const int32_t tk = rows_kmax(a, static_cast<int64_t>(grp) * GR + (r / kRowTile) * kRowTile, kRowTile);
-        const int32_t* wk = work_table(a.sched) + kWorkInts * base;
+        const int32_t* wk = work_table_of(a) + kWorkInts * base;
         nv = 0;
         while (nv < n_chunks && wk[kWorkInts * nv + 2] < tk) ++nv;
     }
