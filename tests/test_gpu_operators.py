@@ -516,6 +516,10 @@ ORACLE_CASES = {
     "token-major, scale 0.17": (17, 128, 259, 6, 3, ("token_major", "token_major", "sparse"), 0.17),
     "sparse, scale 0.17": (17, 128, 259, 6, 3, ("sparse", "sparse", "sparse"), 0.17),
     "padded heads": (33, 64, 700, 8, 2, ("padded", "sparse", "padded"), None),
+    # four query heads per KV head with K/V rows H*D apart: the head-pair kernel's
+    # strided direct-to-LDS loads, with 16-row groups and with 64-row groups
+    "head pairs, token-major, 16-row groups": (40, 128, 700, 8, 2, ("token_major",) * 3, None),
+    "head pairs, token-major, 64-row groups": (1100, 64, 1200, 32, 8, ("token_major",) * 3, None),
 }
 CUSTOM_POSITIONS = [0, 1, 63, 64, 65, 66, 71, 99, 111, 127, 128, 193, 249, 250, 255, 256, 258]
 
