@@ -37,8 +37,10 @@ Other modes (secondary lines, not the headline):
 from __future__ import annotations
 
 import argparse
+import contextlib
 import copy
 import ctypes
+import gc
 import json
 import math
 import os
@@ -212,18 +214,35 @@ def hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=None):
     return cache
 
 
+@contextlib.contextmanager
+def no_gc():
+    """Python's cyclic garbage collector paused (timed regions of both paths:
+    a collection pass during a few hundred launches is a host stall of tens
+    of ms)."""
+    enabled = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if enabled:
+            gc.enable()
+
+
 def time_steps(fn, steps, warmup):
     for _ in range(warmup):
         out = fn()
         torch.cuda.synchronize()
         del out
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        out = fn()
-        del out
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1000.0 / steps
+    with no_gc():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = fn()
+            del out
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    return elapsed * 1000.0 / steps
 
 
 # ----------------------------------------------------------------------------- reference stage (same GPU)
@@ -319,6 +338,40 @@ def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
 
 
 # ----------------------------------------------------------------------------- end-to-end parity at full depth
+def sdpa_backend_used(fn) -> dict:
+    """Run ``fn`` once (untimed) and record which fused backend torch picks for
+    the first ``scaled_dot_product_attention`` call it makes, with that call's
+    own arguments (the reference path's boolean mask and repeat_kv'd K/V)."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend
+
+    seen = {}
+    original = F.scaled_dot_product_attention
+
+    def spy(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None, **kwargs):
+        if not seen:
+            try:
+                choice = torch._fused_sdp_choice(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                                                 is_causal=is_causal, scale=scale, **kwargs)
+                seen["backend"] = SDPBackend(choice).name
+            except Exception as exc:  # private API: record that it could not be asked
+                seen["backend"] = f"unknown ({type(exc).__name__})"
+            seen["query"] = list(query.shape)
+            seen["key"] = list(key.shape)
+            seen["mask"] = None if attn_mask is None else f"{attn_mask.dtype} {list(attn_mask.shape)}"
+        return original(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p, is_causal=is_causal,
+                        scale=scale, **kwargs)
+
+    F.scaled_dot_product_attention = spy
+    try:
+        out = fn()
+        torch.cuda.synchronize()
+        del out
+    finally:
+        F.scaled_dot_product_attention = original
+    return seen
+
+
 def row_errors(a: torch.Tensor, b: torch.Tensor) -> dict:
     """max-abs, RMSE and the smallest per-row cosine of a against b (rows = head_dim vectors)."""
     a, b = a.double(), b.double()
@@ -813,6 +866,19 @@ def selected_intervals(length: int, budget: int, count: int) -> list[tuple[int, 
     return intervals
 
 
+def _interleave(calls, names, samples, rng, repeats):
+    for _ in range(repeats):
+        order = names.copy()
+        rng.shuffle(order)
+        for name in order:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = calls[name]()
+            torch.cuda.synchronize()
+            samples[name].append((time.perf_counter() - t0) * 1000.0)
+            del out
+
+
 def interleaved_latency(calls: dict, warmups: int, repeats: int, seed: int) -> dict:
     """Per-call wall time of each entry of ``calls``, each call bracketed by
     ``torch.cuda.synchronize()``: ``warmups`` untimed rounds, then ``repeats``
@@ -825,16 +891,8 @@ def interleaved_latency(calls: dict, warmups: int, repeats: int, seed: int) -> d
             torch.cuda.synchronize()
     samples = {name: [] for name in names}
     rng = random.Random(seed)
-    for _ in range(repeats):
-        order = names.copy()
-        rng.shuffle(order)
-        for name in order:
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            out = calls[name]()
-            torch.cuda.synchronize()
-            samples[name].append((time.perf_counter() - t0) * 1000.0)
-            del out
+    with no_gc():
+        _interleave(calls, names, samples, rng, repeats)
 
     def summary(values):
         ordered = sorted(values)
@@ -940,7 +998,8 @@ def run_workload(args, workload: Workload, device) -> dict:
         ref_ms = time_steps(ref_step, args.steps, max(1, args.warmup))
         reference = {"ms_per_step": ref_ms, "speedup": ref_ms / ms,
                      "what": "reference eager path on the same GPU: per-layer rotate chain + cats, clone_cache, "
-                             "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv"}
+                             "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv",
+                     "sdpa": sdpa_backend_used(ref_step)}
         if args.interleaved_repeats > 0:
             lat = interleaved_latency({"hip": step, "reference_same_gpu": ref_step}, args.interleaved_warmups,
                                       args.interleaved_repeats, 71)
