@@ -14,7 +14,10 @@ One step = one full refresh stage, inputs resident in HBM: shift-cache build
 projections, the norms, the fused fresh-row epilogue (RoPE of the fresh Q/K +
 K/V scatter) and the packed attention. Prefill, tokenisation and selection are
 outside the step, as in the reference benchmark (benchmark_refresh.py:3-9);
-unlike it, the rotation is inside.
+unlike it, the rotation is inside. The build reads the token ids from host
+copies, as repair_after_deletion does (its tokenizer output is on the host), so
+the step issues no device-to-host copy; the reference path keeps its own
+device-id read (cache.py:116-117).
 
 Printed (one JSON line): stage latency (ms per repair over K steps), the same
 stage run the reference way on the same GPU, the device time of every
@@ -205,11 +208,16 @@ def make_request(device, workload: Workload = C3, layers: int | None = None, voc
 
 
 # ----------------------------------------------------------------------------- our stage
-def hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=None):
+def hip_stage(shim, old, old_ids, new_ids, intervals, native_layers=None, host_ids=None):
+    """The refresh stage as repair_after_deletion runs it after selection: the
+    shift-cache build, then the packed refresh in place. ``host_ids`` (the old and
+    edited ids on the host, as the API layer holds them from its tokenizer) let
+    the build read the ids without a device synchronisation."""
     from kv_cache_repair_amd.cache import build_halo_cache
     from kv_cache_repair_amd.kernels.packed_cache import packed_refresh_owned_
 
-    cache, _ = build_halo_cache(shim, old, old_ids, new_ids, 0)
+    build_old, build_new = host_ids if host_ids is not None else (old_ids, new_ids)
+    cache, _ = build_halo_cache(shim, old, build_old, build_new, 0)
     packed_refresh_owned_(shim, cache, new_ids, intervals, native_layers=native_layers)
     return cache
 
@@ -986,7 +994,8 @@ def run_workload(args, workload: Workload, device) -> dict:
     checks = {} if args.no_reference else parity_checks(model, shim, old, old_ids, new_ids, intervals,
                                                         with_control=not args.no_fp32_control)
 
-    step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals)  # noqa: E731
+    host_ids = (old_ids.cpu(), new_ids.cpu())
+    step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals, host_ids=host_ids)  # noqa: E731
     ms = time_steps(step, args.steps, args.warmup)
     kernels = measure_kernels(model, workload, old, old_ids, new_ids, device)
     roofline, north = rooflines(kernels, workload.name)

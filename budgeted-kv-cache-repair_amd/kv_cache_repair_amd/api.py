@@ -187,8 +187,9 @@ def _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text, sele
     alignment = token_alignment_arrays(old_ids[0].numpy(), edited_ids[0].numpy())
     selection = selector(int(edited_ids.shape[1]), int(alignment["new_suffix_start"]))
     shim = OperatorShim(model, tokenizer)
-    old_dev, edited_dev = _to_model_device(model, old_ids), _to_model_device(model, edited_ids)
-    shifted, alignment = build_halo_cache(shim, old_cache, old_dev, edited_dev, halo_tokens=0)
+    edited_dev = _to_model_device(model, edited_ids)
+    # host ids: the shift build reads them without waiting for the device
+    shifted, alignment = build_halo_cache(shim, old_cache, old_ids, edited_ids, halo_tokens=0)
     if int(alignment["new_suffix_start"]) != selection.suffix_start:
         raise RuntimeError("host alignment and shift-cache alignment disagree")
     execution = packed_refresh_owned_(shim, shifted, edited_dev, list(selection.intervals))

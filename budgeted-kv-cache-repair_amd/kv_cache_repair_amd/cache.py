@@ -213,7 +213,9 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     needs recomputation the whole shifted cache (prefix copy, rotated K tail,
     copied V tail, every layer) is written by ONE kvr_shift_cache_build launch
     into freshly allocated, independently owned tensors; the old cache is
-    never mutated.
+    never mutated. The alignment is computed on the host: id tensors already on
+    the CPU (as the API layer holds them) are read without a device
+    synchronisation; device ids are copied to the host once.
     """
     n_old = int(old_input_ids.shape[1])
     n_new = int(new_input_ids.shape[1])
@@ -251,7 +253,8 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
                        tail_rows=tail_rows, shift=align["position_shift"])
     else:
         prefix_cache = clone_cache(old_cache, align["prefix"])
-        recomputed = run_tokens_from_prefix(generator, prefix_cache, new_input_ids[:, align["prefix"]:recompute_end],
+        recomputed = run_tokens_from_prefix(generator, prefix_cache,
+                                            new_input_ids[:, align["prefix"]:recompute_end].to(k0.device),
                                             recompute_end)
         rec = [layer_kv(recomputed, i) for i in range(len(old))]
         _check_uniform(rec, "build_halo_cache")

@@ -147,8 +147,10 @@ def test_every_bf16_pattern_rotates_as_the_reference_eager_chain(gpu_device, dim
         assert torch.equal(ours.view(torch.int16), eager.contiguous().view(torch.int16))
 
 
-def test_build_halo_cache_matches_reference_config1(gpu_device):
-    """tiny Llama, 256 ids, delete positions 64-95 (shift -32)."""
+@pytest.mark.parametrize("ids_on", ["device", "host"])
+def test_build_halo_cache_matches_reference_config1(gpu_device, ids_on):
+    """BASELINE config 1: tiny Llama, 256 ids, delete positions 64-95 (shift -32);
+    the ids given on the device or on the host (as the API layer passes them)."""
     from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache
 
     model = _tiny_llama(gpu_device, torch.float32, heads=4, kv_heads=2, dim=16, layers=2, seed=0)
@@ -158,7 +160,8 @@ def test_build_halo_cache_matches_reference_config1(gpu_device):
     with torch.no_grad():
         old = model(input_ids=old_ids, use_cache=True).past_key_values
     snapshot = [(k.clone(), v.clone()) for k, v in ((l.keys, l.values) for l in old.layers)]
-    ours, meta = build_halo_cache(OperatorShim(model), old, old_ids, new_ids, 0)
+    where = (lambda t: t.cpu()) if ids_on == "host" else (lambda t: t)
+    ours, meta = build_halo_cache(OperatorShim(model), old, where(old_ids), where(new_ids), 0)
     expect, emeta = ref.build_halo_cache(model, old, old_ids, new_ids, 0)
     torch.cuda.synchronize()
     assert meta == emeta
@@ -168,9 +171,11 @@ def test_build_halo_cache_matches_reference_config1(gpu_device):
         assert torch.equal(old.layers[i].keys, snapshot[i][0]) and torch.equal(old.layers[i].values, snapshot[i][1])
 
 
-def test_build_halo_cache_with_changed_boundary_token(gpu_device):
+@pytest.mark.parametrize("ids_on", ["device", "host"])
+def test_build_halo_cache_with_changed_boundary_token(gpu_device, ids_on):
     """A deletion that changes one boundary token: rows [prefix, new_suffix_start)
-    come from a native forward, the tail is rotated (cache.py:116-139)."""
+    come from a native forward, the tail is rotated (cache.py:116-139); ids on
+    the device or on the host."""
     from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache
 
     model = _tiny_llama(gpu_device, torch.float32, seed=1)
@@ -178,7 +183,8 @@ def test_build_halo_cache_with_changed_boundary_token(gpu_device):
     new_ids = torch.tensor([[5, 6, 99, 11, 12, 13, 14]], device=gpu_device)
     with torch.no_grad():
         old = model(input_ids=old_ids, use_cache=True).past_key_values
-    ours, meta = build_halo_cache(OperatorShim(model), old, old_ids, new_ids, 0)
+    where = (lambda t: t.cpu()) if ids_on == "host" else (lambda t: t)
+    ours, meta = build_halo_cache(OperatorShim(model), old, where(old_ids), where(new_ids), 0)
     expect, emeta = ref.build_halo_cache(model, old, old_ids, new_ids, 0)
     assert meta == emeta and meta["mandatory_changed_tokens"] == 1
     for i in range(2):
