@@ -219,7 +219,8 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     """
     n_old = int(old_input_ids.shape[1])
     n_new = int(new_input_ids.shape[1])
-    ids = torch.cat((old_input_ids[0].reshape(-1), new_input_ids[0].reshape(-1).to(old_input_ids.dtype)))
+    ids = torch.cat((old_input_ids[0].reshape(-1),
+                     new_input_ids[0].reshape(-1).to(device=old_input_ids.device, dtype=old_input_ids.dtype)))
     # Everything that does not depend on the id values (cache checks, the
     # output allocation, the launch arguments) is done before the one
     # device-to-host copy of both id rows, which waits for the stream.
