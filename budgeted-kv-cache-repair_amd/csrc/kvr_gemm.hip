@@ -13,18 +13,19 @@
 // applies the SiLU-gated product (the MLP's act_fn(gate) * up) so the two
 // projections never reach HBM.
 //
-// Work split: block = 4 waves x 16 streamed weight rows (64 rows) x one K
-// slice. The slice is walked in chunks of 256 (128 in launches with more blocks
-// than CUs): x[:, chunk] is staged in one of
+// Work split: block = W waves x 16 streamed weight rows x one K slice, W = 4,
+// or 6 / 7 where that makes the grid exactly one block per CU (q/k/v and the
+// gate/up pairs of 8B-shaped models). The slice is walked in chunks of 256 (128
+// in launches with more blocks than CUs): x[:, chunk] is staged in one of
 // two LDS buffers (the next chunk's global loads are in flight while the
-// current one is multiplied) and shared by the 4 waves; W streams into
+// current one is multiplied) and shared by the waves; the weights stream into
 // registers through a ring of 8 loads per lane (one chunk ahead), each load
 // instruction covering whole 128-B lines of 8 rows (one memory request per
 // line: 16-row x 64-B loads in the MFMA layout reach ~25% less bandwidth),
 // and every pair of loads is transposed to MFMA A fragments through a small
-// per-wave LDS tile. Split-K slices (S > 1) write fp32 partial tiles to a
-// workspace and a second launch sums them in slice order, so results are
-// deterministic.
+// per-wave LDS tile. Split-K slices (S > 1) write fp32 partials to a workspace
+// of 64-column tiles and a second launch (or a fused consumer) sums them in
+// slice order, so results are deterministic.
 #include "kvr_internal.h"
 
 #include <string.h>
@@ -32,9 +33,6 @@
 namespace kvr {
 namespace {
 
-#ifndef KVR_GEMM_WAVES
-#define KVR_GEMM_WAVES 4
-#endif
 #ifndef KVR_GEMM_CHUNK_STEPS
 #define KVR_GEMM_CHUNK_STEPS 8
 #endif
@@ -42,11 +40,15 @@ namespace {
 #define KVR_GEMM_RING_CHUNKS 1
 #endif
 
-constexpr int kWaves = KVR_GEMM_WAVES;      // waves per block, 16 streamed weight rows each
-constexpr int kComputeThreads = 64 * kWaves;
-constexpr int kGemmThreads = kComputeThreads;
-constexpr int kTileN = 16 * kWaves;         // streamed weight rows per block
-constexpr int kHalf = kTileN / 2;           // gated: output columns per block
+// Waves per block (16 streamed weight rows each) is a launch parameter: 4, 6 or
+// 7, whichever makes the grid exactly one block per CU (see choose_waves).
+template <int W>
+struct WaveCfg {
+    static constexpr int kThreads = 64 * W;
+    static constexpr int kTileN = 16 * W;      // streamed weight rows per block
+    static constexpr int kHalf = kTileN / 2;   // gated: output columns per block (8 per wave)
+    static constexpr int kRedStride = kTileN + 4;  // fp32 LDS tile of the gated epilogue
+};
 constexpr int kRowsMax = 64;                // M <= 64 (four 16-row MFMA tiles)
 constexpr int kStep = 32;                   // K per MFMA
 constexpr int kSliceChunk = KVR_GEMM_CHUNK_STEPS * kStep;  // split-K slices are whole multiples of this
@@ -56,7 +58,7 @@ static_assert(kRingChunks == 1 || kRingChunks == 2, "chunk buffers alternate wit
 // Staged x chunk of CS k-steps (CS = the W ring depth per chunk): 8 for
 // launches of at most one block per CU, 4 (half the LDS, chunks turned over
 // twice as often) where some CUs run two blocks.
-template <int CS>
+template <int CS, int W>
 struct ChunkCfg {
     static constexpr int kChunkSteps = CS;            // k-steps per staged x chunk = W ring depth
     static constexpr int kChunk = CS * kStep;         // K per chunk
@@ -64,21 +66,24 @@ struct ChunkCfg {
     static constexpr int kXBuf = kRowsMax * kXStride; // one chunk buffer (elements)
     static constexpr int kRing = kRingChunks * CS;    // W fragments in flight per lane (k-steps)
     static constexpr int kGranules = kChunk / 8;      // 16-B x granules per row per chunk
-    static constexpr int kXLoads = kRowsMax * kGranules / kComputeThreads;  // x granules per thread per chunk
-    // two x chunk buffers + the per-wave W transpose tiles
-    static constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + kWaves * 2048;
+    static constexpr int kXGranules = kRowsMax * kGranules;  // x granules per chunk
+    static constexpr int kXLoads = (kXGranules + 64 * W - 1) / (64 * W);  // x granules per thread per chunk (at most)
+    // two x chunk buffers + the per-wave W transpose tiles (the gated epilogue's fp32 tile reuses them)
+    static constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + W * 2048;
     static_assert(kRing % 2 == 0 && CS % 2 == 0, "whole-line loads come in pairs");
     static_assert(kSliceChunk % kChunk == 0, "slices are whole chunks");
-    static_assert(kXLoads * kComputeThreads == kRowsMax * kGranules && kComputeThreads % kGranules == 0,
-                  "x staging map");
+    static_assert(kLdsBytes >= static_cast<size_t>(kRowsMax) * WaveCfg<W>::kRedStride * 4, "gated epilogue tile fits");
 };
 constexpr int kMinSlice = 512;              // K per split at least (bounds the partial traffic)
 #ifndef KVR_GEMM_TARGET_BLOCKS
 #define KVR_GEMM_TARGET_BLOCKS 256
 #endif
 constexpr int kTargetBlocks = KVR_GEMM_TARGET_BLOCKS;  // split until the grid covers every CU once
-constexpr int kRedStride = kTileN + 4;      // fp32 LDS tile of the gated epilogue
-constexpr int kTile = kRowsMax * kTileN;    // fp32 elements of one partial tile
+// Split-K partials: fp32 tiles of 64 output columns, [ceil(cols / 64)][S][64 rows][64 cols]
+// (the layout kPartialTileCols/kPartialTileRows name for fused consumers), whatever
+// the block width; columns are the concatenated rows (gated: gate features, then up).
+constexpr int kTile = kPartialTileRows * kPartialTileCols;  // fp32 elements of one partial tile
+static_assert(kPartialTileRows == kRowsMax && kPartialTileCols == 64, "partial tile geometry");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -103,7 +108,7 @@ struct GemmArgs {
     const char* w2;
     char* y;                        // [M][ldy]
     const char* res;                // residual [M][ldr] added to y (or null)
-    float* partial;                 // [n_tiles][S][64][kTileN] fp32 (S > 1)
+    float* partial;                 // [ceil(rows / 64)][S][64][64] fp32 (S > 1)
     int64_t ldx, ldy, ldr, ldw0, ldw1, ldw2;
     int32_t end0, end1;             // concatenated row boundaries of w0 | w1 | w2
     int32_t rows;                   // streamed rows in total
@@ -112,6 +117,7 @@ struct GemmArgs {
     int32_t m, k;
     int32_t slice;                  // K per split (multiple of kStep)
     int32_t splits;                 // S
+    int32_t waves;                  // waves per block (4, 6 or 7): 16 streamed rows each
 };
 
 // Output value of a concatenated projection: the fp32 sum, or with a residual
@@ -127,18 +133,23 @@ __device__ inline float with_residual(const GemmArgs& a, float sum, int m, int c
 // B = x^T (32 k x 16 rows of x; lane holds x[m0 + lq][k + 8lj ..]) from LDS;
 // D: lane holds the products of x row m0 + lq with streamed rows 4lj + i, i < 4.
 //
-// Streamed row layout of a block (tile): the rows of wave w are
-// tile*kTileN + 16w + 0..15 (concatenated weights); gated: the first half of
-// the waves stream gate rows tile*kHalf + 16w + 0..15 and the second half the
-// same rows of up. The fp32 tile (column c = 16w + 4lj + i) thus holds gate
-// in columns [0, kHalf) and up in [kHalf, kTileN) in gated mode.
-template <typename T, int MT, int CS>
-__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))  // two blocks per CU
+// Streamed row layout of a block (tile) of W waves: the rows of wave w are
+// tile*kTileN + 16w + 0..15 (concatenated weights); gated: wave w streams gate
+// features tile*kHalf + 8w + 0..7 as its rows 0..7 and the same features of up
+// as rows 8..15, so lane columns 4lj + i hold gate (lj < 2) or up (lj >= 2) of
+// feature 8w + 4(lj & 1) + i, and the SiLU pair meets in one wave.
+template <typename T, int MT, int CS, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2)))  // two blocks per CU
 skinny_gemm_kernel(GemmArgs a) {
     using G = gemm_t<T>;
     using E = elem<T>;
     using v8 = typename G::v8;
-    using K = ChunkCfg<CS>;
+    using K = ChunkCfg<CS, W>;
+    using WC = WaveCfg<W>;
+    constexpr int kThreads = WC::kThreads;
+    constexpr int kTileN = WC::kTileN;
+    constexpr int kHalf = WC::kHalf;
+    constexpr int kRedStride = WC::kRedStride;
     constexpr int kChunkSteps = K::kChunkSteps;
     constexpr int kChunk = K::kChunk;
     constexpr int kXStride = K::kXStride;
@@ -168,8 +179,8 @@ skinny_gemm_kernel(GemmArgs a) {
         int local;
         bool row_ok;
         if (a.gated) {
-            const bool up = wave >= kWaves / 2;
-            local = tile * kHalf + 16 * (up ? wave - kWaves / 2 : wave) + rw;
+            const bool up = rw >= 8;
+            local = tile * kHalf + 8 * wave + (rw & 7);
             row_ok = local < a.n_out;
             wb = up ? a.w1 : a.w0;
             ldw = up ? a.ldw1 : a.ldw0;
@@ -211,24 +222,27 @@ skinny_gemm_kernel(GemmArgs a) {
     const char* const wget0 = wtile + (lq >> 3) * 1024 + (lq & 7) * 128 + (((0 + lj) ^ (lq & 7)) * 16);
     const char* const wget1 = wtile + (lq >> 3) * 1024 + (lq & 7) * 128 + (((4 + lj) ^ (lq & 7)) * 16);
 
-    // ---- x chunks: thread t stages granules (row (threads / G) i + t / G, 8 (t % G)) ----
-    const int xrow = tid / kGranules;
-    const int xcol = 8 * (tid % kGranules);
+    // ---- x chunks: thread t stages granules g = t + threads * i (row g / G, k 8 (g % G)) ----
     const char* xbase = a.x + k0 * 2;
     u32x4 xr[kXLoads];
     auto load_x = [&](int c) __attribute__((always_inline)) {
-        const int kk = min(c * kChunk + xcol, klast);
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
-            const int r = (kComputeThreads / kGranules) * i + xrow;
+            const int g0 = tid + kThreads * i;
+            const int g = g0 < K::kXGranules ? g0 : 0;  // the last round's spare threads re-read granule 0
+            const int r = g / kGranules;
+            const int kk = min(c * kChunk + 8 * (g % kGranules), klast);
             xr[i] = *reinterpret_cast<const u32x4*>(xbase + (static_cast<int64_t>(r < a.m ? r : 0) * a.ldx + kk) * 2);
         }
     };
     auto store_x = [&](int c, uint16_t* buf) __attribute__((always_inline)) {
-        const bool k_ok = c * kChunk + xcol < klen;  // klen is a multiple of 8
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
-            const int r = (kComputeThreads / kGranules) * i + xrow;
+            const int g = tid + kThreads * i;
+            if (K::kXGranules % kThreads != 0 && g >= K::kXGranules) continue;
+            const int r = g / kGranules;
+            const int xcol = 8 * (g % kGranules);
+            const bool k_ok = c * kChunk + xcol < klen;  // klen is a multiple of 8
             const u32x4 zero = {0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(buf + r * kXStride + xcol) = (k_ok && r < a.m) ? xr[i] : zero;
         }
@@ -303,12 +317,13 @@ skinny_gemm_kernel(GemmArgs a) {
             }
             return;
         }
-        float* red = reinterpret_cast<float*>(smem);
+        float* red = reinterpret_cast<float*>(smem);  // [64 rows][gate kHalf | up kHalf]
+        const int gcol = (lj < 2 ? 0 : kHalf) + 8 * wave + 4 * (lj & 1);
 #pragma unroll
         for (int t = 0; t < MT; ++t)
-            *reinterpret_cast<f32x4*>(red + (16 * t + lq) * kRedStride + 16 * wave + 4 * lj) = acc[t];
+            *reinterpret_cast<f32x4*>(red + (16 * t + lq) * kRedStride + gcol) = acc[t];
         __syncthreads();
-        for (int e = tid; e < 16 * MT * kHalf; e += kComputeThreads) {
+        for (int e = tid; e < 16 * MT * kHalf; e += kThreads) {
             const int m = e / kHalf;
             const int c = e % kHalf;
             const int col = tile * kHalf + c;
@@ -321,72 +336,91 @@ skinny_gemm_kernel(GemmArgs a) {
         return;
     }
 
-    // ---- split K: fp32 partial tile [64 rows of x][kTileN streamed rows] ----
-    float* part = a.partial + (static_cast<int64_t>(tile) * a.splits + split) * kTile;
+    // ---- split K: this split's fp32 values in the 64-column partial tiles ----
+    auto part_at = [&](int col, int m) -> float* {
+        return a.partial + (static_cast<int64_t>(col / kPartialTileCols) * a.splits + split) * kTile +
+               m * kPartialTileCols + col % kPartialTileCols;
+    };
+    if (!a.gated) {
+        // 4 columns from a multiple of 4: one 64-column tile; columns past `rows`
+        // stay inside the last tile and are never read
+        const int col = tile * kTileN + 16 * wave + 4 * lj;
+        if (col < a.rows) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-        *reinterpret_cast<f32x4*>(part + (16 * t + lq) * kTileN + 16 * wave + 4 * lj) = acc[t];
+            for (int t = 0; t < MT; ++t) *reinterpret_cast<f32x4*>(part_at(col, 16 * t + lq)) = acc[t];
+        }
+    } else {
+        // gate feature f at column f, up feature f at column n_out + f
+        const int f0 = tile * kHalf + 8 * wave + 4 * (lj & 1);
+        const int base = lj < 2 ? 0 : a.n_out;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (f0 + i < a.n_out) *part_at(base + f0 + i, 16 * t + lq) = acc[t][i];
+    }
 }
 
 // Split-K reduction (a second launch, so every partial is visible): block
-// (tile, 16-row group) sums the S partials of its rows in slice order, four
-// columns per thread, four slices' loads in flight at a time, and writes y
-// (gated: the SiLU-gated product of the gate and up sums).
+// (64-column tile, 16-row group) sums the S partials of its rows in slice
+// order and writes y; non-gated four columns per thread with four slices'
+// loads in flight at a time, gated one feature per thread (the SiLU-gated
+// product of its gate sum, column f, and up sum, column n_out + f).
 constexpr int kReduceThreads = 256;
 
 template <typename T>
 __global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(GemmArgs a) {
     using E = elem<T>;
+    constexpr int kCols = kPartialTileCols;
     const int tile = blockIdx.x;
     const int group = blockIdx.y;
-    const f32x4* base = reinterpret_cast<const f32x4*>(a.partial) + static_cast<int64_t>(tile) * a.splits * (kTile / 4);
-    auto sum_splits = [&](int e4) __attribute__((always_inline)) -> f32x4 {
-        f32x4 sum = base[e4];
-        int sp = 1;
-        for (; sp + 4 <= a.splits; sp += 4) {
-            const f32x4 p0 = base[(sp + 0) * (kTile / 4) + e4];
-            const f32x4 p1 = base[(sp + 1) * (kTile / 4) + e4];
-            const f32x4 p2 = base[(sp + 2) * (kTile / 4) + e4];
-            const f32x4 p3 = base[(sp + 3) * (kTile / 4) + e4];
-            sum += p0;
-            sum += p1;
-            sum += p2;
-            sum += p3;
-        }
-        for (; sp < a.splits; ++sp) sum += base[sp * (kTile / 4) + e4];
-        return sum;
-    };
     uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
     if (!a.gated) {
-        for (int e = threadIdx.x; e < 16 * kTileN / 4; e += kReduceThreads) {
-            const int m = 16 * group + e / (kTileN / 4);
-            const int c = 4 * (e % (kTileN / 4));
+        const f32x4* base = reinterpret_cast<const f32x4*>(a.partial) + static_cast<int64_t>(tile) * a.splits * (kTile / 4);
+        auto sum_splits = [&](int e4) __attribute__((always_inline)) -> f32x4 {
+            f32x4 sum = base[e4];
+            int sp = 1;
+            for (; sp + 4 <= a.splits; sp += 4) {
+                const f32x4 p0 = base[(sp + 0) * (kTile / 4) + e4];
+                const f32x4 p1 = base[(sp + 1) * (kTile / 4) + e4];
+                const f32x4 p2 = base[(sp + 2) * (kTile / 4) + e4];
+                const f32x4 p3 = base[(sp + 3) * (kTile / 4) + e4];
+                sum += p0;
+                sum += p1;
+                sum += p2;
+                sum += p3;
+            }
+            for (; sp < a.splits; ++sp) sum += base[sp * (kTile / 4) + e4];
+            return sum;
+        };
+        for (int e = threadIdx.x; e < 16 * kCols / 4; e += kReduceThreads) {
+            const int m = 16 * group + e / (kCols / 4);
+            const int c = 4 * (e % (kCols / 4));
             if (m >= a.m) continue;
-            const f32x4 sum = sum_splits(m * (kTileN / 4) + c / 4);
-            const int col = tile * kTileN + c;
+            const f32x4 sum = sum_splits(m * (kCols / 4) + c / 4);
+            const int col = tile * kCols + c;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (col + i < a.rows)
                     y[static_cast<int64_t>(m) * a.ldy + col + i] = E::from_float(with_residual<T>(a, sum[i], m, col + i));
         }
     } else {
-        for (int e = threadIdx.x; e < 16 * kHalf / 4; e += kReduceThreads) {
-            const int m = 16 * group + e / (kHalf / 4);
-            const int c = 4 * (e % (kHalf / 4));
-            if (m >= a.m) continue;
-            const f32x4 g = sum_splits(m * (kTileN / 4) + c / 4);
-            const f32x4 u = sum_splits(m * (kTileN / 4) + kHalf / 4 + c / 4);
-            const int col = tile * kHalf + c;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (col + i < a.n_out)
-                    y[static_cast<int64_t>(m) * a.ldy + col + i] =
-                        E::from_float(silu_gate<T>(round_through<T>(g[i]), round_through<T>(u[i])));
+        auto sum_col = [&](int col, int m) __attribute__((always_inline)) -> float {
+            const float* at = a.partial + static_cast<int64_t>(col / kCols) * a.splits * kTile + m * kCols + col % kCols;
+            float sum = at[0];
+            for (int sp = 1; sp < a.splits; ++sp) sum += at[static_cast<int64_t>(sp) * kTile];
+            return sum;
+        };
+        for (int e = threadIdx.x; e < 16 * kCols; e += kReduceThreads) {
+            const int m = 16 * group + e / kCols;
+            const int f = tile * kCols + e % kCols;
+            if (m >= a.m || f >= a.n_out) continue;
+            const float g = sum_col(f, m);
+            const float u = sum_col(a.n_out + f, m);
+            y[static_cast<int64_t>(m) * a.ldy + f] = E::from_float(silu_gate<T>(round_through<T>(g), round_through<T>(u)));
         }
     }
 }
-
-static_assert(ChunkCfg<4>::kLdsBytes >= static_cast<size_t>(kRowsMax) * kRedStride * 4, "gated epilogue tile fits");
 
 template <typename F>
 bool allow_lds(F fn, size_t bytes) {
@@ -395,24 +429,34 @@ bool allow_lds(F fn, size_t bytes) {
                                static_cast<int>(bytes)) == hipSuccess;
 }
 
-template <typename T, int MT, int CS>
+template <typename T, int MT, int CS, int W>
 int launch_cs(const GemmArgs& a, dim3 grid, hipStream_t s) {
-    constexpr size_t lds = ChunkCfg<CS>::kLdsBytes;
-    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT, CS>, lds);
+    constexpr size_t lds = ChunkCfg<CS, W>::kLdsBytes;
+    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT, CS, W>, lds);
     if (!ok) return KVR_E_LAUNCH_FAILED;
-    skinny_gemm_kernel<T, MT, CS><<<grid, kGemmThreads, lds, s>>>(a);
+    skinny_gemm_kernel<T, MT, CS, W><<<grid, 64 * W, lds, s>>>(a);
     return KVR_OK;
 }
 
 template <typename T, int MT>
 int launch_mt(const GemmArgs& a, hipStream_t s, bool reduce) {
-    const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, kTileN)), static_cast<unsigned>(a.splits));
-    // more blocks than CUs (some CUs run two): 4-step chunks; else 8
-    const int st = static_cast<int64_t>(grid.x) * grid.y > kTargetBlocks ? launch_cs<T, MT, 4>(a, grid, s)
-                                                                        : launch_cs<T, MT, 8>(a, grid, s);
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, 16 * a.waves)), static_cast<unsigned>(a.splits));
+    int st;
+    if (a.waves == 6) {
+        st = launch_cs<T, MT, 8, 6>(a, grid, s);
+    } else if (a.waves == 7) {
+        st = launch_cs<T, MT, 8, 7>(a, grid, s);
+    } else {
+        // more blocks than CUs (some CUs run two): 4-step chunks; else 8
+        st = static_cast<int64_t>(grid.x) * grid.y > kTargetBlocks ? launch_cs<T, MT, 4, 4>(a, grid, s)
+                                                                  : launch_cs<T, MT, 8, 4>(a, grid, s);
+    }
     if (st != KVR_OK) return st;
-    if (a.splits > 1 && reduce)
-        splitk_reduce_kernel<T><<<dim3(grid.x, static_cast<unsigned>(MT)), kReduceThreads, 0, s>>>(a);
+    if (a.splits > 1 && reduce) {
+        const int64_t cols = a.gated ? a.n_out : a.rows;
+        const dim3 rgrid(static_cast<unsigned>(ceil_div(cols, kPartialTileCols)), static_cast<unsigned>(MT));
+        splitk_reduce_kernel<T><<<rgrid, kReduceThreads, 0, s>>>(a);
+    }
     return launch_status();
 }
 
@@ -433,23 +477,39 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using namespace kvr;
 
-// K split of a launch: the smallest power of two giving >= kTargetBlocks
-// blocks, at most k / kMinSlice; slices are whole 256-chunks, so the split
-// count is then ceil(k / slice).
+// K split of a launch of `waves`-wave blocks: the smallest power of two
+// giving >= kTargetBlocks blocks, at most k / kMinSlice; slices are whole
+// 256-chunks, so the split count is then ceil(k / slice). Blocks have 4 waves
+// unless 6 or 7 make the grid exactly one block per CU where 4 do not (q/k/v
+// of 8B-shaped models: 6144 rows, 64 x 4 blocks of 6 waves instead of 96 x 4;
+// their gate/up pairs: 256 blocks of 7 or 6 waves instead of 448 or 384 of 4):
+// a CU running two blocks while others run one makes the launch last as long
+// as its slowest CU.
 namespace {
 struct Split {
     int32_t splits;
     int32_t slice;
+    int32_t waves;
 };
 
-Split plan_split(int32_t rows, int32_t k) {
-    const int64_t tiles = ceil_div(rows, kTileN);
+Split split_for(int32_t rows, int32_t k, int32_t waves) {
+    const int64_t tiles = ceil_div(rows, 16 * waves);
     int32_t want = 1;
     while (tiles * want < kTargetBlocks && want < 64) want *= 2;
     const int32_t cap = k / kMinSlice > 1 ? k / kMinSlice : 1;
     const int32_t s = want < cap ? want : cap;
     const int32_t slice = static_cast<int32_t>(ceil_div(ceil_div(k, s), kSliceChunk) * kSliceChunk);
-    return Split{static_cast<int32_t>(ceil_div(k, slice)), slice};
+    return Split{static_cast<int32_t>(ceil_div(k, slice)), slice, waves};
+}
+
+Split plan_split(int32_t rows, int32_t k) {
+    const Split four = split_for(rows, k, 4);
+    if (ceil_div(rows, 64) * four.splits == kTargetBlocks) return four;
+    for (int32_t waves : {6, 7}) {
+        const Split sp = split_for(rows, k, waves);
+        if (ceil_div(rows, 16 * waves) * sp.splits == kTargetBlocks) return sp;
+    }
+    return four;
 }
 }  // namespace
 
@@ -462,7 +522,7 @@ extern "C" int64_t kvr_linear_workspace_bytes(int32_t m, int32_t rows, int32_t k
     const int32_t splits = kvr_linear_splits(m, rows, k);
     if (splits < 0) return splits;
     if (splits == 1) return 0;
-    return ceil_div(rows, kTileN) * splits * static_cast<int64_t>(kRowsMax) * kTileN * 4;
+    return ceil_div(rows, kPartialTileCols) * splits * static_cast<int64_t>(kTile) * 4;
 }
 
 namespace kvr {
@@ -527,6 +587,7 @@ int linear_multi(const void* x, int32_t n_weights, const void* const* w, const i
     const Split sp = plan_split(static_cast<int32_t>(total), k);
     a.splits = sp.splits;
     a.slice = sp.slice;
+    a.waves = sp.waves;
     if (!reduce && (gated || a.res)) return KVR_E_INVALID_ARGUMENT;  // partial consumers take plain sums
     if (splits_out) *splits_out = sp.splits;
     hipStream_t s = as_stream(stream);

@@ -379,10 +379,11 @@ def assert_linear_close(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> No
     assert (y == ref.to(y.dtype)).float().mean().item() >= 0.99
 
 
-# (n, k): split counts 4 / 2 / 4 / 1 / 1 / 3; k = 136 and 1000 end inside a
+# (n, k): split counts 4 / 2 / 4 / 1 / 1 / 3 / 4; k = 136 and 1000 end inside a
 # 32-wide step and a 256-chunk, n = 100 inside a 64-row tile, k = 2000 splits
-# into 768 + 768 + 464
-LINEAR_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (100, 136), (1024, 1000), (512, 2000)]
+# into 768 + 768 + 464; n = 14336 and 6144 take 7- and 6-wave blocks (their
+# grids are then exactly 256 blocks), the others 4
+LINEAR_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (100, 136), (1024, 1000), (512, 2000), (6144, 4096)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -460,6 +461,29 @@ def test_silu_gate_linear_is_bitwise_linear_then_silu_mul(gpu_device, dtype, sha
     chained = _silu_mul(projection.linear(x, gate), projection.linear(x, up))
     assert bits_equal(fused, chained)
     eager = torch.nn.functional.silu(exact_linear(x, gate)) * exact_linear(x, up)
+    dist = ulp_distance(fused, eager)
+    assert (dist <= 2).float().mean().item() >= 0.99
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n", [14336, 12288])
+def test_silu_gate_linear_at_the_mlp_shapes(gpu_device, dtype, n):
+    """The Llama-8B (14336) and Qwen3-8B (12288) gate/up pairs, which take 7- and
+    6-wave blocks with each wave streaming 8 gate rows and the same 8 up rows (one
+    block per CU, no K split): within the eager act_fn(gate) * up chain's rounding
+    of the exact products."""
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.kernels import projection
+
+    k = 4096
+    assert _native.lib().kvr_linear_splits(64, 2 * n, k) == 1
+    torch.manual_seed(n)
+    x = torch.randn(1, 64, k, device=gpu_device).to(dtype)
+    gate = (torch.randn(n, k, device=gpu_device) * 0.05).to(dtype)
+    up = (torch.randn(n, k, device=gpu_device) * 0.05).to(dtype)
+    fused = projection.silu_gate_linear(x, gate, up)
+    eager = torch.nn.functional.silu(exact_linear(x, gate)) * exact_linear(x, up)
+    assert fused.shape == (1, 64, n) and torch.isfinite(fused.float()).all()
     dist = ulp_distance(fused, eager)
     assert (dist <= 2).float().mean().item() >= 0.99
 
