@@ -484,13 +484,13 @@ def graph_device_us(launch, per_graph: int = 20, replays: int = 5) -> float:
     return us
 
 
-def _checked(fn, *args):
-    """A launch of ``fn(*args, stream)`` on the stream current at call time (a
-    graph capture swaps it), raising on a nonzero status."""
+def _checked(fn, *args, after=()):
+    """A launch of ``fn(*args, stream, *after)`` on the stream current at call
+    time (a graph capture swaps it), raising on a nonzero status."""
     from kv_cache_repair_amd import _native
 
     def launch():
-        status = fn(*args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        status = fn(*args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), *after)
         if status != 0:
             raise RuntimeError(f"{fn.__name__} returned {status}: {_native.lib().kvr_status_string(status)}")
     return launch
@@ -576,7 +576,9 @@ def kernel_launchers(model, workload: Workload, old, old_ids, new_ids, device):
     out["kvr_packed_causal_attention"] = (_checked(lib.kvr_packed_causal_attention, *args), attn_bytes, attn_flops,
                                           w.layers)
 
-    # projections of one layer (<= 64 rows: the stage runs them on kvr_linear_multi)
+    # projections of one layer as the stage's native forward launches them (<= 64 rows): q/k/v, o and down
+    # leave their split-K partials to the consumer kernels (kvr_linear_multi_partials, no reduce launch),
+    # gate/up runs with the SiLU gate in its epilogue (one split)
     if b <= 64:
         from kv_cache_repair_amd.kernels import projection as proj
 
@@ -586,22 +588,28 @@ def kernel_launchers(model, workload: Workload, old, old_ids, new_ids, device):
         xi = torch.randn(b, w.mlp, device=device, generator=gen, dtype=torch.bfloat16)
         xo = torch.randn(b, w.hq * w.dim, device=device, generator=gen, dtype=torch.bfloat16)
         calls, total_bytes = [], 0
-        for weights, epi, xin, residual in (
-                ([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], proj.CONCAT, x, False),
-                ([a.o_proj.weight], proj.CONCAT, xo, True),
-                ([m.gate_proj.weight, m.up_proj.weight], proj.SILU_GATE, x, False),
-                ([m.down_proj.weight], proj.CONCAT, xi, True)):
+        for weights, epi, xin in (
+                ([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], proj.CONCAT, x),
+                ([a.o_proj.weight], proj.CONCAT, xo),
+                ([m.gate_proj.weight, m.up_proj.weight], proj.SILU_GATE, x),
+                ([m.down_proj.weight], proj.CONCAT, xi)):
             pl = proj.ProjectionPlan(weights, epi)
             need = pl.workspace_bytes(b)
             wsp = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
             y = torch.empty(b, pl.n_out, device=device, dtype=torch.bfloat16)
-            res = torch.randn(b, pl.n_out, device=device, generator=gen, dtype=torch.bfloat16) if residual else None
-            calls.append((_checked(lib.kvr_linear_multi, xin.data_ptr(), pl._count, pl._w, pl._rows, pl._ldw,
-                                   y.data_ptr(), b, pl.k, xin.stride(0), pl.n_out,
-                                   proj.RESIDUAL if residual else epi, res.data_ptr() if residual else None,
-                                   pl.n_out if residual else 0, wsp.data_ptr(), need, code),
-                          (xin, y, wsp, res)))
-            total_bytes += esz * (pl.rows * pl.k + b * pl.k + b * pl.n_out * (2 if residual else 1))
+            if epi == proj.SILU_GATE:
+                launch = _checked(lib.kvr_linear_multi, xin.data_ptr(), pl._count, pl._w, pl._rows, pl._ldw,
+                                  y.data_ptr(), b, pl.k, xin.stride(0), pl.n_out, epi, None, 0, wsp.data_ptr(), need,
+                                  code)
+                splits = None
+            else:
+                splits = ctypes.c_int32(0)
+                launch = _checked(lib.kvr_linear_multi_partials, xin.data_ptr(), pl._count, pl._w, pl._rows,
+                                  pl._ldw, y.data_ptr(), b, pl.k, xin.stride(0), pl.n_out, wsp.data_ptr(), need, code,
+                                  after=(ctypes.byref(splits),))
+            calls.append((launch, (xin, y, wsp, splits)))
+            # algorithmic: the weights, x and the bf16 output once
+            total_bytes += esz * (pl.rows * pl.k + b * pl.k + b * pl.n_out)
         keep = [c[1] for c in calls]
 
         def launch_all():
@@ -1043,7 +1051,8 @@ def run_workload(args, workload: Workload, device) -> dict:
         "roofline": roofline, "rooflines": north, "kernels": kernels,
         "kernel_timing": "HIP events around 5 replays of a graph of 20 back-to-back launches of each libkvrepair "
                          "call with the stage's shapes (device time only); kvr_linear_multi = one layer's four "
-                         "projections, per call",
+                         "projections as the native forward launches them (q/k/v, o, down leave split-K partials "
+                         "to their consumers: kvr_linear_multi_partials), per projection",
         "reference_same_gpu": reference, "interleaved": interleaved, "checks": checks, "selection_scoring": scoring,
         "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
     }

@@ -284,6 +284,15 @@ extern "C" int kvr_decoder_forward(const kvr_layer_desc* layers, int32_t n_layer
     return KVR_OK;
 }
 
+extern "C" int kvr_linear_multi_partials(const void* x, int32_t n_weights, const void* const* w,
+                                         const int32_t* rows, const int64_t* ldw, void* y, int32_t m, int32_t k,
+                                         int64_t ldx, int64_t ldy, void* workspace, int64_t workspace_bytes,
+                                         int32_t dtype, void* stream, int32_t* splits_out) {
+    if (!splits_out) return KVR_E_NULL_POINTER;
+    return kvr::linear_multi(x, n_weights, w, rows, ldw, y, m, k, ldx, ldy, KVR_LINEAR_CONCAT, nullptr, 0, workspace,
+                             workspace_bytes, dtype, stream, /*reduce=*/false, splits_out);
+}
+
 extern "C" void kvr_decoder_desc_sizes(int64_t sizes[2]) {
     sizes[0] = static_cast<int64_t>(sizeof(kvr_layer_desc));
     sizes[1] = static_cast<int64_t>(sizeof(kvr_refresh_desc));

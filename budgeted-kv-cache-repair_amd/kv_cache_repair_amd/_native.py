@@ -98,6 +98,10 @@ def _declare(lib: ctypes.CDLL) -> None:
                                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, ctypes.c_int64, _vp,
                                      ctypes.c_int64, ctypes.c_int32, _vp]
     lib.kvr_linear_multi.restype = ctypes.c_int
+    lib.kvr_linear_multi_partials.argtypes = [_vp, ctypes.c_int32, _vpp, _i32p, _i64p, _vp, ctypes.c_int32,
+                                              ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, _vp, ctypes.c_int64,
+                                              ctypes.c_int32, _vp, _i32p]
+    lib.kvr_linear_multi_partials.restype = ctypes.c_int
     lib.kvr_copy_kv_interval.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
                                          ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, _i64p, ctypes.c_int32, _vp]
     lib.kvr_copy_kv_interval.restype = ctypes.c_int

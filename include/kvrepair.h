@@ -277,6 +277,21 @@ int kvr_linear_multi(const void* x, int32_t n_weights, const void* const* w, con
                      const void* residual, int64_t ldr, void* workspace, int64_t workspace_bytes, int32_t dtype,
                      void* stream);
 
+/* kvr_linear_multi (KVR_LINEAR_CONCAT) without its split-K reduction, as the
+ * packed forward runs the q/k/v, o and down projections whose consumers read
+ * the partial sums: with more than one split y is left unwritten and
+ * `workspace` holds fp32 partials [ceil(rows / 64)][splits][64 rows][64 cols],
+ * element (row, col) of x W^T being the sum over s of
+ * tile(col / 64)[s][row][col % 64] in split order (rounded once, that is
+ * kvr_linear_multi's y bit for bit); with one split y is written as by
+ * kvr_linear_multi. *splits_out receives the split count. No reference
+ * counterpart: the reference's projections are nn.Linear calls whose output
+ * the next op reads (modeling_llama.py:243-252). */
+int kvr_linear_multi_partials(const void* x, int32_t n_weights, const void* const* w, const int32_t* rows,
+                              const int64_t* ldw, void* y, int32_t m, int32_t k, int64_t ldx, int64_t ldy,
+                              void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream,
+                              int32_t* splits_out);
+
 /*
  * One decoder layer of the packed refresh, enqueued by a single call.
  *

@@ -465,6 +465,47 @@ def test_silu_gate_linear_is_bitwise_linear_then_silu_mul(gpu_device, dtype, sha
     assert (dist <= 2).float().mean().item() >= 0.99
 
 
+@pytest.mark.parametrize("shape", [(6144, 4096), (4096, 4096), (4096, 14336), (100, 136)])
+@pytest.mark.parametrize("rows", [17, 64])
+def test_linear_partials_sum_to_the_reduced_projection(gpu_device, shape, rows):
+    """kvr_linear_multi_partials leaves the split-K partials in 64-column tiles
+    ([ceil(n / 64)][splits][64][64]); summed over the splits in order and rounded
+    once they are kvr_linear_multi's output bit for bit (one split: y itself)."""
+    import ctypes
+
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.kernels import projection
+
+    n, k = shape
+    lib = _native.lib()
+    torch.manual_seed(n + k + rows)
+    x = torch.randn(rows, k, device=gpu_device).to(torch.bfloat16)
+    w = (torch.randn(n, k, device=gpu_device) * 0.03).to(torch.bfloat16)
+    plan = projection.ProjectionPlan([w])
+    need = plan.workspace_bytes(rows)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=gpu_device)
+    y = torch.zeros(rows, n, device=gpu_device, dtype=torch.bfloat16)
+    splits = ctypes.c_int32(0)
+    stream = _native.stream_handle(gpu_device)
+    status = lib.kvr_linear_multi_partials(x.data_ptr(), 1, plan._w, plan._rows, plan._ldw, y.data_ptr(), rows, k, k,
+                                           n, ws.data_ptr(), need, _native.DTYPE_CODES[torch.bfloat16], stream,
+                                           ctypes.byref(splits))
+    assert status == 0
+    reduced = plan(x)
+    torch.cuda.synchronize()
+    assert splits.value == lib.kvr_linear_splits(rows, n, k)
+    if splits.value == 1:
+        assert bits_equal(y, reduced)
+        return
+    tiles = (n + 63) // 64
+    part = ws.view(torch.float32)[:tiles * splits.value * 64 * 64].view(tiles, splits.value, 64, 64)
+    acc = part[:, 0].clone()
+    for s in range(1, splits.value):
+        acc = acc + part[:, s]
+    summed = acc.permute(1, 0, 2).reshape(64, tiles * 64)[:rows, :n]
+    assert bits_equal(summed.to(torch.bfloat16), reduced)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("n", [14336, 12288])
 def test_silu_gate_linear_at_the_mlp_shapes(gpu_device, dtype, n):

@@ -25,7 +25,8 @@ def test_header_declares_the_entry_points():
         "kvr_abi_version", "kvr_status_string", "kvr_rope_delta_rotate", "kvr_shift_cache_build",
         "kvr_indexed_scatter_kv", "kvr_rope_scatter_kv", "kvr_rope_scatter_kv_norm", "kvr_attention_schedule",
         "kvr_attention_schedule_ex", "kvr_attention_workspace_bytes", "kvr_packed_causal_attention", "kvr_rms_norm",
-        "kvr_silu_mul", "kvr_linear", "kvr_linear_splits", "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_decoder_scratch_bytes",
+        "kvr_silu_mul", "kvr_linear", "kvr_linear_splits", "kvr_linear_workspace_bytes", "kvr_linear_multi", "kvr_linear_multi_partials",
+        "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
         "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance", "kvr_packed_causal_attention_noalloc",
         "kvr_attention_scratch_limit"])
