@@ -13,7 +13,7 @@
 // applies the SiLU-gated product (the MLP's act_fn(gate) * up) so the two
 // projections never reach HBM.
 //
-// Work split: block = W waves x 16 streamed weight rows x one K slice, W = 4,
+// Work split: block = NW waves x 16 streamed weight rows x one K slice, NW = 4,
 // or 6 / 7 where that makes the grid exactly one block per CU (q/k/v and the
 // gate/up pairs of 8B-shaped models). The slice is walked in chunks of 256 (128
 // in launches with more blocks than CUs): x[:, chunk] is staged in one of
@@ -41,11 +41,11 @@ namespace {
 #endif
 
 // Waves per block (16 streamed weight rows each) is a launch parameter: 4, 6 or
-// 7, whichever makes the grid exactly one block per CU (see choose_waves).
-template <int W>
+// 7, whichever makes the grid exactly one block per CU (plan_split).
+template <int NW>
 struct WaveCfg {
-    static constexpr int kThreads = 64 * W;
-    static constexpr int kTileN = 16 * W;      // streamed weight rows per block
+    static constexpr int kThreads = 64 * NW;
+    static constexpr int kTileN = 16 * NW;      // streamed weight rows per block
     static constexpr int kHalf = kTileN / 2;   // gated: output columns per block (8 per wave)
     static constexpr int kRedStride = kTileN + 4;  // fp32 LDS tile of the gated epilogue
 };
@@ -58,7 +58,7 @@ static_assert(kRingChunks == 1 || kRingChunks == 2, "chunk buffers alternate wit
 // Staged x chunk of CS k-steps (CS = the W ring depth per chunk): 8 for
 // launches of at most one block per CU, 4 (half the LDS, chunks turned over
 // twice as often) where some CUs run two blocks.
-template <int CS, int W>
+template <int CS, int NW>
 struct ChunkCfg {
     static constexpr int kChunkSteps = CS;            // k-steps per staged x chunk = W ring depth
     static constexpr int kChunk = CS * kStep;         // K per chunk
@@ -67,12 +67,12 @@ struct ChunkCfg {
     static constexpr int kRing = kRingChunks * CS;    // W fragments in flight per lane (k-steps)
     static constexpr int kGranules = kChunk / 8;      // 16-B x granules per row per chunk
     static constexpr int kXGranules = kRowsMax * kGranules;  // x granules per chunk
-    static constexpr int kXLoads = (kXGranules + 64 * W - 1) / (64 * W);  // x granules per thread per chunk (at most)
+    static constexpr int kXLoads = (kXGranules + 64 * NW - 1) / (64 * NW);  // x granules per thread per chunk (at most)
     // two x chunk buffers + the per-wave W transpose tiles (the gated epilogue's fp32 tile reuses them)
-    static constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + W * 2048;
+    static constexpr size_t kLdsBytes = 2 * static_cast<size_t>(kXBuf) * 2 + NW * 2048;
     static_assert(kRing % 2 == 0 && CS % 2 == 0, "whole-line loads come in pairs");
     static_assert(kSliceChunk % kChunk == 0, "slices are whole chunks");
-    static_assert(kLdsBytes >= static_cast<size_t>(kRowsMax) * WaveCfg<W>::kRedStride * 4, "gated epilogue tile fits");
+    static_assert(kLdsBytes >= static_cast<size_t>(kRowsMax) * WaveCfg<NW>::kRedStride * 4, "gated epilogue tile fits");
 };
 constexpr int kMinSlice = 512;              // K per split at least (bounds the partial traffic)
 #ifndef KVR_GEMM_TARGET_BLOCKS
@@ -133,19 +133,19 @@ __device__ inline float with_residual(const GemmArgs& a, float sum, int m, int c
 // B = x^T (32 k x 16 rows of x; lane holds x[m0 + lq][k + 8lj ..]) from LDS;
 // D: lane holds the products of x row m0 + lq with streamed rows 4lj + i, i < 4.
 //
-// Streamed row layout of a block (tile) of W waves: the rows of wave w are
+// Streamed row layout of a block (tile) of NW waves: the rows of wave w are
 // tile*kTileN + 16w + 0..15 (concatenated weights); gated: wave w streams gate
 // features tile*kHalf + 8w + 0..7 as its rows 0..7 and the same features of up
 // as rows 8..15, so lane columns 4lj + i hold gate (lj < 2) or up (lj >= 2) of
 // feature 8w + 4(lj & 1) + i, and the SiLU pair meets in one wave.
-template <typename T, int MT, int CS, int W>
-__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2)))  // two blocks per CU
+template <typename T, int MT, int CS, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))  // two blocks per CU
 skinny_gemm_kernel(GemmArgs a) {
     using G = gemm_t<T>;
     using E = elem<T>;
     using v8 = typename G::v8;
-    using K = ChunkCfg<CS, W>;
-    using WC = WaveCfg<W>;
+    using K = ChunkCfg<CS, NW>;
+    using WC = WaveCfg<NW>;
     constexpr int kThreads = WC::kThreads;
     constexpr int kTileN = WC::kTileN;
     constexpr int kHalf = WC::kHalf;
@@ -429,12 +429,12 @@ bool allow_lds(F fn, size_t bytes) {
                                static_cast<int>(bytes)) == hipSuccess;
 }
 
-template <typename T, int MT, int CS, int W>
+template <typename T, int MT, int CS, int NW>
 int launch_cs(const GemmArgs& a, dim3 grid, hipStream_t s) {
-    constexpr size_t lds = ChunkCfg<CS, W>::kLdsBytes;
-    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT, CS, W>, lds);
+    constexpr size_t lds = ChunkCfg<CS, NW>::kLdsBytes;
+    static const bool ok = allow_lds(skinny_gemm_kernel<T, MT, CS, NW>, lds);
     if (!ok) return KVR_E_LAUNCH_FAILED;
-    skinny_gemm_kernel<T, MT, CS, W><<<grid, 64 * W, lds, s>>>(a);
+    skinny_gemm_kernel<T, MT, CS, NW><<<grid, 64 * NW, lds, s>>>(a);
     return KVR_OK;
 }
 
