@@ -5,10 +5,11 @@ Mirrors the reference public surface (src/kv_cache_repair/api.py):
 ``repair_after_deletion(..., executor="packed")``. Positional correction
 (build_halo_cache) and the packed refresh run on libkvrepair.
 
-Query-relevance (SUR) support selection is host-side text processing outside
-this build: budgets of 0% (shift only) and 100% (full suffix) are selected
-here exactly as the reference selects them (api.py:77-84); for any other
-budget the caller passes the selected positions to ``repair_with_positions``.
+Support selection follows the reference (api.py:62-110): 0% selects nothing,
+100% the whole suffix, and any budget in between the semantic-unit (SUR)
+allocation over the GPU query-relevance scores (``semantic_units`` on the host,
+``scoring.dense_query_relevance_scores`` on libkvrepair).
+``repair_with_positions`` takes caller-selected positions instead.
 """
 
 from __future__ import annotations
@@ -22,6 +23,8 @@ import torch
 from .alignment import token_alignment_arrays
 from .cache import OperatorShim, build_halo_cache
 from .execution import positions_to_intervals
+from .scoring import dense_query_relevance_scores, query_text_token_ids
+from .semantic_units import select_semantic_unit_support, semantic_unit_token_ranges
 from .kernels.executor import layer_kv
 from .kernels.packed_cache import _qualify, packed_refresh_owned_
 
@@ -87,9 +90,15 @@ def _selection(positions: Sequence[int], suffix_start: int, length: int, budget:
                      metadata=metadata)
 
 
-def _budget_selection(length: int, suffix_start: int, budget_percent: float) -> Selection:
+def _budget_selection(model: Any, tokenizer: Any, text: str, query: str, ids: torch.Tensor, suffix_start: int,
+                      budget_percent: float) -> Selection:
+    """``ceil(budget_percent / 100 * suffix_tokens)`` suffix positions of the
+    edited prompt ``text`` (host ids ``ids``), as the reference selects them
+    (api.py:62-110): none, the whole suffix, or the semantic-unit allocation
+    over the query-relevance scores of every prompt token."""
     if isinstance(suffix_start, bool) or not isinstance(suffix_start, int):
         raise ValueError("suffix_start must be an integer token position")
+    length = int(ids.shape[1])
     if not 0 <= suffix_start <= length:
         raise ValueError("suffix_start must lie inside the edited prompt")
     suffix_tokens = length - suffix_start
@@ -101,10 +110,14 @@ def _budget_selection(length: int, suffix_start: int, budget_percent: float) -> 
     if budget == suffix_tokens:
         metadata["selection"] = "full_suffix"
         return _selection(range(suffix_start, length), suffix_start, length, budget, metadata)
-    raise NotImplementedError(
-        f"a {budget_percent:g}% budget ({budget} of {suffix_tokens} suffix tokens) needs query-relevance (SUR) "
-        "support selection, which is not part of this build; select positions with the reference select_support "
-        "and call repair_with_positions, or use a 0% or 100% budget")
+    units = semantic_unit_token_ranges(tokenizer=tokenizer, text=text, expected_token_ids=ids[0].tolist(),
+                                       suffix_start=suffix_start)
+    scores, scoring = dense_query_relevance_scores(model=OperatorShim(model, tokenizer),
+                                                   edited_input_ids=_to_model_device(model, ids),
+                                                   query_token_ids=query_text_token_ids(tokenizer, query))
+    positions, allocator = select_semantic_unit_support(units=units, token_scores=scores, budget_tokens=budget)
+    metadata.update({"selection": "sur", "scoring": scoring, "allocator": allocator})
+    return _selection(positions, suffix_start, length, budget, metadata)
 
 
 @torch.no_grad()
@@ -112,12 +125,13 @@ def select_support(model: Any, tokenizer: Any, edited_text: str, query: str, *, 
                    budget_percent: float = 5.0) -> Selection:
     """``ceil(budget_percent / 100 * suffix_tokens)`` positions (reference api.py:113-132).
 
-    0% selects nothing and 100% the whole suffix; other budgets need SUR
-    selection, which this build does not provide (NotImplementedError).
+    0% selects nothing and 100% the whole suffix; other budgets take the
+    semantic-unit allocation, whose scores need only the frozen input
+    embeddings (one scorer launch, no transformer forward).
     """
     budget_percent = _check_budget(budget_percent)
     ids = _encode_host(model, tokenizer, edited_text)
-    return _budget_selection(int(ids.shape[1]), suffix_start, budget_percent)
+    return _budget_selection(model, tokenizer, edited_text, query, ids, suffix_start, budget_percent)
 
 
 def _check_model(model: Any) -> None:
@@ -181,9 +195,9 @@ def _prepare(model, tokenizer, old_cache, original_text, start, end):
 
 
 def _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text, selector):
-    """Select on the host first (the suffix start comes from the host alignment,
-    the same one build_halo_cache computes), so a request this build cannot
-    serve is refused before any device work; then shift and refresh."""
+    """Select first (the suffix start comes from the host alignment, the same
+    one build_halo_cache computes), so a selection error leaves no shifted cache
+    behind; then shift and refresh."""
     alignment = token_alignment_arrays(old_ids[0].numpy(), edited_ids[0].numpy())
     selection = selector(int(edited_ids.shape[1]), int(alignment["new_suffix_start"]))
     shim = OperatorShim(model, tokenizer)
@@ -215,7 +229,8 @@ def repair_after_deletion(model: Any, tokenizer: Any, old_cache: Any, original_t
     start, end = _check_span(original_text, delete_span)
     old_ids, edited_text, edited_ids = _prepare(model, tokenizer, old_cache, original_text, start, end)
     return _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text,
-                    lambda length, suffix_start: _budget_selection(length, suffix_start, budget_percent))
+                    lambda length, suffix_start: _budget_selection(model, tokenizer, edited_text, query, edited_ids,
+                                                                   suffix_start, budget_percent))
 
 
 @torch.no_grad()

@@ -2,7 +2,8 @@
 tokenizer), against the oracle's restatement of the reference's schedules.
 
 Vectors follow the reference's public-contract tests (tests/test_api.py:
-152-273): 0% and 100% budgets agree with the sequential interval recurrence,
+100-273): 0%, 2%, 5% (semantic-unit selection) and 100% budgets agree with the
+sequential interval recurrence, partial budgets take their ceiling,
 the full suffix reproduces a clean prefill, trailing and whole-prompt
 deletions leave an empty suffix, boundary retokenization is recomputed outside
 the budget, a cache of the wrong length is refused, and the input cache is
@@ -17,6 +18,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
+from oracle import oracle as orc
 from oracle import reference_path as ref
 
 pytestmark = pytest.mark.gpu
@@ -182,22 +184,78 @@ def test_cache_of_the_wrong_length_is_refused(model, tokenizer):
         repair_after_deletion(**req)
 
 
+def f64_selection(model, tokenizer, text, query, suffix_start, budget):
+    """The semantic-unit allocation over the oracle's float64 relevance scores."""
+    from kv_cache_repair_amd.semantic_units import select_semantic_unit_support, semantic_unit_token_ranges
+
+    ids = tokenizer(text, add_special_tokens=False)["input_ids"]
+    qids = tokenizer(query, add_special_tokens=False)["input_ids"]
+    table = model.get_input_embeddings().weight.detach().double().cpu().numpy()
+    scores = [float(v) for v in orc.query_relevance_f64(table, ids, qids)]
+    units = semantic_unit_token_ranges(tokenizer=tokenizer, text=text, expected_token_ids=ids,
+                                       suffix_start=suffix_start)
+    return select_semantic_unit_support(units=units, token_scores=scores, budget_tokens=budget)[0]
+
+
+@pytest.mark.parametrize("budget,expected", [(2, 2), (5, 5)])
+def test_select_support_partial_budgets_without_a_forward(model, tokenizer, budget, expected):
+    """tests/test_api.py:100-130: SUR selection obeys the suffix budget and runs
+    no transformer forward; its positions equal the allocation over float64 scores."""
+    from kv_cache_repair_amd import select_support
+
+    text = "prefix " + SUFFIX
+
+    def no_forward(module, args):
+        raise AssertionError("selection must not run a transformer forward")
+
+    handles = [m.register_forward_pre_hook(no_forward) for m in (model, model.base_model)]
+    try:
+        result = select_support(model, tokenizer, text, "alpha", suffix_start=1, budget_percent=budget)
+    finally:
+        for h in handles:
+            h.remove()
+    assert (result.suffix_start, result.suffix_tokens, result.budget_tokens) == (1, 100, expected)
+    assert len(result.positions) == len(set(result.positions)) == expected
+    assert list(result.positions) == sorted(result.positions) and all(1 <= p < 101 for p in result.positions)
+    assert [p for s, e in result.intervals for p in range(s, e)] == list(result.positions)
+    assert result.metadata["selection"] == "sur"
+    assert result.metadata["scoring"]["exact_token_boost"] == 0.25
+    assert list(result.positions) == f64_selection(model, tokenizer, text, "alpha", 1, expected)
+
+
 @pytest.mark.parametrize("budget", [2, 5])
-def test_partial_budgets_are_refused_before_any_device_work(model, tokenizer, monkeypatch, budget):
-    """The suffix start (hence the budget) is known from the host alignment, so a
-    budget this build cannot select is refused before the shift-cache build."""
-    from kv_cache_repair_amd import api, repair_after_deletion
+def test_small_suffix_takes_the_ceiling(model, tokenizer, budget):
+    from kv_cache_repair_amd import select_support
 
-    def forbidden(*args, **kwargs):
-        raise AssertionError("no device work may run for a refused request")
+    result = select_support(model, tokenizer, "prefix alpha beta gamma", "alpha", suffix_start=1,
+                            budget_percent=budget)
+    assert (result.suffix_tokens, result.budget_tokens, len(result.positions)) == (3, 1, 1)
+    assert 1 <= result.positions[0] < 4
 
-    monkeypatch.setattr(api, "build_halo_cache", forbidden)
-    monkeypatch.setattr(api, "packed_refresh_owned_", forbidden)
+
+@pytest.mark.parametrize("budget", [2, 5])
+def test_partial_budget_repair_matches_the_sequential_recurrence(model, tokenizer, budget):
+    """tests/test_api.py:152-171 at the partial budgets: the default call selects
+    by semantic units and its cache equals the reference recurrence over the
+    same intervals; the input cache is untouched and the output owned."""
+    from kv_cache_repair_amd import repair_after_deletion, select_support
+
     req = request(model, tokenizer)
     snap = snapshot(req["old_cache"])
-    with pytest.raises(NotImplementedError, match=rf"\({budget} of 100 suffix tokens\)"):
-        repair_after_deletion(**req, budget_percent=budget)
+    result = repair_after_deletion(**req, budget_percent=budget)
+    assert result.edited_text == "prefix " + SUFFIX
+    assert result.selection.budget_tokens == budget and result.selection.metadata["selection"] == "sur"
+    alone = select_support(model, tokenizer, result.edited_text, "alpha", suffix_start=1, budget_percent=budget)
+    assert result.selection.positions == alone.positions
+    assert list(result.selection.positions) == f64_selection(model, tokenizer, result.edited_text, "alpha", 1,
+                                                             budget)
+    old_ids = tokenizer(req["original_text"], add_special_tokens=False, return_tensors="pt")["input_ids"]
+    shifted, _ = ref.build_halo_cache(model, req["old_cache"], old_ids.to(model.device), result.input_ids, 0)
+    expected = ref.sequential_repair(model, shifted, result.input_ids, list(result.selection.intervals))
+    assert_caches_close(result.cache, expected)
     assert_unchanged(req["old_cache"], snap)
+    for new, old in zip(result.cache.layers, req["old_cache"].layers):
+        assert new.keys.data_ptr() != old.keys.data_ptr() and new.values.data_ptr() != old.values.data_ptr()
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -341,14 +341,47 @@ def test_select_support_budget_edges_without_a_forward(api_model, tokenizer, bud
     assert result.metadata["selection"] == ("shift_only" if budget == 0 else "full_suffix")
 
 
+def _host_scores(monkeypatch):
+    """The oracle's float64 scorer in place of the device scorer (test only: the
+    package's scorer has no CPU path)."""
+    from kv_cache_repair_amd import api
+
+    def scores(*, model, edited_input_ids, query_token_ids):
+        table = model.generator.get_input_embeddings().weight.detach().double().numpy()
+        values = orc.query_relevance_f64(table, edited_input_ids[0].numpy(), query_token_ids)
+        return [float(v) for v in values], {"exact_token_boost": 0.25}
+
+    monkeypatch.setattr(api, "dense_query_relevance_scores", scores)
+
+
 @pytest.mark.parametrize("budget,suffix,want", [(2, 100, 2), (5, 100, 5), (2, 3, 1), (5, 3, 1), (50, 3, 2)])
-def test_partial_budgets_name_their_ceiling_and_need_caller_selection(api_model, tokenizer, budget, suffix, want):
-    """ceil(pct/100 * suffix) rows (api.py:77), never rounded to nearest; budgets
-    strictly between empty and the whole suffix need SUR selection, which this
-    build leaves to the caller (repair_with_positions)."""
-    text = "prefix " + " ".join(["alpha"] * suffix)
-    with pytest.raises(NotImplementedError, match=rf"\({want} of {suffix} suffix tokens\)"):
-        select_support(api_model, tokenizer, text, "alpha", suffix_start=1, budget_percent=budget)
+def test_partial_budgets_take_their_ceiling_through_semantic_units(api_model, tokenizer, monkeypatch, budget,
+                                                                    suffix, want):
+    """ceil(pct/100 * suffix) rows (api.py:77), never rounded to nearest, chosen
+    by the semantic-unit allocation (tests/test_api.py:100-149)."""
+    _host_scores(monkeypatch)
+    text = "prefix " + " ".join(["alpha", "beta", "gamma", "."] * (suffix // 4) + ["alpha"] * (suffix % 4))
+    result = select_support(api_model, tokenizer, text, "alpha", suffix_start=1, budget_percent=budget)
+    assert (result.suffix_tokens, result.budget_tokens) == (suffix, want)
+    assert len(result.positions) == len(set(result.positions)) == want
+    assert list(result.positions) == sorted(result.positions) and all(1 <= p <= suffix for p in result.positions)
+    assert [p for s, e in result.intervals for p in range(s, e)] == list(result.positions)
+    assert result.metadata["selection"] == "sur" and result.metadata["budget_percent"] == budget
+    assert result.metadata["allocator"]["budget_tokens"] == want
+
+
+def test_partial_budgets_on_a_host_model_fail_in_the_device_scorer(api_model, tokenizer):
+    """No CPU fallback: the scorer refuses a model that is not on a ROCm device."""
+    text = "prefix " + "alpha beta gamma . " * 25
+    with pytest.raises(ValueError, match="ROCm GPU device"):
+        select_support(api_model, tokenizer, text, "alpha", suffix_start=1, budget_percent=5)
+
+
+def test_empty_query_is_refused_by_the_selection(api_model, tokenizer, monkeypatch):
+    _host_scores(monkeypatch)
+    with pytest.raises(ValueError, match="query text tokenization is empty"):
+        select_support(api_model, tokenizer, "prefix " + "alpha beta gamma . " * 25, "", suffix_start=1,
+                       budget_percent=5)
 
 
 def test_repair_rejects_training_mode_before_any_device_work(api_model, tokenizer):
