@@ -2,8 +2,9 @@
 
 Mirrors the reference public surface (src/kv_cache_repair/api.py):
 ``Selection``, ``RepairResult``, ``select_support`` and
-``repair_after_deletion(..., executor="packed")``. Positional correction
-(build_halo_cache) and the packed refresh run on libkvrepair.
+``repair_after_deletion(..., executor="packed" | "sequential")``. Positional
+correction (build_halo_cache), the packed refresh and the sequential
+executor's writeback run on libkvrepair.
 
 Support selection follows the reference (api.py:62-110): 0% selects nothing,
 100% the whole suffix, and any budget in between the semantic-unit (SUR)
@@ -15,6 +16,7 @@ allocation over the GPU query-relevance scores (``semantic_units`` on the host,
 from __future__ import annotations
 
 import math
+import time
 from dataclasses import dataclass
 from typing import Any, Sequence
 
@@ -22,7 +24,7 @@ import torch
 
 from .alignment import token_alignment_arrays
 from .cache import OperatorShim, build_halo_cache
-from .execution import positions_to_intervals
+from .execution import _refresh_intervals_, positions_to_intervals
 from .scoring import dense_query_relevance_scores, query_text_token_ids
 from .semantic_units import select_semantic_unit_support, semantic_unit_token_ranges
 from .kernels.executor import layer_kv
@@ -194,10 +196,11 @@ def _prepare(model, tokenizer, old_cache, original_text, start, end):
     return old_ids, edited_text, edited_ids
 
 
-def _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text, selector):
+def _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text, selector, executor="packed"):
     """Select first (the suffix start comes from the host alignment, the same
     one build_halo_cache computes), so a selection error leaves no shifted cache
-    behind; then shift and refresh."""
+    behind; then shift and refresh the private shifted cache in place (packed:
+    one pass over every selected row; sequential: the interval recurrence)."""
     alignment = token_alignment_arrays(old_ids[0].numpy(), edited_ids[0].numpy())
     selection = selector(int(edited_ids.shape[1]), int(alignment["new_suffix_start"]))
     shim = OperatorShim(model, tokenizer)
@@ -206,9 +209,17 @@ def _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text, sele
     shifted, alignment = build_halo_cache(shim, old_cache, old_ids, edited_ids, halo_tokens=0)
     if int(alignment["new_suffix_start"]) != selection.suffix_start:
         raise RuntimeError("host alignment and shift-cache alignment disagree")
-    execution = packed_refresh_owned_(shim, shifted, edited_dev, list(selection.intervals))
+    if executor == "packed":
+        execution = packed_refresh_owned_(shim, shifted, edited_dev, list(selection.intervals))
+    else:
+        started = time.perf_counter()
+        intervals = list(selection.intervals)
+        _refresh_intervals_(shim, shifted, edited_dev, intervals)
+        execution = {"executor": "sequential_interval_repair", "interval_count": len(intervals),
+                     "recomputed_tokens": sum(e - s for s, e in intervals),
+                     "seconds": time.perf_counter() - started, "conditioned_on_earlier_intervals": True}
     return RepairResult(cache=shifted, edited_text=edited_text, input_ids=edited_dev, selection=selection,
-                        metadata={"alignment": alignment, "execution": execution, "executor": "packed"})
+                        metadata={"alignment": alignment, "execution": execution, "executor": executor})
 
 
 @torch.no_grad()
@@ -217,20 +228,24 @@ def repair_after_deletion(model: Any, tokenizer: Any, old_cache: Any, original_t
                           executor: str = "packed") -> RepairResult:
     """Delete a character span, correct positions, refresh selected suffix KV.
 
-    Same contract as the reference (api.py:169-244) with executor="packed":
-    the input cache is never modified, boundary tokens whose tokenization
-    changed are recomputed outside the suffix budget, and the returned cache is
-    independently owned. The shifted cache built here is private, so the
-    packed refresh scatters into it in place instead of cloning it again.
+    Same contract as the reference (api.py:169-244): the input cache is never
+    modified, boundary tokens whose tokenization changed are recomputed outside
+    the suffix budget, and the returned cache is independently owned.
+    ``executor="packed"`` refreshes every selected row in one pass on
+    libkvrepair; ``"sequential"`` is the interval recurrence (one model forward
+    per interval, each conditioned on the intervals before it, fresh rows
+    written back by kvr_copy_kv_interval). The shifted cache built here is
+    private, so either executor writes into it in place instead of cloning it
+    again.
     """
     budget_percent = _check_budget(budget_percent)
-    if executor != "packed":
-        raise ValueError("executor must be 'packed' (the sequential interval executor is not part of this build)")
+    if executor not in ("packed", "sequential"):
+        raise ValueError("executor must be 'packed' or 'sequential'")
     start, end = _check_span(original_text, delete_span)
     old_ids, edited_text, edited_ids = _prepare(model, tokenizer, old_cache, original_text, start, end)
     return _refresh(model, tokenizer, old_cache, old_ids, edited_ids, edited_text,
                     lambda length, suffix_start: _budget_selection(model, tokenizer, edited_text, query, edited_ids,
-                                                                   suffix_start, budget_percent))
+                                                                   suffix_start, budget_percent), executor)
 
 
 @torch.no_grad()

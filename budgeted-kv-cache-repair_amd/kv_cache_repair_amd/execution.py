@@ -1,6 +1,19 @@
-"""Support-set helpers shared by the API and the executors."""
+"""Support-set helpers and the sequential interval executor.
+
+``positions_to_intervals`` and ``sequential_repair`` keep the reference's
+names and contract (src/kv_cache_repair/execution.py:14-59).
+"""
 
 from __future__ import annotations
+
+import time
+from typing import Any
+
+import torch
+
+from .cache import cache_from_tensors, clone_cache, run_tokens_from_prefix
+from .kernels.executor import _validate_cache, layer_kv
+from .kernels.writeback import scatter_fresh_kv
 
 
 def positions_to_intervals(positions: list[int]) -> list[tuple[int, int]]:
@@ -13,3 +26,69 @@ def positions_to_intervals(positions: list[int]) -> list[tuple[int, int]]:
         else:
             runs.append([p, p + 1])
     return [(start, end) for start, end in runs]
+
+
+def _validate_sequential_intervals(intervals, length: int) -> list[tuple[int, int]]:
+    """Sorted, disjoint, non-empty ranges inside [0, length); adjacent ranges are
+    allowed (reference execution.py:26-31)."""
+    out = []
+    previous_end = 0
+    for start, end in intervals:
+        start, end = int(start), int(end)
+        if not previous_end <= start < end <= length:
+            raise ValueError("intervals must be sorted, disjoint, and within the edited sequence")
+        out.append((start, end))
+        previous_end = end
+    return out
+
+
+def _refresh_intervals_(shim: Any, cache: Any, edited_ids_t: torch.Tensor, intervals) -> None:
+    """The interval recurrence IN PLACE on a cache the caller owns.
+
+    Interval [s, e) runs the model's own forward over its tokens after a view of
+    the cache's first s rows (the forward's cache update concatenates into new
+    tensors, so the view is only read), then its fresh K/V rows are copied over
+    rows [s, e) of every layer by kvr_copy_kv_interval (a bit copy), so the next
+    interval attends to them.
+    """
+    layers = [layer_kv(cache, i) for i in range(len(cache.layers))]
+    for start, end in intervals:
+        prefix = cache_from_tensors([(k[:, :, :start], v[:, :, :start]) for k, v in layers])
+        fresh = run_tokens_from_prefix(shim, prefix, edited_ids_t[:, start:end], end)
+        for i, (key, value) in enumerate(layers):
+            new_key, new_value = layer_kv(fresh, i)
+            if (new_key.dtype != key.dtype or new_value.dtype != value.dtype or new_key.device != key.device
+                    or new_key.shape[:2] != key.shape[:2] or new_key.shape[3] != key.shape[3]
+                    or new_key.shape[2] != end or new_value.shape != new_key.shape):
+                raise ValueError(f"recomputed K/V of layer {i} do not match the cache's layout or dtype")
+            scatter_fresh_kv(key, value, new_key[:, :, start:end], new_value[:, :, start:end], start, end)
+
+
+@torch.no_grad()
+def sequential_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
+                      intervals: list[tuple[int, int]]) -> tuple[Any, dict[str, Any]]:
+    """Refresh the intervals in order, each conditioned on the rows refreshed
+    before it (reference execution.py:34-59 over cache.py:147-192).
+
+    The reference rebuilds every layer per interval (a prefix clone, then a
+    concatenation of three pieces); here the output is cloned once, in one
+    libkvrepair launch for every layer, and each interval writes only its own
+    rows (``_refresh_intervals_``). The base cache is not modified; with no
+    interval it is returned as it is, as the reference returns it. ``seconds``
+    is host time, as in the reference (GPU work may still be queued).
+    """
+    length = int(edited_ids_t.shape[1])
+    intervals = _validate_sequential_intervals(intervals, length)
+    cache = base_cache
+    started = time.perf_counter()
+    if intervals:
+        _validate_cache(base_cache, length)
+        cache = clone_cache(base_cache)
+        _refresh_intervals_(shim, cache, edited_ids_t, intervals)
+    return cache, {
+        "executor": "sequential_interval_repair",
+        "interval_count": len(intervals),
+        "recomputed_tokens": sum(end - start for start, end in intervals),
+        "seconds": time.perf_counter() - started,
+        "conditioned_on_earlier_intervals": True,
+    }

@@ -2,8 +2,9 @@
 tokenizer), against the oracle's restatement of the reference's schedules.
 
 Vectors follow the reference's public-contract tests (tests/test_api.py:
-100-273): 0%, 2%, 5% (semantic-unit selection) and 100% budgets agree with the
-sequential interval recurrence, partial budgets take their ceiling,
+100-273): the packed and sequential executors agree at 0%, 2%, 5%
+(semantic-unit selection) and 100% budgets, and with the reference's interval
+recurrence, partial budgets take their ceiling,
 the full suffix reproduces a clean prefill, trailing and whole-prompt
 deletions leave an empty suffix, boundary retokenization is recomputed outside
 the budget, a cache of the wrong length is refused, and the input cache is
@@ -112,22 +113,49 @@ def test_budget_edges_match_the_sequential_recurrence_and_keep_the_input(model, 
         assert new.keys.data_ptr() != old.keys.data_ptr() and new.values.data_ptr() != old.values.data_ptr()
 
 
-def test_full_suffix_repair_reproduces_a_clean_prefill(model, tokenizer):
+@pytest.mark.parametrize("budget", [0, 2, 5, 100])
+def test_packed_and_sequential_agree_and_keep_the_input(model, tokenizer, budget):
+    """tests/test_api.py:152-171: both executors select the same positions, give
+    the same cache, never modify the input and own their output."""
     from kv_cache_repair_amd import repair_after_deletion
 
-    result = repair_after_deletion(**request(model, tokenizer), budget_percent=100)
+    req = request(model, tokenizer)
+    snap = snapshot(req["old_cache"])
+    sequential = repair_after_deletion(**req, budget_percent=budget, executor="sequential")
+    packed = repair_after_deletion(**req, budget_percent=budget, executor="packed")
+    assert packed.edited_text == "prefix " + SUFFIX and tuple(packed.input_ids.shape) == (1, 101)
+    assert packed.selection.positions == sequential.selection.positions
+    assert packed.selection.budget_tokens == budget
+    assert (sequential.metadata["executor"], packed.metadata["executor"]) == ("sequential", "packed")
+    assert sequential.metadata["execution"]["executor"] == "sequential_interval_repair"
+    assert packed.metadata["alignment"]["mandatory_changed_tokens"] == 0
+    assert packed.metadata["alignment"]["position_shift"] == -2
+    assert_caches_close(packed.cache, sequential.cache)
+    assert_unchanged(req["old_cache"], snap)
+    for result in (packed, sequential):
+        for new, old in zip(result.cache.layers, req["old_cache"].layers):
+            assert new.keys.data_ptr() != old.keys.data_ptr() and new.values.data_ptr() != old.values.data_ptr()
+
+
+@pytest.mark.parametrize("executor", ["packed", "sequential"])
+def test_full_suffix_repair_reproduces_a_clean_prefill(model, tokenizer, executor):
+    from kv_cache_repair_amd import repair_after_deletion
+
+    result = repair_after_deletion(**request(model, tokenizer), budget_percent=100, executor=executor)
     assert result.selection.positions == tuple(range(1, 101))
     assert_caches_close(result.cache, prefill(model, tokenizer, result.edited_text))
 
 
+@pytest.mark.parametrize("executor", ["packed", "sequential"])
 @pytest.mark.parametrize("span,edited", [((7, 21), "prefix "), ((0, 21), "")])
-def test_trailing_and_whole_prompt_deletions_leave_an_empty_suffix(model, tokenizer, span, edited):
+def test_trailing_and_whole_prompt_deletions_leave_an_empty_suffix(model, tokenizer, span, edited, executor):
     from kv_cache_repair_amd import repair_after_deletion
 
     original = "prefix obsolete alpha"
     old = prefill(model, tokenizer, original)
     snap = snapshot(old)
-    result = repair_after_deletion(model, tokenizer, old, original, delete_span=span, query="", budget_percent=5)
+    result = repair_after_deletion(model, tokenizer, old, original, delete_span=span, query="", budget_percent=5,
+                                   executor=executor)
     assert result.edited_text == edited
     assert result.selection.suffix_tokens == result.selection.budget_tokens == 0
     assert result.selection.positions == result.selection.intervals == ()
@@ -138,14 +166,15 @@ def test_trailing_and_whole_prompt_deletions_leave_an_empty_suffix(model, tokeni
         assert torch.equal(new.keys, src.keys[:, :, :kept]) and torch.equal(new.values, src.values[:, :, :kept])
 
 
-def test_boundary_retokenization_is_recomputed_outside_the_budget(model, tokenizer):
+@pytest.mark.parametrize("executor", ["packed", "sequential"])
+def test_boundary_retokenization_is_recomputed_outside_the_budget(model, tokenizer, executor):
     from kv_cache_repair_amd import repair_after_deletion
 
     original = "prefix red blue alpha beta"
     join = original.index(" blue")
     old = prefill(model, tokenizer, original)
     result = repair_after_deletion(model, tokenizer, old, original, delete_span=(join, join + 1), query="alpha",
-                                   budget_percent=0)
+                                   budget_percent=0, executor=executor)
     assert result.edited_text == "prefix redblue alpha beta"
     assert result.input_ids.tolist() == [[1, 10, 4, 5]]
     assert (result.selection.suffix_start, result.selection.suffix_tokens, result.selection.budget_tokens) == (2, 2, 0)

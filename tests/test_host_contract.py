@@ -310,8 +310,8 @@ def test_repair_rejects_invalid_spans_before_touching_the_model(delete_span):
         repair_with_positions(None, None, None, "alpha", delete_span=delete_span, positions=[])
 
 
-@pytest.mark.parametrize("executor", ["unknown", "sequential", "direct", ""])
-def test_repair_rejects_executors_other_than_packed_before_touching_the_model(executor):
+@pytest.mark.parametrize("executor", ["unknown", "direct", "Packed", ""])
+def test_repair_rejects_unknown_executors_before_touching_the_model(executor):
     with pytest.raises(ValueError, match="executor"):
         repair_after_deletion(None, None, None, "alpha", delete_span=(0, 1), query="alpha", executor=executor)
 
