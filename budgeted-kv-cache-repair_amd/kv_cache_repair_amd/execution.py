@@ -92,3 +92,37 @@ def sequential_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
         "seconds": time.perf_counter() - started,
         "conditioned_on_earlier_intervals": True,
     }
+
+
+@torch.no_grad()
+def oneshot_sparse_repair(shim: Any, base_cache: Any, edited_ids_t: torch.Tensor,
+                          intervals: list[tuple[int, int]]) -> tuple[Any, dict[str, Any]]:
+    """One forward over every selected position at its absolute position
+    (reference execution.py:62-140, the control schedule of its benchmark).
+
+    Every selected row attends causally to the cache in which all selected rows
+    of that layer are already refreshed; the reference gets this schedule from a
+    StaticCache written at absolute cache positions. It is the packed
+    executor's schedule, so it runs on that path (libkvrepair attention and
+    scatter): adjacent intervals, which the reference accepts here, are
+    coalesced into the packed executor's maximal runs first. The base cache is
+    not modified; with no interval it is returned as it is.
+    """
+    from .kernels.packed_cache import packed_interval_repair
+
+    length = int(edited_ids_t.shape[1])
+    intervals = _validate_sequential_intervals(intervals, length)
+    positions = [p for start, end in intervals for p in range(start, end)]
+    started = time.perf_counter()
+    if not positions:
+        return base_cache, {"executor": "oneshot_sparse_repair", "interval_count": 0, "recomputed_tokens": 0,
+                            "seconds": 0.0}
+    output, _ = packed_interval_repair(shim, base_cache, edited_ids_t, positions_to_intervals(positions))
+    return output, {
+        "executor": "oneshot_sparse_repair",
+        "interval_count": len(intervals),
+        "recomputed_tokens": len(positions),
+        "rows_written": len(positions),
+        "seconds": time.perf_counter() - started,
+        "absolute_position_ids_used": True,
+    }

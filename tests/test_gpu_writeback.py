@@ -271,3 +271,38 @@ def test_direct_executor_returns_the_base_for_an_empty_support(gpu_device):
     model.train()
     with pytest.raises(ValueError, match="eval-mode"):
         direct_interval_repair(OperatorShim(model), base, ids, [(0, 2)])
+
+
+@pytest.mark.parametrize("dtype,attn", PRECISIONS)
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+def test_oneshot_control_equals_the_reference_packed_schedule(gpu_device, family, dtype, attn):
+    """The one-shot control (every selected row in one forward at its absolute
+    position) is the packed schedule: against the reference's packed SDPA
+    restatement within the packed executor's tolerances; adjacent intervals are
+    accepted and coalesced, an empty support returns the base."""
+    from kv_cache_repair_amd.cache import OperatorShim
+    from kv_cache_repair_amd.execution import oneshot_sparse_repair
+    from oracle import reference_path as ref
+
+    model = _tiny_model(family, dtype, gpu_device)
+    model.set_attn_implementation(attn)
+    gen = torch.Generator(device=gpu_device).manual_seed(13)
+    ids = torch.randint(0, 64, (1, 64), device=gpu_device, generator=gen)
+    with torch.no_grad():
+        base = model.base_model(input_ids=ids, use_cache=True).past_key_values
+    edited = ids.clone()
+    edited[0, 2::4] = torch.randint(0, 64, (16,), device=gpu_device, generator=gen)
+    snap = [(l.keys.clone(), l.values.clone()) for l in base.layers]
+    out, receipt = oneshot_sparse_repair(OperatorShim(model), base, edited, [(2, 6), (6, 9), (30, 31), (50, 64)])
+    assert receipt["executor"] == "oneshot_sparse_repair" and receipt["recomputed_tokens"] == 22
+    assert receipt["interval_count"] == 4 and receipt["absolute_position_ids_used"] is True
+    want = ref.packed_sdpa_repair(model, base, edited, [(2, 9), (30, 31), (50, 64)])
+    tol = dict(rtol=1e-5, atol=2e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    for got, w, (k0, v0), b in zip(out.layers, want.layers, snap, base.layers):
+        torch.testing.assert_close(got.keys, w.keys, **tol)
+        torch.testing.assert_close(got.values, w.values, **tol)
+        assert same_bits(b.keys, k0) and same_bits(b.values, v0)
+    same, receipt = oneshot_sparse_repair(OperatorShim(model), base, edited, [])
+    assert same is base and receipt["recomputed_tokens"] == 0
+    with pytest.raises(ValueError, match="sorted, disjoint, and within"):
+        oneshot_sparse_repair(OperatorShim(model), base, edited, [(5, 9), (8, 10)])
