@@ -918,13 +918,40 @@ def interleaved_latency(calls: dict, warmups: int, repeats: int, seed: int) -> d
     return {name: summary(v) for name, v in samples.items()}
 
 
+def reference_sequential(model, shifted, ids, intervals):
+    """The reference's sequential schedule on this GPU (execution.py:34-59 over
+    cache.py:147-192): per interval a clone of every layer's prefix, the native
+    forward over the interval's tokens, then a new cache concatenated from the
+    old rows before, the fresh rows and the old rows after."""
+    from kv_cache_repair_amd.cache import cache_from_tensors
+
+    cache = shifted
+    for start, end in intervals:
+        prefix = cache_from_tensors([(l.keys[:, :, :start].clone(), l.values[:, :, :start].clone())
+                                     for l in cache.layers])
+        mask = torch.ones((1, end), dtype=torch.long, device=ids.device)
+        fresh = model.model(input_ids=ids[:, start:end], attention_mask=mask, past_key_values=prefix, use_cache=True,
+                            return_dict=True).past_key_values
+        cache = cache_from_tensors([
+            (torch.cat((o.keys[:, :, :start], f.keys[:, :, start:end], o.keys[:, :, end:]), dim=2),
+             torch.cat((o.values[:, :, :start], f.values[:, :, start:end], o.values[:, :, end:]), dim=2))
+            for o, f in zip(cache.layers, fresh.layers)])
+    return cache
+
+
 def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats: int, seed: int) -> dict:
     """One case of the reference grid: a stale cache of ``length + 8`` tokens (K/V
     ~ N(0,1)) loses 8 tokens at length // 8 and is shifted (untimed); then the
     packed refresh alone (ownership copy, plan upload, layer-major forward) is
     timed for this build and for the reference path, interleaved in shuffled
-    order (benchmark_refresh.py:52-61, 106-126)."""
+    order (benchmark_refresh.py:52-61, 106-126). The reference benchmark's
+    other schedules are timed beside them: this build's sequential and direct
+    executors against the reference's sequential schedule, which they must
+    equal bit for bit (benchmark_refresh.py:150-153; direct with contiguous
+    attention rows)."""
     from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache, cache_from_tensors
+    from kv_cache_repair_amd.execution import sequential_repair
+    from kv_cache_repair_amd.kernels.direct_cache import direct_interval_repair
     from kv_cache_repair_amd.kernels.packed_cache import packed_interval_repair
 
     device = model.device
@@ -943,12 +970,27 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
     intervals = selected_intervals(length, budget, count)
     positions = [p for s, e in intervals for p in range(s, e)]
     calls = {"hip": lambda: packed_interval_repair(shim, shifted, ids, intervals)[0],
-             "reference_packed_sdpa": lambda: reference_stage(model, None, None, ids, intervals, shifted=shifted)}
+             "reference_packed_sdpa": lambda: reference_stage(model, None, None, ids, intervals, shifted=shifted),
+             "sequential": lambda: sequential_repair(shim, shifted, ids, intervals)[0],
+             "direct": lambda: direct_interval_repair(shim, shifted, ids, intervals,
+                                                      attention_layout="contiguous")[0],
+             "reference_sequential": lambda: reference_sequential(model, shifted, ids, intervals)}
     outputs = {name: fn() for name, fn in calls.items()}
     index = torch.tensor(positions, device=device)
-    max_abs = max((a.index_select(2, index).float() - b.index_select(2, index).float()).abs().max().item()
-                  for la, lb in zip(outputs["hip"].layers, outputs["reference_packed_sdpa"].layers)
-                  for a, b in ((la.keys, lb.keys), (la.values, lb.values)))
+
+    def max_abs_rows(x, y):
+        return max((a.index_select(2, index).float() - b.index_select(2, index).float()).abs().max().item()
+                   for la, lb in zip(x.layers, y.layers) for a, b in ((la.keys, lb.keys), (la.values, lb.values)))
+
+    def bitwise(x, y):
+        return all(torch.equal(a.view(torch.int16), b.view(torch.int16))
+                   for la, lb in zip(x.layers, y.layers) for a, b in ((la.keys, lb.keys), (la.values, lb.values)))
+
+    max_abs = max_abs_rows(outputs["hip"], outputs["reference_packed_sdpa"])
+    same_schedule = {name: {"bitwise_equal": bitwise(outputs[name], outputs["reference_sequential"]),
+                            "max_abs": max_abs_rows(outputs[name], outputs["reference_sequential"])}
+                     for name in ("sequential", "direct")}
+    packed_vs_sequential = max_abs_rows(outputs["hip"], outputs["reference_sequential"])
     del outputs
     lat = interleaved_latency(calls, warmups, repeats, seed)
     return {"metric": "refresh-only latency (ms), reference benchmark grid", "length": length,
@@ -957,6 +999,10 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
             "value": lat["hip"]["median_ms"], "unit": "ms", "higher_is_better": False,
             "reference_same_gpu_ms": lat["reference_packed_sdpa"]["median_ms"],
             "speedup": lat["reference_packed_sdpa"]["median_ms"] / lat["hip"]["median_ms"],
+            "sequential_ms": lat["sequential"]["median_ms"], "direct_ms": lat["direct"]["median_ms"],
+            "reference_sequential_ms": lat["reference_sequential"]["median_ms"],
+            "same_schedule_vs_reference_sequential": same_schedule,
+            "packed_max_abs_vs_reference_sequential": packed_vs_sequential,
             "latency": lat, "max_abs_vs_reference": max_abs, "warmups": warmups, "repeats": repeats, "seed": seed,
             "scope": "refresh only (ownership copy, plan upload, packed forward); the shift is untimed as in the "
                      "reference benchmark", "dtype": "bf16",
