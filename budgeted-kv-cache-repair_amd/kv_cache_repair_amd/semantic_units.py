@@ -101,27 +101,31 @@ def _json_spans(text: str, start: int, end: int) -> Iterable[tuple[int, int]]:
     when the container has no newline before the bracket (as the reference
     computes it)."""
     decoder = json.JSONDecoder()
-    bounded = text[:end]
+    window = text[start:end]  # decoding stops at the container's end
     cursor = start
     while cursor < end:
         m = _JSON_OPEN.search(text, cursor, end)
         if m is None:
             return
         open_at = m.start()
-        lead = text[text.rfind("\n", start, open_at) + 1:open_at].strip()
-        if lead and not lead.endswith(_JSON_LEADS):
+        # the last non-space character of the line before the bracket, if any
+        line_start = text.rfind("\n", start, open_at) + 1
+        j = open_at - 1
+        while j >= line_start and text[j].isspace():
+            j -= 1
+        if j >= line_start and text[j] not in _JSON_LEADS:
             cursor = open_at + 1
             continue
         try:
-            value, close_at = decoder.raw_decode(bounded, open_at)
+            value, close_rel = decoder.raw_decode(window, open_at - start)
         except json.JSONDecodeError:
             cursor = open_at + 1
             continue
         if not isinstance(value, (dict, list)):
             cursor = open_at + 1
             continue
-        yield open_at, close_at
-        cursor = close_at
+        yield open_at, start + close_rel
+        cursor = start + close_rel
 
 
 def _pieces(text: str, start: int, end: int, cid: Any, kind: str) -> list[tuple[int, int, Any, str, str]]:
