@@ -1898,6 +1898,47 @@ struct Chunk {
     int32_t group, index, begin, end;
 };
 
+// Modelled cost of one block besides its sub-tiles (dispatch, prologue, the
+// key-class combine and the partial stores), and of merging one chunk of a split
+// group (its partials written and read back), in sub-tile cost units.
+constexpr int64_t kCostBlock = 16;
+constexpr int64_t kCostMergeChunk = 2;
+
+int64_t chunk_cost(const GroupKeys& k, const Chunk& c) {
+    int64_t cost = 0;
+    for (int64_t s = c.begin / kSub; s < (c.end + kSub - 1) / kSub; ++s) cost += subtile_cost(k, s);
+    return cost;
+}
+
+// Longest-first order: whole groups (their chunks stay contiguous and in chunk
+// order, as the merge reads them) sorted by their chunks' largest cost, so the
+// blocks that take longest are dispatched first and the cheap ones fill in.
+void order_longest_first(const std::vector<GroupKeys>& keys, std::vector<Chunk>& chunks) {
+    std::vector<int64_t> worst(keys.size(), 0);
+    for (const Chunk& c : chunks) worst[c.group] = std::max(worst[c.group], chunk_cost(keys[c.group], c));
+    std::stable_sort(chunks.begin(), chunks.end(), [&](const Chunk& a, const Chunk& b) {
+        if (a.group == b.group) return a.index < b.index;
+        return worst[a.group] > worst[b.group] || (worst[a.group] == worst[b.group] && a.group < b.group);
+    });
+}
+
+// Modelled span of one head's blocks in dispatch order on the `cus` CUs its
+// blocks run on (the blocks of one head land on that head's XCD): each block
+// goes to the CU that frees first; split groups add their merge work.
+int64_t schedule_span(const std::vector<GroupKeys>& keys, std::vector<Chunk>& chunks, int64_t cus) {
+    order_longest_first(keys, chunks);
+    std::vector<int64_t> load(static_cast<size_t>(cus > 0 ? cus : 1), 0);
+    std::vector<int32_t> count(keys.size(), 0);
+    for (const Chunk& c : chunks) {
+        auto least = std::min_element(load.begin(), load.end());
+        *least += chunk_cost(keys[c.group], c) + kCostBlock;
+        ++count[c.group];
+    }
+    int64_t merge = 0;
+    for (int32_t n : count) merge += n > 1 ? n * kCostMergeChunk : 0;
+    return *std::max_element(load.begin(), load.end()) + merge;
+}
+
 // ---------------------------------------------------------------------------
 // Static scratch of kvr_packed_causal_attention_noalloc: the split-K partials
 // live in this file-scope device array instead of a caller workspace. Each
@@ -2021,47 +2062,68 @@ extern "C" int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n
             total += group_cost[g];
         }
         const int64_t per_head = kTargetBlocks / heads > 1 ? kTargetBlocks / heads : 1;
-        auto chunks_of = [&](int64_t g, int64_t cap) {
-            const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
-            int64_t nc = (group_cost[g] + cap - 1) / cap;
-            nc = nc < 1 ? 1 : nc;
-            nc = nc > n_sub ? n_sub : nc;
-            return nc > kMaxChunksPerGroup ? int64_t(kMaxChunksPerGroup) : nc;
-        };
-        // Per-chunk cost cap: the even share of the total. The tile kernel
-        // (one block per CU) raises it until the groups' rounded-up chunk
-        // counts fit the share too (no second, partial round of blocks), or
-        // every group is one chunk; the wide kernel runs two blocks per CU.
-        int64_t cap = (total + per_head - 1) / per_head;
         const int64_t max_cost = *std::max_element(group_cost.begin(), group_cost.end());
         // (The head-pair kernel also runs one block per CU in 64-row groups.)
         const bool one_block_per_cu = group_rows == kTileGroupRows || (mfma && qt == 4 && KVR_ATTN_PAIR);
-        while (one_block_per_cu) {
-            int64_t sum = 0;
-            for (int64_t g = 0; g < n_groups; ++g) sum += chunks_of(g, cap);
-            if (sum <= per_head || cap >= max_cost) break;
-            cap += (cap + 15) / 16;
-        }
-        for (int64_t g = 0; g < n_groups; ++g) {
-            const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
-            const int64_t nc = chunks_of(g, cap);
-            // Boundary i closes the chunk once the running cost reaches i/nc of
-            // the group's cost, leaving at least one sub-tile per later chunk.
-            int64_t s = 0, acc = 0;
-            for (int64_t i = 0; i < nc; ++i) {
-                const int64_t begin = s;
-                if (i == nc - 1) {
-                    s = n_sub;
-                } else {
-                    const int64_t goal = group_cost[g] * (i + 1) / nc;
-                    do {
-                        acc += subtile_cost(keys[g], s);
-                        ++s;
-                    } while (acc < goal && n_sub - s > nc - 1 - i);
+        // Chunks for a share of `share` blocks per head.
+        auto build = [&](int64_t share) {
+            auto chunks_of = [&](int64_t g, int64_t cap) {
+                const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
+                int64_t nc = (group_cost[g] + cap - 1) / cap;
+                nc = nc < 1 ? 1 : nc;
+                nc = nc > n_sub ? n_sub : nc;
+                return nc > kMaxChunksPerGroup ? int64_t(kMaxChunksPerGroup) : nc;
+            };
+            // Per-chunk cost cap: the even share of the total. The tile kernel
+            // (one block per CU) raises it until the groups' rounded-up chunk
+            // counts fit the share too (no extra, partial round of blocks), or
+            // every group is one chunk; the wide kernel runs two blocks per CU.
+            int64_t cap = (total + share - 1) / share;
+            while (one_block_per_cu) {
+                int64_t sum = 0;
+                for (int64_t g = 0; g < n_groups; ++g) sum += chunks_of(g, cap);
+                if (sum <= share || cap >= max_cost) break;
+                cap += (cap + 15) / 16;
+            }
+            std::vector<Chunk> out;
+            for (int64_t g = 0; g < n_groups; ++g) {
+                const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
+                const int64_t nc = chunks_of(g, cap);
+                // Boundary i closes the chunk once the running cost reaches i/nc of
+                // the group's cost, leaving at least one sub-tile per later chunk.
+                int64_t s = 0, acc = 0;
+                for (int64_t i = 0; i < nc; ++i) {
+                    const int64_t begin = s;
+                    if (i == nc - 1) {
+                        s = n_sub;
+                    } else {
+                        const int64_t goal = group_cost[g] * (i + 1) / nc;
+                        do {
+                            acc += subtile_cost(keys[g], s);
+                            ++s;
+                        } while (acc < goal && n_sub - s > nc - 1 - i);
+                    }
+                    const int64_t end = s * kSub < keys[g].kmax ? s * kSub : keys[g].kmax;
+                    out.push_back({static_cast<int32_t>(g), static_cast<int32_t>(i),
+                                   static_cast<int32_t>(begin * kSub), static_cast<int32_t>(end)});
                 }
-                const int64_t end = s * kSub < keys[g].kmax ? s * kSub : keys[g].kmax;
-                chunks.push_back({static_cast<int32_t>(g), static_cast<int32_t>(i),
-                                  static_cast<int32_t>(begin * kSub), static_cast<int32_t>(end)});
+            }
+            return out;
+        };
+        chunks = build(per_head);
+        if (group_rows == kGroupRows && one_block_per_cu) {
+            // 64-row groups (MFMA-bound launches): one block per CU means one round
+            // is balanced only as well as the chunk costs are. Two or four rounds
+            // of smaller chunks let the dispatcher even the CUs out; keep the
+            // share whose modelled span (below) is shortest.
+            int64_t best = schedule_span(keys, chunks, per_head);
+            for (int64_t rounds : {2, 4}) {
+                std::vector<Chunk> more = build(per_head * rounds);
+                const int64_t span = schedule_span(keys, more, per_head);
+                if (span < best) {
+                    best = span;
+                    chunks = std::move(more);
+                }
             }
         }
     }
