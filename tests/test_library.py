@@ -164,8 +164,10 @@ def schedule(positions, n_keys, hq, hkv, dim, dtype=2, chunk=0):
 @pytest.mark.parametrize("positions,n_keys,chunk", [
     ([0, 1, 2], 3, 0), (list(range(928, 992)), 1920, 0), (list(range(0, 4000, 7)), 4000, 256),
     ([5, 9, 4095], 4096, 0), (list(range(1024, 2048)), 2048, 512), (list(range(100, 200)), 300, 64),
-    (list(range(0, 40000, 37)), 40000, 0), ([7], 8, 0)])
+    (list(range(0, 40000, 37)), 40000, 0), ([7], 8, 0), ("c4", 31744, 0)])
 def test_attention_schedule_covers_every_causal_pair_exactly_once(positions, n_keys, chunk):
+    if positions == "c4":
+        positions = c4_positions()
     s = schedule(positions, n_keys, 32, 8, 128, chunk=chunk)
     header, n_groups, longest, n_work, rows = s[:18], s[3], s[4], s[5], s[16]
     assert header[0] == 0x4B565253 and header[1] == 5 and header[17] == 0 and header[2] == len(positions)
@@ -213,6 +215,38 @@ def test_default_chunking_keeps_one_block_per_cu_for_the_c3_support():
     # a group that fits one block's share is never split
     s = schedule(list(range(15104)), 16128, 32, 8, 128)
     assert s[16] == 64 and s[12] == 0 and s[5] == s[3]
+
+
+def c4_positions():
+    import random
+
+    rnd = random.Random(3)
+    slots = sorted(rnd.sample(range(27648 // 88), 32))
+    return [4096 + 88 * k + i for j, k in enumerate(slots) for i in range(44 if j < 7 else 43)]
+
+
+def test_64_row_schedules_dispatch_longest_groups_first_and_may_take_more_rounds():
+    """64-row groups: blocks are listed longest first (whole groups, chunks in key
+    order) and the share may be two or four rounds of 256 blocks when one round
+    would leave CUs idle (c4: 22 groups in 32 one-round blocks per KV head)."""
+    s = schedule(list(range(1024, 16128)), 16128, 32, 8, 128)  # c5: one chunk per group
+    n_groups, n_work = s[3], s[5]
+    order = [s[18 + 2 * n_groups + 4 * w] for w in range(n_work)]
+    assert order == sorted(range(n_groups), reverse=True)  # later groups attend to more keys
+    assert [s[18 + 2 * g] for g in range(n_groups)] == [n_groups - 1 - g for g in range(n_groups)]
+    s = schedule(c4_positions(), 31744, 32, 8, 128)
+    n_groups, n_work = s[3], s[5]
+    assert s[16] == 64 and n_groups == 22
+    assert 32 < n_work <= 4 * 32  # more than one round of 256 blocks, at most four
+    work = [tuple(s[18 + 2 * n_groups + 4 * w:22 + 2 * n_groups + 4 * w]) for w in range(n_work)]
+    seen = []
+    for g, c, b, e in work:  # each group's chunks contiguous and in key order
+        if not seen or seen[-1] != g:
+            assert g not in seen and c == 0
+            seen.append(g)
+    assert sorted(seen) == list(range(n_groups))
+    longest = [max(e - b for g2, _, b, e in work if g2 == g) for g in seen]
+    assert longest[0] == max(longest)
 
 
 def test_generic_schedules_keep_64_row_groups():
