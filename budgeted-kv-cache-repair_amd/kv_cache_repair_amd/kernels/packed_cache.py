@@ -22,6 +22,9 @@ import copy
 import ctypes
 import types
 import weakref
+from functools import partial
+from itertools import chain, repeat
+from operator import attrgetter, is_not, itemgetter, methodcaller
 from dataclasses import dataclass, field
 from threading import Lock
 from typing import Any, Sequence
@@ -519,13 +522,27 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
     return view
 
 
+_MODULES = itemgetter("_modules")
+_PARAMETERS = itemgetter("_parameters")
+_TRAINING = itemgetter("training")
+_FORWARD_HOOKS = itemgetter("_forward_hooks")
+_FORWARD_PRE_HOOKS = itemgetter("_forward_pre_hooks")
+_HF_HOOK = methodcaller("get", "_hf_hook")
+_DICT_OF = attrgetter("__dict__")
+_NOT_NONE = partial(is_not, None)
+
+
 def _subtree_dicts(root, skip) -> list:
     """The __dict__ of every module under ``root`` (itself included), level by
-    level through the `_modules` dicts, leaving out the subtree of ``skip``."""
+    level through the `_modules` dicts, leaving out the subtree of ``skip``.
+    (Iterated with map/chain: the qualification walks every module per refresh.)"""
     found, level = [], [root.__dict__]
     while level:
         found += level
-        level = [m.__dict__ for attrs in level for m in attrs["_modules"].values() if m is not None and m is not skip]
+        children = filter(_NOT_NONE, chain.from_iterable(map(dict.values, map(_MODULES, level))))
+        if skip is not None:
+            children = filter(partial(is_not, skip), children)
+        level = list(map(_DICT_OF, children))
     return found
 
 
@@ -551,24 +568,25 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     # off the GPUs, and the request device is a GPU when it matters below).
     index = device.index if device.type == "cuda" else -2
     inner, outer = _subtree_dicts(base, None), _subtree_dicts(model, base)
-    training = True in [attrs["training"] for attrs in inner]
-    overridden = True in ["forward" in attrs for attrs in inner]
+    training = any(map(_TRAINING, inner))
+    overridden = True in map(dict.__contains__, inner, repeat("forward"))
     everything = inner + outer
-    hooked = True in [attrs.get("_hf_hook") is not None for attrs in everything]
+    hooked = True in map(is_not, map(_HF_HOOK, everything), repeat(None))
     # Forward hooks on the decoder's modules (or global ones) run only where the
     # modules' own forwards run: the refresh then takes the module path.
     from torch.nn.modules import module as _module
 
-    forward_hooked = (True in [bool(attrs["_forward_hooks"]) or bool(attrs["_forward_pre_hooks"]) for attrs in inner]
+    forward_hooked = (any(map(_FORWARD_HOOKS, inner)) or any(map(_FORWARD_PRE_HOOKS, inner))
                       or bool(_module._global_forward_hooks) or bool(_module._global_forward_pre_hooks))
     # Fingerprint of the tree: every module (its __dict__'s identity) and every
     # parameter slot (the tensor's identity and storage address; an empty slot
     # counts). A tree with the fingerprint that last qualified on this GPU has
     # the same parameter tensors at the same addresses, so their device check
     # holds as it did; the layer plans are reused under the same condition.
-    params = [p for attrs in everything for p in attrs["_parameters"].values()]
-    fingerprint = (tuple(map(id, everything)), tuple(map(id, params)),
-                   tuple([0 if p is None else p.data_ptr() for p in params]))
+    params = list(chain.from_iterable(map(dict.values, map(_PARAMETERS, everything))))
+    # (empty slots hold None, whose identity the second tuple already records)
+    ptrs = tuple(map(torch.Tensor.data_ptr, filter(_NOT_NONE, params)))
+    fingerprint = (tuple(map(id, everything)), tuple(map(id, params)), ptrs)
     with _PLAN_LOCK:
         previous = _QUALIFIED.get(base)
     if previous is not None and previous[1] == index and previous[0] == fingerprint:
