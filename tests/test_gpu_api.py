@@ -287,6 +287,34 @@ def test_partial_budget_repair_matches_the_sequential_recurrence(model, tokenize
         assert new.keys.data_ptr() != old.keys.data_ptr() and new.values.data_ptr() != old.values.data_ptr()
 
 
+def test_partial_budget_on_structured_text_selects_by_semantic_units(model, tokenizer):
+    """A ChatML transcript with a tool element, a JSON value and prose (unknown
+    words map to [UNK]): the default 5% call partitions it into containers,
+    structured pieces and sentences, selects against the float64 allocation and
+    refreshes the selection as the reference recurrence does."""
+    from kv_cache_repair_amd import repair_after_deletion
+    from kv_cache_repair_amd.semantic_units import semantic_char_units
+
+    body = ("<|im_start|>user alpha beta . gamma alpha . <|im_end|> "
+            "<tool_result> alpha : red blue </tool_result> "
+            "config : {\"alpha\": [1, 2]} beta gamma . " + "alpha beta gamma . " * 12)
+    original = "prefix obsolete discard " + body
+    kinds = {u["boundary_kind"] for u in semantic_char_units("prefix " + body)}
+    assert {"tool_container", "json_container", "generic_sentence_or_paragraph"} <= kinds
+    old = prefill(model, tokenizer, original)
+    snap = snapshot(old)
+    span = (len("prefix "), len("prefix obsolete discard "))
+    result = repair_after_deletion(model, tokenizer, old, original, delete_span=span, query="alpha red")
+    sel = result.selection
+    assert sel.metadata["selection"] == "sur" and sel.budget_tokens == -(-sel.suffix_tokens * 5 // 100)
+    assert list(sel.positions) == f64_selection(model, tokenizer, result.edited_text, "alpha red", sel.suffix_start,
+                                                sel.budget_tokens)
+    old_ids = tokenizer(original, add_special_tokens=False, return_tensors="pt")["input_ids"]
+    shifted, _ = ref.build_halo_cache(model, old, old_ids.to(model.device), result.input_ids, 0)
+    assert_caches_close(result.cache, ref.sequential_repair(model, shifted, result.input_ids, list(sel.intervals)))
+    assert_unchanged(old, snap)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_packed_attention_plugin_on_zero_keys_and_arange_values(gpu_device, dtype):
     """K = 0 makes every visible key equally likely, so row r's output is the mean
