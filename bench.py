@@ -945,13 +945,11 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
     packed refresh alone (ownership copy, plan upload, layer-major forward) is
     timed for this build and for the reference path, interleaved in shuffled
     order (benchmark_refresh.py:52-61, 106-126). The reference benchmark's
-    other schedules are timed beside them: this build's sequential and direct
-    executors against the reference's sequential schedule, which they must
-    equal bit for bit (benchmark_refresh.py:150-153; direct with contiguous
-    attention rows)."""
+    sequential schedule is timed beside them: this build's sequential executor
+    against the reference's sequential schedule, which it must equal bit for
+    bit (benchmark_refresh.py:150-153)."""
     from kv_cache_repair_amd.cache import OperatorShim, build_halo_cache, cache_from_tensors
     from kv_cache_repair_amd.execution import sequential_repair
-    from kv_cache_repair_amd.kernels.direct_cache import direct_interval_repair
     from kv_cache_repair_amd.kernels.packed_cache import packed_interval_repair
 
     device = model.device
@@ -972,8 +970,6 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
     calls = {"hip": lambda: packed_interval_repair(shim, shifted, ids, intervals)[0],
              "reference_packed_sdpa": lambda: reference_stage(model, None, None, ids, intervals, shifted=shifted),
              "sequential": lambda: sequential_repair(shim, shifted, ids, intervals)[0],
-             "direct": lambda: direct_interval_repair(shim, shifted, ids, intervals,
-                                                      attention_layout="contiguous")[0],
              "reference_sequential": lambda: reference_sequential(model, shifted, ids, intervals)}
     outputs = {name: fn() for name, fn in calls.items()}
     index = torch.tensor(positions, device=device)
@@ -989,7 +985,7 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
     max_abs = max_abs_rows(outputs["hip"], outputs["reference_packed_sdpa"])
     same_schedule = {name: {"bitwise_equal": bitwise(outputs[name], outputs["reference_sequential"]),
                             "max_abs": max_abs_rows(outputs[name], outputs["reference_sequential"])}
-                     for name in ("sequential", "direct")}
+                     for name in ("sequential",)}
     packed_vs_sequential = max_abs_rows(outputs["hip"], outputs["reference_sequential"])
     del outputs
     lat = interleaved_latency(calls, warmups, repeats, seed)
@@ -999,7 +995,7 @@ def grid_case(model, length: int, count: int, budget: int, warmups: int, repeats
             "value": lat["hip"]["median_ms"], "unit": "ms", "higher_is_better": False,
             "reference_same_gpu_ms": lat["reference_packed_sdpa"]["median_ms"],
             "speedup": lat["reference_packed_sdpa"]["median_ms"] / lat["hip"]["median_ms"],
-            "sequential_ms": lat["sequential"]["median_ms"], "direct_ms": lat["direct"]["median_ms"],
+            "sequential_ms": lat["sequential"]["median_ms"],
             "reference_sequential_ms": lat["reference_sequential"]["median_ms"],
             "same_schedule_vs_reference_sequential": same_schedule,
             "packed_max_abs_vs_reference_sequential": packed_vs_sequential,

@@ -216,63 +216,6 @@ def test_sequential_executor_refuses_unordered_or_outside_intervals(gpu_device, 
         sequential_repair(OperatorShim(model), base, ids, intervals)
 
 
-# ---------------------------------------------------------------------------
-# the direct interval executor (reference kernels/direct_cache.py:147-226)
-# ---------------------------------------------------------------------------
-
-@pytest.mark.parametrize("dtype,attn", PRECISIONS)
-@pytest.mark.parametrize("family", ["llama", "qwen3"])
-def test_direct_executor_equals_the_sequential_schedule(gpu_device, family, dtype, attn):
-    """Same schedule as the sequential executor (the reference benchmark requires
-    them bitwise equal, benchmarks/benchmark_refresh.py:150-153): with contiguous
-    attention rows the result is bit-identical; with strided views it must stay
-    within fp32 round-off of it (bf16: one ulp)."""
-    from kv_cache_repair_amd.cache import OperatorShim
-    from kv_cache_repair_amd.execution import sequential_repair
-    from kv_cache_repair_amd.kernels.direct_cache import direct_interval_repair
-
-    model = _tiny_model(family, dtype, gpu_device)
-    model.set_attn_implementation(attn)
-    gen = torch.Generator(device=gpu_device).manual_seed(11)
-    ids = torch.randint(0, 64, (1, 64), device=gpu_device, generator=gen)
-    with torch.no_grad():
-        base = model.base_model(input_ids=ids, use_cache=True).past_key_values
-    edited = ids.clone()
-    edited[0, 1::2] = torch.randint(0, 64, (32,), device=gpu_device, generator=gen)
-    intervals = [(0, 3), (9, 17), (30, 31), (40, 64)]
-    snap = [(l.keys.clone(), l.values.clone()) for l in base.layers]
-    shim = OperatorShim(model)
-    want, _ = sequential_repair(shim, base, edited, intervals)
-    exact, receipt = direct_interval_repair(shim, base, edited, intervals, attention_layout="contiguous")
-    strided, _ = direct_interval_repair(shim, base, edited, intervals)
-    assert receipt["executor"] == "direct_interval_repair" and receipt["writeback_launch"] == "kvr_copy_kv_interval"
-    assert receipt["recomputed_tokens"] == 3 + 8 + 1 + 24 and receipt["output_cache_ownership"] == "independent"
-    tol = dict(rtol=1e-5, atol=2e-6) if dtype == torch.float32 else dict(rtol=8e-3, atol=8e-3)
-    for e, s, w, (k0, v0), b in zip(exact.layers, strided.layers, want.layers, snap, base.layers):
-        assert same_bits(e.keys, w.keys) and same_bits(e.values, w.values)
-        torch.testing.assert_close(s.keys, w.keys, **tol)
-        torch.testing.assert_close(s.values, w.values, **tol)
-        assert same_bits(b.keys, k0) and same_bits(b.values, v0)
-        assert e.keys.data_ptr() != b.keys.data_ptr()
-
-
-def test_direct_executor_returns_the_base_for_an_empty_support(gpu_device):
-    from kv_cache_repair_amd.cache import OperatorShim
-    from kv_cache_repair_amd.kernels.direct_cache import direct_interval_repair
-
-    model = _tiny_model("llama", torch.float32, gpu_device)
-    ids = torch.zeros((1, 16), dtype=torch.long, device=gpu_device)
-    with torch.no_grad():
-        base = model.base_model(input_ids=ids, use_cache=True).past_key_values
-    out, receipt = direct_interval_repair(OperatorShim(model), base, ids, [])
-    assert out is base and receipt["output_cache_ownership"] == "borrowed_base"
-    with pytest.raises(ValueError, match="maximal"):
-        direct_interval_repair(OperatorShim(model), base, ids, [(0, 2), (2, 4)])
-    model.train()
-    with pytest.raises(ValueError, match="eval-mode"):
-        direct_interval_repair(OperatorShim(model), base, ids, [(0, 2)])
-
-
 @pytest.mark.parametrize("dtype,attn", PRECISIONS)
 @pytest.mark.parametrize("family", ["llama", "qwen3"])
 def test_oneshot_control_equals_the_reference_packed_schedule(gpu_device, family, dtype, attn):

@@ -422,20 +422,3 @@ def test_token_ids_outside_the_vocabulary_are_refused_on_the_host(tokenizer):
     model.set_input_embeddings(small)
     with pytest.raises(ValueError, match="vocabulary"):
         select_support(model, tokenizer, "alpha beta", "", suffix_start=0, budget_percent=0)
-
-
-@pytest.mark.parametrize("kwargs,message", [({"writeback_backend": "cuda"}, "writeback_backend"),
-                                            ({"attention_layout": "packed"}, "attention_layout")])
-def test_direct_executor_rejects_unknown_options_first(kwargs, message):
-    from kv_cache_repair_amd.kernels.direct_cache import direct_interval_repair
-
-    with pytest.raises(ValueError, match=message):
-        direct_interval_repair(None, None, torch.zeros((1, 4), dtype=torch.long), [], **kwargs)
-
-
-@pytest.mark.parametrize("ids", [torch.zeros((2, 4), dtype=torch.long), torch.zeros((1, 4)), [[0, 1]]])
-def test_direct_executor_rejects_malformed_ids_before_the_cache(ids):
-    from kv_cache_repair_amd.kernels.direct_cache import direct_interval_repair
-
-    with pytest.raises(ValueError, match="edited_ids_t"):
-        direct_interval_repair(None, None, ids, [])
