@@ -148,13 +148,14 @@ extern "C" int kvr_decoder_layer(const kvr_layer_desc* L, const kvr_refresh_desc
     const bool norm_partials = rms_norm_partials_ok(h, dt);
 
     // q/k/v projections (+ Qwen3's per-head norms: inside the fresh-row
-    // epilogue, except for fp16, whose epilogue takes its scalar kernel)
+    // epilogue where its vector kernel serves them, else two kvr_rms_norm launches)
     const char* qp;
     const char* kp;
     const char* vp;
     int64_t q_ld, k_ld, v_ld;
     int32_t qkv_splits = 1;
-    const bool norms_in_epilogue = qk_norm && dt != KVR_DTYPE_F16;
+    const bool norms_in_epilogue =
+        qk_norm && rope_norm_fold_ok(dim, dt, L->q_norm, L->k_norm, d->cs_strides, d->cos, d->sin);
     if (!qk_norm || norms_in_epilogue) {
         const void* w[3] = {L->w_q, L->w_k, L->w_v};
         const int32_t rows[3] = {qd, kd, kd};

@@ -277,6 +277,24 @@ __global__ void __launch_bounds__(kThreads) fresh_scalar_kernel(FreshArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Head dims the vector kernel serves: each half row splits into a power-of-two
+// number (at most 64) of 16-byte chunks; *tpr_log2 = log2(chunks).
+bool vec_head_dim(int32_t head_dim, int esize, int* tpr_log2) {
+    const int64_t half_bytes = static_cast<int64_t>(head_dim / 2) * esize;
+    if (half_bytes <= 0 || half_bytes % 16 != 0) return false;
+    const int64_t chunks = half_bytes / 16;
+    int t = 0;
+    while ((int64_t(1) << t) < chunks) ++t;
+    *tpr_log2 = t;
+    return (int64_t(1) << t) == chunks && t <= 6;
+}
+
+// cos/sin tables the vector kernel reads: unit dim stride, 16-byte rows and bases.
+bool vec_tables(const int64_t cs_strides[4], const void* cos, const void* sin, int esize) {
+    return cs_strides[1] == 1 && cs_strides[3] == 1 && (cs_strides[0] * esize) % 16 == 0 &&
+           (cs_strides[2] * esize) % 16 == 0 && aligned16(cos) && aligned16(sin);
+}
+
 template <typename T>
 int launch(const FreshArgs& a, bool vec, int tpr_log2, hipStream_t s) {
     const int64_t rows = (static_cast<int64_t>(a.n_q_heads) + 2 * a.n_kv_heads) * a.n_sel;
@@ -364,24 +382,18 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
     a.norm_eps[1] = eps_k;
 
     // Vector path: each half splits into a power-of-two number of 16-byte chunks.
-    const int64_t half_bytes = static_cast<int64_t>(head_dim / 2) * esize;
-    bool vec = half_bytes % 16 == 0;
     int tpr_log2 = 0;
-    if (vec) {
-        const int64_t chunks = half_bytes / 16;
-        while ((int64_t(1) << tpr_log2) < chunks) ++tpr_log2;
-        vec = (int64_t(1) << tpr_log2) == chunks && tpr_log2 <= 6;
-    }
+    bool vec = vec_head_dim(head_dim, esize, &tpr_log2);
     for (int t = 0; t < 6 && vec; ++t) {
         const int64_t* st = strides + 3 * t;
         vec = st[2] == 1 && (st[0] * esize) % 16 == 0 && (st[1] * esize) % 16 == 0;
     }
-    vec = vec && cs_strides[1] == 1 && cs_strides[3] == 1 && (cs_strides[0] * esize) % 16 == 0 &&
-          (cs_strides[2] * esize) % 16 == 0;
+    vec = vec && vec_tables(cs_strides, cos, sin, esize);
     vec = vec && aligned16(q) && aligned16(q_out) && aligned16(fresh_k) && aligned16(fresh_v) && aligned16(out_k) &&
-          aligned16(out_v) && aligned16(cos) && aligned16(sin);
+          aligned16(out_v);
     // the norms run on the vector path only (their butterfly is over its lane
-    // groups), which fp16 does not take (see launch)
+    // groups), which fp16 does not take (see launch); rope_norm_fold_ok is the
+    // same condition minus the row layouts
     if (norms && (!vec || dtype == KVR_DTYPE_F16 || !aligned16(q_norm) || !aligned16(k_norm)))
         return KVR_E_UNSUPPORTED_SHAPE;
 
@@ -394,6 +406,14 @@ int rope_scatter_impl(const void* q, void* q_out, const void* fresh_k, const voi
 }
 
 }  // namespace
+
+bool rope_norm_fold_ok(int32_t head_dim, int32_t dtype, const void* q_norm, const void* k_norm,
+                       const int64_t cs_strides[4], const void* cos, const void* sin) {
+    const int esize = dtype_size(dtype);
+    int tpr_log2 = 0;
+    return esize != 0 && dtype != KVR_DTYPE_F16 && vec_head_dim(head_dim, esize, &tpr_log2) &&
+           vec_tables(cs_strides, cos, sin, esize) && aligned16(q_norm) && aligned16(k_norm);
+}
 
 int rope_scatter_partials(const PartialSums& src, const int64_t part_col[3], void* q_out, void* out_k, void* out_v,
                           const void* cos, const void* sin, const int64_t* positions, int64_t n_sel,

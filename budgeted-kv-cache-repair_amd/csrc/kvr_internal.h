@@ -157,6 +157,16 @@ int rope_scatter_partials(const PartialSums& src, const int64_t part_col[3], voi
                           const int64_t strides[18], const int64_t cs_strides[4], int32_t dtype, void* stream,
                           const void* q_norm, const void* k_norm, float eps_q, float eps_k);
 
+// Whether Qwen3's per-head q/k norms can be folded into the fresh-row epilogue
+// (kvr_rope_scatter_kv_norm / rope_scatter_partials) for this head dim, dtype,
+// norm weights and rotary tables: the fold runs on the epilogue's vector
+// kernel only (not fp16; each half row a power-of-two count of 16-byte chunks,
+// 16-byte aligned weights and table rows). Given q/k/v rows with unit dim
+// stride and 16-byte aligned rows, the epilogue then accepts the norms;
+// otherwise callers run kvr_rms_norm on the q and k rows first.
+bool rope_norm_fold_ok(int32_t head_dim, int32_t dtype, const void* q_norm, const void* k_norm,
+                       const int64_t cs_strides[4], const void* cos, const void* sin);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

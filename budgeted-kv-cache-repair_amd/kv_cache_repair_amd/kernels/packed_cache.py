@@ -167,11 +167,20 @@ def _silu_activations() -> tuple[type, ...]:
 _SILU_ACTIVATIONS = _silu_activations()
 
 
-def _norms_in_epilogue(dtype) -> bool:
-    """Qwen3's per-head q/k norms run inside the fresh-row epilogue
-    (kvr_rope_scatter_kv_norm) for bf16 / fp32 rows; fp16 rows take the epilogue's
-    scalar kernel, which has no norm, so they keep separate kvr_rms_norm launches."""
-    return dtype in (torch.bfloat16, torch.float32)
+def _norms_in_epilogue(dtype, head_dim: int, q_weight: torch.Tensor, k_weight: torch.Tensor) -> bool:
+    """Whether Qwen3's per-head q/k norms run inside the fresh-row epilogue
+    (kvr_rope_scatter_kv_norm). The fold lives in the epilogue's vector kernel
+    only, so it needs what that kernel needs (kvr_fresh.hip, rope_norm_fold_ok):
+    bf16 / fp32 rows (fp16 rows take the scalar kernel), each half row a
+    power-of-two count (at most 64) of 16-byte chunks, 16-byte aligned norm
+    weights. Otherwise the q and k rows are normalised by two kvr_rms_norm
+    launches first, as kvr_decoder_layer does under the same condition."""
+    if dtype not in (torch.bfloat16, torch.float32):
+        return False
+    half_bytes = (int(head_dim) // 2) * (4 if dtype == torch.float32 else 2)
+    chunks = half_bytes // 16
+    return (half_bytes > 0 and half_bytes % 16 == 0 and chunks & (chunks - 1) == 0 and chunks <= 64
+            and q_weight.data_ptr() % 16 == 0 and k_weight.data_ptr() % 16 == 0)
 
 
 def _checked_head_norm(module, x: torch.Tensor):
@@ -299,8 +308,9 @@ def _layer_plans(layer) -> _LayerPlans | None:
     q, k, v, o, gate, up, down = weights
     plan = _projection.ProjectionPlan
     # q/k/v in one launch, unless per-head norms must run as separate launches
-    # on contiguous q and k (fp16: the epilogue cannot fold them in)
-    separate = len(norms) > 2 and not _norms_in_epilogue(q.dtype)
+    # on contiguous q and k (where the epilogue cannot fold them in)
+    separate = len(norms) > 2 and not _norms_in_epilogue(
+        q.dtype, getattr(layer._modules["self_attn"], "head_dim", 0), norms[2].weight, norms[3].weight)
     plans = _LayerPlans(
         pointers=key, qkv=None if separate else plan([q, k, v]), q=plan([q]) if separate else None,
         k=plan([k]) if separate else None, v=plan([v]) if separate else None, o=plan([o]),
@@ -461,11 +471,12 @@ def _fused_attention_forward(self, hidden_states, position_embeddings=None, atte
     q_norm = getattr(self, "q_norm", None)
     norms = None
     if q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
-        if getattr(self, "_kvr_fused_norms", False) and _norms_in_epilogue(query.dtype):
+        fused_norms = getattr(self, "_kvr_fused_norms", False)
+        if fused_norms and _norms_in_epilogue(query.dtype, self.head_dim, q_norm.weight, self.k_norm.weight):
             norms = (_checked_head_norm(q_norm, query), _checked_head_norm(self.k_norm, key))
-        elif getattr(self, "_kvr_fused_norms", False):
-            query = _rms_norm(q_norm, query)
-            key = _rms_norm(self.k_norm, key)
+        elif fused_norms:  # kvr_rms_norm reads contiguous rows
+            query = _rms_norm(q_norm, query.contiguous())
+            key = _rms_norm(self.k_norm, key.contiguous())
         else:
             query = q_norm(query)
             key = self.k_norm(key)

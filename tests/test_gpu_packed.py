@@ -494,6 +494,43 @@ def test_projection_plans_match_module_linears(gpu_device, family, dtype):
 
 
 
+@pytest.mark.parametrize("head_dim", [96, 8])
+def test_bf16_qwen3_head_dims_outside_the_vector_epilogue(gpu_device, head_dim):
+    """bf16 Qwen3 with a head dim whose half row is not a power-of-two count of
+    16-byte chunks (96: 6 chunks; 8: 8 bytes): the fresh-row epilogue's vector
+    kernel cannot fold the per-head q/k norms in, so both the Python-dispatched
+    shells and kvr_decoder_layer run them as kvr_rms_norm launches before the
+    plain epilogue. The refresh runs by default, native and dispatched layers are
+    bit-identical, and the cache agrees with the module path (hipBLASLt GEMMs,
+    eager norms and RoPE) to the bf16 floor."""
+    from kv_cache_repair_amd.kernels import packed_cache as pc
+
+    model = make_model(gpu_device, "qwen3", kv_heads=2, head_dim=head_dim, dtype=torch.bfloat16, layers=3)
+    shim, ids, base = make_request(model, length=140)
+    edited = ids.clone()
+    edited[0, 70:] = (edited[0, 70:] + 7) % 97
+    intervals = [(0, 2), (5, 9), (63, 70), (100, 117), (139, 140)]
+    snap = snapshot(base)
+    default, receipt = pc.packed_interval_repair(shim, base, edited, intervals)
+    native, _ = pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True)
+    dispatched, _ = pc.packed_interval_repair(shim, base, edited, intervals, native_layers=False)
+    plain, _ = pc.packed_interval_repair(shim, base, edited, intervals, fused_epilogue=False, fused_layers=False,
+                                         fused_projections=False)
+    assert_ownership_and_untouched(default, base, snap, intervals)
+    decoder = shim._base_transformer(model)
+    assert all(pc._layer_plans(layer).qkv is None for layer in decoder.layers)  # q, k, v launched apart
+    n = edited.shape[1]
+    for a, b, c, d in zip(default.layers, native.layers, dispatched.layers, plain.layers):
+        for w, x, y, z in ((a.keys, b.keys, c.keys, d.keys), (a.values, b.values, c.values, d.values)):
+            assert bits_equal(w, x) and bits_equal(x, y)
+            xf, zf = x.float(), z.float()
+            ulp = torch.clamp(zf.abs(), min=2.0 ** -20) * 2.0 ** -7
+            assert ((xf - zf).abs() <= 2 * ulp).float().mean().item() >= 0.99
+            rows_x = xf.permute(0, 2, 1, 3).reshape(n, -1)
+            rows_z = zf.permute(0, 2, 1, 3).reshape(n, -1)
+            assert torch.nn.functional.cosine_similarity(rows_x, rows_z, dim=-1).min().item() >= 0.9999
+
+
 def test_model_changes_between_refreshes_are_seen(gpu_device):
     """The executor caches the model's qualification and layer plans under a
     fingerprint of the module tree (module and parameter identities, storage
