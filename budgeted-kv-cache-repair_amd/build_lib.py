@@ -39,14 +39,27 @@ def hipcc() -> str:
     return str(path) if path.exists() else "hipcc"
 
 
+def _defines() -> list[str]:
+    """-D options from the environment: KVR_ATTN_SCRATCH_MB sizes the static
+    device array of kvr_packed_causal_attention_noalloc (MiB, default 64),
+    which every GPU the library's code object loads on holds."""
+    mb = os.environ.get("KVR_ATTN_SCRATCH_MB")
+    if mb is None:
+        return []
+    if not mb.isdigit() or not 1 <= int(mb) <= 4096:
+        raise ValueError("KVR_ATTN_SCRATCH_MB must be an integer number of MiB in [1, 4096]")
+    return [f"-DKVR_ATTN_SCRATCH_MB={int(mb)}"]
+
+
 def build(verbose: bool = False, jobs: int = 4) -> Path:
     """Compile every HIP source and link the shared library; returns its path."""
     build_dir = PACKAGE_ROOT / "_build"
+    defines = _defines()
     build_dir.mkdir(exist_ok=True)
     objects, procs = [], []
     for name in SOURCES:
         obj = build_dir / (Path(name).stem + ".o")
-        cmd = [hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)]
+        cmd = [hipcc(), *HIP_FLAGS, *defines, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))

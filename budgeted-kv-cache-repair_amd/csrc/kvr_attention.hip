@@ -1947,7 +1947,13 @@ int64_t schedule_span(const std::vector<GroupKeys>& keys, std::vector<Chunk>& ch
 // device address comes from hipGetSymbolAddress, looked up once per device
 // (with that device current) and kept per device.
 // ---------------------------------------------------------------------------
-constexpr int64_t kScratchBytes = int64_t(64) << 20;
+// Size in MiB, set at build time with -DKVR_ATTN_SCRATCH_MB=<n> (default 64:
+// every c1-c5 schedule fits; the largest, c4, needs 49 MB).
+#ifndef KVR_ATTN_SCRATCH_MB
+#define KVR_ATTN_SCRATCH_MB 64
+#endif
+static_assert(KVR_ATTN_SCRATCH_MB >= 1 && KVR_ATTN_SCRATCH_MB <= 4096, "KVR_ATTN_SCRATCH_MB out of range");
+constexpr int64_t kScratchBytes = int64_t(KVR_ATTN_SCRATCH_MB) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -1993,7 +1999,8 @@ extern "C" int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n
     }
     const bool mfma = mfma_eligible(dtype, head_dim);
     if (!mfma && generic_dmax(head_dim) == 0) return KVR_E_UNSUPPORTED_SHAPE;
-    if (chunk_keys < 0 || (chunk_keys > 0 && chunk_keys % kSub != 0)) return KVR_E_INVALID_ARGUMENT;
+    if (chunk_keys < 0) chunk_keys = 0;  // ABI v1: a negative size means "choose from the geometry"
+    if (chunk_keys > 0 && chunk_keys % kSub != 0) return KVR_E_INVALID_ARGUMENT;
     const int group = n_q_heads / n_kv_heads;
     const int qt = pick_qt(group);
     const int n_head_groups = group / qt;

@@ -389,8 +389,8 @@ int kvr_copy_kv_interval(void* out_k, void* out_v, const void* in_k, const void*
  * [0, positions[last row] + 1) into chunks of `chunk_keys` keys. `positions`
  * is the HOST copy of the strictly increasing selected positions (the
  * reference IndexedPlan.positions, indexed_attention.py:56-83).
- * chunk_keys == 0 selects a size from the geometry; a positive value must be
- * a multiple of 64; a negative value is rejected. Writes at most `capacity`
+ * chunk_keys <= 0 selects a size from the geometry; a positive value must be
+ * a multiple of 64. Writes at most `capacity`
  * int32 entries to `schedule` and returns the entry count, or a negative
  * status. With schedule == NULL it returns the required entry count.
  * n_sel == 0 gives a header-only schedule (no work).
@@ -448,8 +448,9 @@ int kvr_packed_causal_attention(const void* q, const void* k, const void* v, voi
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same arguments, kernels and results as
  * kvr_packed_causal_attention, without `workspace`: the split-K partials go to
- * a static device array of kvr_attention_scratch_limit() bytes (64 MiB) that
- * the library holds on every device it runs on until the process ends. A
+ * a static device array of kvr_attention_scratch_limit() bytes (64 MiB unless
+ * the library is built with -DKVR_ATTN_SCRATCH_MB=<n>) that the library holds
+ * on every device where its code object loads, until the process ends. A
  * schedule whose kvr_attention_workspace_bytes exceeds that limit is refused
  * with KVR_E_SCRATCH_LIMIT before anything is launched; use the workspace
  * entry point for it. The call allocates and frees nothing. `stream` must

@@ -379,4 +379,13 @@ def test_empty_selection_gives_a_header_only_schedule():
         assert lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, chunk, buf, need) == need
         assert (buf[2], buf[3], buf[5]) == (0, 0, 0)  # rows, groups, work items
         assert lib.kvr_attention_workspace_bytes(buf, need, 32, 128) == 0
-    assert lib.kvr_attention_schedule(empty, 0, 100, 32, 8, 128, 2, -64, None, 0) == -1  # negative chunk
+    # a negative chunk size means "choose from the geometry", as 0 does
+    positions = [3, 9, 200, 201, 202, 299]
+    pos = _native.i64_array(positions)
+    need = lib.kvr_attention_schedule(pos, len(positions), 300, 32, 8, 128, 2, 0, None, 0)
+    assert lib.kvr_attention_schedule(pos, len(positions), 300, 32, 8, 128, 2, -64, None, 0) == need
+    auto, neg = (ctypes.c_int32 * need)(), (ctypes.c_int32 * need)()
+    assert lib.kvr_attention_schedule(pos, len(positions), 300, 32, 8, 128, 2, 0, auto, need) == need
+    assert lib.kvr_attention_schedule(pos, len(positions), 300, 32, 8, 128, 2, -64, neg, need) == need
+    assert list(auto) == list(neg)
+    assert lib.kvr_attention_schedule(pos, len(positions), 300, 32, 8, 128, 2, 96, None, 0) == -1  # not 64k
