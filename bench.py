@@ -255,12 +255,15 @@ def time_steps(fn, steps, warmup):
 
 # ----------------------------------------------------------------------------- reference stage (same GPU)
 @torch.no_grad()
-def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
+def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None, record=None):
     """The reference's eager path on this GPU: build_halo_cache with the per-layer
     rotate chain and cats (cache.py:103-144), clone_cache, boolean mask and
     index_copy_ + HF sdpa_attention_forward per layer (packed_cache.py:179-298).
     With ``shifted`` (a shifted cache) only the packed refresh runs, as the
-    reference benchmark times it (benchmark_refresh.py:129-164)."""
+    reference benchmark times it (benchmark_refresh.py:129-164). ``record``
+    (a dict) receives the shifted cache (``shifted``) and, per decoder layer,
+    its input hidden rows (``inputs[i]``) and attention output (``attention[i]``,
+    [1, B, Hq, D]), plus the selected rows' rotary tables (``tables``)."""
     from transformers.cache_utils import Cache, DynamicLayer
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
@@ -270,9 +273,12 @@ def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
     base = model.model
     name = "bench_reference_packed_sdpa"
     if name not in ALL_ATTENTION_FUNCTIONS:
-        def attend(module, q, k, v, mask, *, scaling=None, dropout=0.0, bench_mask=None, **kw):
-            return sdpa_attention_forward(module, q, k, v, bench_mask, dropout=0.0, scaling=scaling,
-                                          is_causal=False)
+        def attend(module, q, k, v, mask, *, scaling=None, dropout=0.0, bench_mask=None, bench_record=None, **kw):
+            out, weights = sdpa_attention_forward(module, q, k, v, bench_mask, dropout=0.0, scaling=scaling,
+                                                  is_causal=False)
+            if bench_record is not None:
+                bench_record["attention"][module.layer_idx] = out.detach().clone()
+            return out, weights
         ALL_ATTENTION_FUNCTIONS.register(name, attend)
 
     if shifted is None:
@@ -303,6 +309,8 @@ def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
                           torch.cat((torch.empty_like(nv[:, :, :0]), nv), dim=2)))  # DynamicLayer.update cat
     else:
         pairs = [(layer.keys, layer.values) for layer in shifted.layers]
+    if record is not None:
+        record.update(shifted=cache_from_tensors(pairs), inputs={}, attention={}, tables=None)
     # packed_interval_repair (sdpa + torch writeback)
     selected = [p for s, e in intervals for p in range(s, e)]
     positions = torch.tensor(selected, dtype=torch.long, device=new_ids.device)
@@ -337,12 +345,26 @@ def reference_stage(model, old, old_ids, new_ids, intervals, shifted=None):
         attn._modules = original.self_attn._modules.copy()
         attn.config = config
         layer._modules["self_attn"] = attn
+        if record is not None:
+            layer.forward = _recording_forward(layer.forward, len(layers), record)
         layers.append(layer)
     view._modules["layers"] = torch.nn.ModuleList(layers)
     cache = Cache(layers=[_Layer(l.keys, l.values) for l in output.layers])
+    extra = {"bench_record": record} if record is not None else {}
     view(input_ids=new_ids.index_select(1, positions), position_ids=positions[None], past_key_values=cache,
-         use_cache=True, bench_mask=mask)
+         use_cache=True, bench_mask=mask, **extra)
     return output
+
+
+def _recording_forward(forward, index, record):
+    """A decoder layer's forward that first records its input hidden rows (and,
+    at layer 0, the rotary tables of the selected rows)."""
+    def run(hidden_states, *args, **kwargs):
+        record["inputs"][index] = hidden_states.detach().clone()
+        if index == 0:
+            record["tables"] = tuple(t.detach().clone() for t in kwargs["position_embeddings"])
+        return forward(hidden_states, *args, **kwargs)
+    return run
 
 
 # ----------------------------------------------------------------------------- end-to-end parity at full depth
@@ -424,6 +446,139 @@ def depth_parity(ours, theirs, control, positions) -> dict:
             r["ours_vs_fp32"][m] / max(r["reference_vs_fp32"][m], 1e-30) for r in rows for m in ("max_abs", "rmse")),
         "layers": rows,
     }
+
+
+NORTH_STAR_MAX_ABS = 2e-2
+NORTH_STAR_MIN_COS = 0.9999
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """One unit in the last place of bf16 at |x| (2^(e-7) for |x| in [2^e, 2^(e+1)))."""
+    _, exponent = torch.frexp(x.float().abs().clamp_min(2.0 ** -126))
+    return torch.ldexp(torch.ones_like(x, dtype=torch.float32), exponent - 8)
+
+
+def _north_star(a: torch.Tensor, b: torch.Tensor) -> dict:
+    """max-abs, RMSE, smallest per-row cosine (rows = last-dim vectors) of ``a``
+    against ``b``, the count of elements beyond 2e-2 and whether each of those
+    is within two bf16 ulps of ``b``. A projection rounded once in fp32 by two
+    summation orders can differ by one ulp of the projected value; RoPE adds two
+    rounded products of such values, so a rotated key can differ by two ulps of
+    its own binade (0.031 at |x| in [2, 4), where 2e-2 is 1.3 ulps)."""
+    stats = row_errors(a, b)
+    d = (a.float() - b.float()).abs()
+    beyond = d > NORTH_STAR_MAX_ABS
+    stats["beyond_2e-2"] = int(beyond.sum().item())
+    stats["beyond_2e-2_within_2ulp"] = bool((d[beyond] <= 2 * _bf16_ulp(b)[beyond]).all().item())
+    return stats
+
+
+@torch.no_grad()
+def teacher_forced_parity(model, new_ids, intervals, record, reference_output) -> dict:
+    """Each decoder layer of this build fed the reference path's own layer input.
+
+    ``record`` comes from a reference run (bench.reference_stage or the oracle's
+    reference_refresh_stage with ``record``): its shifted cache, each layer's
+    input hidden rows and attention output, the rotary tables. Layer i of this
+    build runs once on ``inputs[i]`` over a copy of that shifted cache with the
+    executor's own launches (projection plans, fused RMSNorm, fresh-row
+    epilogue, the rounded-probability attention schedule: the Python-dispatched
+    shells, which enqueue the same kernels as the native layer call). Its fresh
+    K/V rows (scattered into the copy), its attention output and its output
+    hidden rows are compared with the reference layer's, so each layer's own
+    error is separated from the bf16 drift that accumulates over the depth.
+    Where the native layer call serves the model (<= 64 rows), kvr_decoder_layer
+    also runs each layer on the same input and must give the same bits.
+    """
+    import dataclasses
+
+    from transformers.cache_utils import Cache
+
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.cache import cache_from_tensors
+    from kv_cache_repair_amd.kernels import packed_cache as pc
+    from kv_cache_repair_amd.kernels.indexed_attention import IndexedPlan
+
+    base = model.model
+    device = new_ids.device
+    n = int(new_ids.shape[1])
+    positions = [p for s, e in intervals for p in range(s, e)]
+    index = torch.tensor(positions, dtype=torch.long, device=device)
+    shifted = record["shifted"]
+    n_layers = len(shifted.layers)
+    key0 = shifted.layers[0].keys
+    plan = IndexedPlan(positions, n).to(device)
+    launcher = pc._launcher(plan, base.config, key0)
+    plans = pc._projection_plans_for(base, None, key0.dtype, len(positions))
+    attended = {}
+
+    def recorder(fn, i):
+        def run(x, *args, **kwargs):
+            attended[i] = x.detach().clone()
+            return fn(x, *args, **kwargs)
+        return run
+
+    shell_plans = None
+    if plans is not None:
+        shell_plans = [dataclasses.replace(p, o=recorder(p.o, i)) for i, p in enumerate(plans)]
+    view = pc._make_native_view(base, True, True, shell_plans)
+    if plans is None:  # the shells call the o_proj modules: wrap them in the shells only
+        for i, layer in enumerate(view.layers):
+            shell = layer._modules["self_attn"]
+            shell._modules["o_proj"] = recorder(shell._modules["o_proj"], i)
+    output = cache_from_tensors([(l.keys.clone(), l.values.clone()) for l in shifted.layers])
+    context = pc._PackedContext(plan.positions, n, "hip", plan, launcher)
+    cache = Cache(layers=[pc._PackedLayer(l.keys, l.values, context, "hip") for l in output.layers])
+    tables = record["tables"]
+    hidden_out = {}
+    for i, layer in enumerate(view.layers):
+        hidden_out[i] = layer(record["inputs"][i].clone(), position_embeddings=tables, past_key_values=cache,
+                              use_cache=True, sur_packed_context=context)
+    native = None
+    if pc._native_layers_for(None, base, plans, True, True):
+        native_cache = cache_from_tensors([(l.keys.clone(), l.values.clone()) for l in shifted.layers])
+        first = base.layers[0]
+        forward = pc._NativeForward(launcher, int(first.mlp.down_proj.weight.shape[0]),
+                                    int(first.mlp.gate_proj.weight.shape[0]), float(first.self_attn.scaling))
+        forward.bind_tables(tables)
+        descs = pc._native_layer_descs(plans, native_cache, n_layers)
+        same = True
+        for i in range(n_layers):
+            desc = descs[i]
+            desc.input_normed, desc.next_norm = 0, None  # a single layer: its own input norm, none for the next
+            h = record["inputs"][i].clone().contiguous()
+            status = _native.lib().kvr_decoder_layer(ctypes.byref(desc), ctypes.byref(forward.desc), h.data_ptr(),
+                                                     forward.stream)
+            _native.check(status, "kvr_decoder_layer")
+            same &= bool(torch.equal(h.view(torch.int16), hidden_out[i].contiguous().view(torch.int16)))
+        for a, b in zip(native_cache.layers, output.layers):
+            same &= bool(torch.equal(a.keys.view(torch.int16), b.keys.view(torch.int16)))
+            same &= bool(torch.equal(a.values.view(torch.int16), b.values.view(torch.int16)))
+        native = same
+        del native_cache, forward
+    rows = []
+    dim = key0.shape[-1]
+    for i in range(n_layers):
+        ours, theirs = output.layers[i], reference_output.layers[i]
+        entry = {"layer": i,
+                 "k": _north_star(ours.keys.index_select(2, index), theirs.keys.index_select(2, index)),
+                 "v": _north_star(ours.values.index_select(2, index), theirs.values.index_select(2, index)),
+                 "attention": _north_star(attended[i].reshape(-1, dim), record["attention"][i].reshape(-1, dim))}
+        for p, t in (("k", ours.keys), ("v", ours.values), ("attention", attended[i])):
+            entry[p]["elements"] = len(positions) * (t.numel() // t.shape[2] if p != "attention" else
+                                                     t.numel() // len(positions))
+        if i + 1 < n_layers:
+            entry["hidden_out_min_cos"] = row_errors(hidden_out[i].reshape(len(positions), -1),
+                                                     record["inputs"][i + 1].reshape(len(positions), -1))["min_cos"]
+        rows.append(entry)
+    parts = ("k", "v", "attention")
+    worst = {p: {"max_abs": max(r[p]["max_abs"] for r in rows), "min_cos": min(r[p]["min_cos"] for r in rows),
+                 "beyond_2e-2": sum(r[p]["beyond_2e-2"] for r in rows),
+                 "beyond_2e-2_within_2ulp": all(r[p]["beyond_2e-2_within_2ulp"] for r in rows),
+                 "elements": sum(r[p]["elements"] for r in rows)} for p in parts}
+    del output, cache, view
+    return {"layers": rows, "worst": worst, "native_layer_call_bit_identical": native,
+            "min_cos_all": min(worst[p]["min_cos"] for p in parts)}
 
 
 def fp32_control(model, old):

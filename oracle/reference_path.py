@@ -165,11 +165,14 @@ def sequential_repair(model, base_cache, ids, intervals):
 # packed executor with SDPA attention and torch index_copy_ writeback
 # ---------------------------------------------------------------------------
 def _sdpa_packed(module, query, key, value, attention_mask, *, scaling=None, dropout=0.0,
-                 oracle_packed_mask=None, **kwargs):
+                 oracle_packed_mask=None, oracle_record=None, **kwargs):
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
-    return sdpa_attention_forward(module, query, key, value, oracle_packed_mask, dropout=0.0, scaling=scaling,
-                                  is_causal=False)
+    out, weights = sdpa_attention_forward(module, query, key, value, oracle_packed_mask, dropout=0.0,
+                                          scaling=scaling, is_causal=False)
+    if oracle_record is not None:  # [1, B, Hq, D], the o_proj input
+        oracle_record["attention"][module.layer_idx] = out.detach().clone()
+    return out, weights
 
 
 def _register():
@@ -197,6 +200,17 @@ class _IndexCopyLayer(DynamicLayer):
         return self.keys.shape[2], 0
 
 
+def _recording_forward(forward, index, record):
+    """A decoder layer's forward that first records its input hidden rows (and,
+    at layer 0, the rotary tables the model computed for the selected rows)."""
+    def run(hidden_states, *args, **kwargs):
+        record["inputs"][index] = hidden_states.detach().clone()
+        if index == 0:
+            record["tables"] = tuple(t.detach().clone() for t in kwargs["position_embeddings"])
+        return forward(hidden_states, *args, **kwargs)
+    return run
+
+
 def _view_with_attention(base, name):
     config = copy.deepcopy(base.config)
     config._attn_implementation = name
@@ -217,8 +231,13 @@ def _view_with_attention(base, name):
 
 
 @torch.no_grad()
-def packed_sdpa_repair(model, base_cache, ids, intervals):
-    """packed_cache.py:225-298 with the default sdpa/torch backends."""
+def packed_sdpa_repair(model, base_cache, ids, intervals, record=None):
+    """packed_cache.py:225-298 with the default sdpa/torch backends.
+
+    ``record`` (a dict) receives, per decoder layer, what teacher-forced
+    per-layer checks need: ``inputs[i]`` the layer's input hidden rows,
+    ``attention[i]`` its attention output (the o_proj input, [1, B, Hq, D]),
+    and ``tables`` the (cos, sin) rotary tables of the selected rows."""
     selected = [p for start, end in intervals for p in range(start, end)]
     if not selected:
         return base_cache
@@ -231,13 +250,23 @@ def packed_sdpa_repair(model, base_cache, ids, intervals):
     output = clone_cache(base_cache)
     cache = Cache(layers=[_IndexCopyLayer(*layer_kv(output, i), positions) for i in range(len(output.layers))])
     view = _view_with_attention(base, _NAME)
+    extra = {}
+    if record is not None:
+        record.update(inputs={}, attention={}, tables=None)
+        for i, layer in enumerate(view.layers):
+            layer.forward = _recording_forward(layer.forward, i, record)
+        extra["oracle_record"] = record
     view(input_ids=ids.index_select(1, positions), position_ids=positions[None], past_key_values=cache,
-         use_cache=True, oracle_packed_mask=mask)
+         use_cache=True, oracle_packed_mask=mask, **extra)
     return output
 
 
 @torch.no_grad()
-def reference_refresh_stage(model, old_cache, old_ids, new_ids, intervals):
-    """Shift cache (rotate) + packed SDPA refresh: the stage the bench times."""
+def reference_refresh_stage(model, old_cache, old_ids, new_ids, intervals, record=None):
+    """Shift cache (rotate) + packed SDPA refresh: the stage the bench times.
+    With ``record``, also ``record["shifted"]``: the shifted cache the refresh
+    started from (see packed_sdpa_repair for the per-layer records)."""
     shifted, _ = build_halo_cache(model, old_cache, old_ids, new_ids, 0)
-    return packed_sdpa_repair(model, shifted, new_ids, intervals)
+    if record is not None:
+        record["shifted"] = shifted
+    return packed_sdpa_repair(model, shifted, new_ids, intervals, record)

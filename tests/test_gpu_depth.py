@@ -11,6 +11,18 @@ against fp32 at most twice the reference path's, with an fp32-epsilon floor;
 its angular error (1 - cosine) per row at most twice the reference's largest;
 and every row the refresh does not select must be bit-identical to the
 reference's (rotated K within 0 ulp, copied V and prefix exact).
+
+The teacher-forced test separates each layer's own error from that drift:
+every layer of this build is fed the reference path's own input for that
+layer (recorded from one reference run) and its fresh K/V rows and attention
+output must meet the north-star gate against the reference layer's: per-row
+cosine >= 0.9999 and max-abs <= 2e-2. An element beyond 2e-2 is accepted only
+within two bf16 ulps of the reference value: the q/k/v projection, rounded
+once from fp32 by this build's GEMM and by hipBLASLt in different summation
+orders, can differ by one ulp of the projected value, and RoPE adds two rounded
+products of such values, so a rotated key can sit two ulps of its own binade
+away (0.031 for |x| in [2, 4), where 2e-2 is 1.3 ulps). The counts of such
+elements are printed (c3: 1 of 2.1M K elements).
 """
 
 from __future__ import annotations
@@ -63,4 +75,35 @@ def test_full_depth_refresh_within_the_reference_precision_floor(gpu_device, nam
         ref_angle = 1.0 - row["reference_vs_fp32"]["min_cos"]
         assert ours_angle <= 2.0 * max(ref_angle, 1e-7), (where, row)
     del ours, theirs, control
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_teacher_forced_layers_meet_the_north_star_gate(gpu_device, name):
+    workload = bench.WORKLOADS[name]
+    print(f"teacher-forced per-layer parity: {workload.description}", flush=True)
+    model = bench.make_model(gpu_device, workload)
+    old, old_ids, new_ids = bench.make_request(gpu_device, workload)
+    intervals = workload.intervals()
+    record = {}  # the reference's shifted cache, per-layer inputs, attention outputs, rotary tables
+    theirs = ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals, record=record)
+    del old
+    result = bench.teacher_forced_parity(model, new_ids, intervals, record, theirs)
+    print(json.dumps({"workload": name, "worst": result["worst"],
+                      "native_layer_call_bit_identical": result["native_layer_call_bit_identical"]}), flush=True)
+    for row in result["layers"]:
+        print(f"  layer {row['layer']:2d}: " + " | ".join(
+            f"{p} max {row[p]['max_abs']:.4f} (>2e-2: {row[p]['beyond_2e-2']}) cos {row[p]['min_cos']:.6f}"
+            for p in ("k", "v", "attention")), flush=True)
+    assert len(result["layers"]) == workload.layers
+    if name == "c3":  # <= 64 rows: the product runs kvr_decoder_layer
+        assert result["native_layer_call_bit_identical"] is True
+    for row in result["layers"]:
+        for part in ("k", "v", "attention"):
+            stats = row[part]
+            where = f"{name} layer {row['layer']} {part}"
+            assert stats["min_cos"] >= bench.NORTH_STAR_MIN_COS, (where, stats)
+            assert stats["max_abs"] <= bench.NORTH_STAR_MAX_ABS or stats["beyond_2e-2_within_2ulp"], (where, stats)
+        assert row.get("hidden_out_min_cos", 1.0) >= bench.NORTH_STAR_MIN_COS, row
+    del record, theirs, model
     torch.cuda.empty_cache()
