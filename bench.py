@@ -19,15 +19,19 @@ copies, as repair_after_deletion does (its tokenizer output is on the host), so
 the step issues no device-to-host copy; the reference path keeps its own
 device-id read (cache.py:116-117).
 
-Printed (one JSON line): stage latency (ms per repair over K steps), the same
-stage run the reference way on the same GPU, the device time of every
+Printed (one JSON line): stage latency in ms per repair (value = the median of
+the K steps' per-call samples, each call bracketed by torch.cuda.synchronize()
+as the reference benchmark times it, benchmark_refresh.py:106-126; with p95 and
+the back-to-back figure beside it), the same stage run the reference way on the
+same GPU, the device time of every
 libkvrepair kernel of the step (HIP events around replays of a graph of
 back-to-back launches of that kernel with the stage's own shapes: no host time
 inside), a roofline object for the dominant kernel and one per north-star
 kernel (rotate, shift-cache build, scatter, fresh-row epilogue, attention),
 the end-to-end parity checks at full depth against the reference path and an
-fp32 control, the selection scorer, and the reference path timed on the host
-CPU (cpu_baseline).
+fp32 control plus the teacher-forced per-layer north-star check, the selection
+scorer, and the reference stage timed on the host CPU over all layers
+(cpu_baseline).
 
 Other modes (secondary lines, not the headline):
   --workload c2|c4|c5   the same measurements on BASELINE configs 2, 4, 5 at
@@ -235,6 +239,30 @@ def no_gc():
     finally:
         if enabled:
             gc.enable()
+
+
+def time_calls(fn, steps, warmup) -> dict:
+    """The reference benchmark's timing (benchmark_refresh.py:106-126): ``warmup``
+    untimed calls, then ``steps`` calls each bracketed by torch.cuda.synchronize()
+    on both sides, so every sample is one whole repair from host entry to device
+    completion. Returns the median, p95, mean and raw samples (ms)."""
+    for _ in range(warmup):
+        out = fn()
+        torch.cuda.synchronize()
+        del out
+    samples = []
+    with no_gc():
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize()
+            samples.append((time.perf_counter() - t0) * 1000.0)
+            del out
+    ordered = sorted(samples)
+    return {"median_ms": statistics.median(samples), "p95_ms": ordered[min(len(ordered) - 1,
+                                                                             math.ceil(0.95 * len(ordered)) - 1)],
+            "mean_ms": statistics.fmean(samples), "min_ms": ordered[0], "samples_ms": samples}
 
 
 def time_steps(fn, steps, warmup):
@@ -593,7 +621,10 @@ def fp32_control(model, old):
 def parity_checks(model, shim, old, old_ids, new_ids, intervals, with_control=True) -> dict:
     positions = [p for s, e in intervals for p in range(s, e)]
     ours = hip_stage(shim, old, old_ids, new_ids, intervals)
-    theirs = reference_stage(model, old, old_ids, new_ids, intervals)
+    record = {}
+    theirs = reference_stage(model, old, old_ids, new_ids, intervals, record=record)
+    forced = teacher_forced_parity(model, new_ids, intervals, record, theirs)
+    del record
     if with_control:
         control_model, control_old = fp32_control(model, old)
         control = reference_stage(control_model, control_old, old_ids, new_ids, intervals)
@@ -607,6 +638,16 @@ def parity_checks(model, shim, old, old_ids, new_ids, intervals, with_control=Tr
                          "ours_vs_fp32_max_abs": r["ours_vs_fp32"]["max_abs"],
                          "reference_vs_fp32_max_abs": r["reference_vs_fp32"]["max_abs"]}
                         for r in result["layers"]] if with_control else []
+    gate = all(r[p]["min_cos"] >= NORTH_STAR_MIN_COS and (r[p]["max_abs"] <= NORTH_STAR_MAX_ABS
+                                                           or r[p]["beyond_2e-2_within_2ulp"])
+               for r in forced["layers"] for p in ("k", "v", "attention"))
+    result["teacher_forced_per_layer"] = {
+        "method": "every layer fed the reference path's own input for it; its fresh K/V rows and attention output "
+                  "against the reference layer's",
+        "north_star_gate": gate, "worst": forced["worst"],
+        "native_layer_call_bit_identical": forced["native_layer_call_bit_identical"],
+        "per_layer_max_abs": [{p: round(r[p]["max_abs"], 6) for p in ("k", "v", "attention")}
+                              for r in forced["layers"]]}
     del ours, theirs, control
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -773,6 +814,26 @@ def kernel_launchers(model, workload: Workload, old, old_ids, new_ids, device):
         launch_all.keep = keep  # the bound tensors live as long as the launcher
         # one "launch" = the four projections of a layer; bytes/flops averaged per kvr_linear_multi call
         out["kvr_linear_multi"] = (launch_all, total_bytes, 0, 4 * w.layers, 4)
+    else:
+        # more rows than one kvr_linear_multi launch serves: the stage runs the modules' own
+        # projections (torch -> hipBLASLt): one layer's seven GEMMs at the workload's row count
+        layer = model.model.layers[0]
+        a, m = layer.self_attn, layer.mlp
+        x = torch.randn(b, w.hidden, device=device, generator=gen, dtype=torch.bfloat16)
+        xi = torch.randn(b, w.mlp, device=device, generator=gen, dtype=torch.bfloat16)
+        xo = torch.randn(b, w.hq * w.dim, device=device, generator=gen, dtype=torch.bfloat16)
+        gemms = [(mod.weight, xin) for mod, xin in ((a.q_proj, x), (a.k_proj, x), (a.v_proj, x), (a.o_proj, xo),
+                                                    (m.gate_proj, x), (m.up_proj, x), (m.down_proj, xi))]
+        outs = [torch.empty(b, wt.shape[0], device=device, dtype=torch.bfloat16) for wt, _ in gemms]
+
+        def launch_gemms():
+            for (wt, xin), y in zip(gemms, outs):
+                torch.matmul(xin, wt.t(), out=y)
+        launch_gemms.keep = (gemms, outs)
+        params = sum(wt.numel() for wt, _ in gemms)
+        nbytes = esz * (params + sum(xin.numel() + y.numel() for (_, xin), y in zip(gemms, outs)))
+        # one "launch" = the seven GEMMs of a layer; per GEMM on average
+        out["hipblaslt_projections"] = (launch_gemms, nbytes, 2 * b * params, 7 * w.layers, 7)
     launch_keep = (shifted, plan, qkv, q_out, cos, sin, ws, attn_out, host, dev)
     return out, launch_keep
 
@@ -788,8 +849,8 @@ def measure_kernels(model, workload, old, old_ids, new_ids, device) -> dict:
                "frac_of_hbm_peak": nbytes / calls / (us * 1e3) / HBM_PEAK_GBPS, "launches_per_step": per_step,
                "total_us_per_step": us * per_step}
         if flops:
-            rec["achieved_TFLOPs"] = flops / (us * 1e6)
-            rec["frac_of_bf16_mfma_peak"] = flops / (us * 1e6) / MFMA_BF16_PEAK_TFLOPS
+            rec["achieved_TFLOPs"] = flops / calls / (us * 1e6)
+            rec["frac_of_bf16_mfma_peak"] = flops / calls / (us * 1e6) / MFMA_BF16_PEAK_TFLOPS
         kernels[name] = rec
     del keep
     torch.cuda.synchronize()
@@ -842,12 +903,15 @@ def rooflines(kernels: dict, workload: str) -> tuple[dict, dict]:
     stepping = {n: k for n, k in kernels.items() if k["launches_per_step"]}
     dominant = max(stepping, key=lambda n: stepping[n]["total_us_per_step"])
     attention_bound = "mfma" if workload in ("c4", "c5") else "hbm"
+    # the bound of the dominant kernel: attention as above; hipBLASLt's projections of
+    # more than 64 rows are MFMA-bound (2*rows flops per weight element read once)
+    bound = {"kvr_packed_causal_attention": attention_bound, "hipblaslt_projections": "mfma"}.get(dominant, "hbm")
     north = {"rotate": entry("kvr_rope_delta_rotate"), "shift_cache_build": entry("kvr_shift_cache_build"),
              "scatter": entry("kvr_indexed_scatter_kv"), "fresh_row_epilogue": entry("kvr_rope_scatter_kv"),
              "attention": entry("kvr_packed_causal_attention", attention_bound)}
     north["attention"]["achieved_TFLOPs"] = kernels["kvr_packed_causal_attention"]["achieved_TFLOPs"]
     north["attention"]["achieved_GBps"] = kernels["kvr_packed_causal_attention"]["achieved_GBps"]
-    return entry(dominant), north
+    return entry(dominant, bound), north
 
 
 # ----------------------------------------------------------------------------- selection scoring
@@ -919,19 +983,57 @@ def _cpu_name() -> str:
     return "unknown"
 
 
-def cpu_baseline(workload: Workload, layers_sample: int, repeats: int = 10) -> dict:
+def host_copy(model, workload: Workload, layers: int):
+    """The first ``layers`` decoder layers of ``model`` (with its embedding, norm
+    and head) as a CPU model holding the same weights bit for bit."""
+    from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM
+
+    cfg = copy.deepcopy(model.config)
+    cfg.num_hidden_layers = layers
+    if workload.family == "qwen3":
+        cfg.layer_types = ["full_attention"] * layers
+    ctor = Qwen3ForCausalLM if workload.family == "qwen3" else LlamaForCausalLM
+    assert isinstance(cfg, (LlamaConfig, Qwen3Config))
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(next(model.parameters()).dtype)
+    try:
+        with torch.device("meta"):
+            host = ctor(cfg)
+    finally:
+        torch.set_default_dtype(previous)
+    host = host.to_empty(device="cpu").eval()
+    source = dict(model.named_parameters())
+    with torch.no_grad():
+        for name, param in host.named_parameters():
+            param.copy_(source[name])
+        rotary = host.model.rotary_emb
+        rotary.inv_freq = model.model.rotary_emb.inv_freq.detach().cpu()
+        rotary.original_inv_freq = rotary.inv_freq.clone()
+        rotary.attention_scaling = model.model.rotary_emb.attention_scaling
+    host.set_attn_implementation("sdpa")
+    return host
+
+
+def cpu_baseline(workload: Workload, model, old, old_ids, new_ids, layers_sample: int = 0,
+                 repeats: int = 5) -> dict:
     """The oracle's torch restatement of the reference stage (rotate chain +
-    packed SDPA forward), timed on every host core over the first
-    ``layers_sample`` layers of the workload (median of ``repeats`` runs after
-    one warm-up) and scaled to all layers."""
+    packed SDPA forward) on every host core, over a host copy of the GPU run's
+    own model and stale cache: all layers by default (``layers_sample`` > 0 times
+    only the first layers and scales), median of ``repeats`` runs after one
+    warm-up."""
+    from kv_cache_repair_amd.cache import cache_from_tensors
     from oracle import reference_path as ref
 
+    layers_sample = workload.layers if layers_sample <= 0 else min(layers_sample, workload.layers)
     threads = max(1, os.cpu_count() or 1)
     previous = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        model = make_model("cpu", workload, layers=layers_sample)
-        old, old_ids, new_ids = make_request("cpu", workload, layers=layers_sample)
+        t_copy = time.perf_counter()
+        model = host_copy(model, workload, layers_sample)
+        old = cache_from_tensors([(l.keys.cpu(), l.values.cpu()) for l in old.layers[:layers_sample]])
+        old_ids, new_ids = old_ids.cpu(), new_ids.cpu()
+        copy_s = time.perf_counter() - t_copy
         intervals = workload.intervals()
         ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)  # warm-up (allocator, kernels)
         samples = []
@@ -940,15 +1042,18 @@ def cpu_baseline(workload: Workload, layers_sample: int, repeats: int = 10) -> d
             ref.reference_refresh_stage(model, old, old_ids, new_ids, intervals)
             samples.append((time.perf_counter() - t0) * 1000.0)
         per_sample_ms = statistics.median(samples)
+        del model, old
     finally:
         torch.set_num_threads(previous)
     scale = workload.layers / layers_sample
+    scope = (f"all {workload.layers} layers" if scale == 1 else
+             f"the first {layers_sample} of {workload.layers} layers, scaled x{scale:g}")
     return {"value": per_sample_ms * scale, "unit": "ms", "cores": threads, "kind": "port",
             "sample": f"oracle torch restatement of the reference stage (eager rotate chain, clone, boolean mask, "
-                      f"index_copy_, HF sdpa) on the first {layers_sample} of {workload.layers} layers of the "
-                      f"{workload.name} workload, bf16, median of {repeats} runs after one warm-up, scaled "
-                      f"x{scale:g} to {workload.layers} layers; torch threads = os.cpu_count()",
-            "cpu": _cpu_name(), "os_cpu_count": os.cpu_count()}
+                      f"index_copy_, HF sdpa) over {scope} of the {workload.name} workload on a host copy of the "
+                      f"GPU run's model and stale cache, bf16, median of {repeats} runs after one warm-up; torch "
+                      f"threads = os.cpu_count()",
+            "samples_ms": samples, "host_copy_s": copy_s, "cpu": _cpu_name(), "os_cpu_count": os.cpu_count()}
 
 
 def cpu_kernel_baseline(workload: Workload, repeats: int = 2) -> dict:
@@ -1201,7 +1306,9 @@ def run_workload(args, workload: Workload, device) -> dict:
 
     host_ids = (old_ids.cpu(), new_ids.cpu())
     step = lambda: hip_stage(shim, old, old_ids, new_ids, intervals, host_ids=host_ids)  # noqa: E731
-    ms = time_steps(step, args.steps, args.warmup)
+    per_call = time_calls(step, args.steps, args.warmup)
+    ms = per_call["median_ms"]
+    back_to_back = time_steps(step, args.steps, 0)
     kernels = measure_kernels(model, workload, old, old_ids, new_ids, device)
     roofline, north = rooflines(kernels, workload.name)
 
@@ -1209,8 +1316,10 @@ def run_workload(args, workload: Workload, device) -> dict:
     interleaved = None
     if not args.no_reference:
         ref_step = lambda: reference_stage(model, old, old_ids, new_ids, intervals)  # noqa: E731
-        ref_ms = time_steps(ref_step, args.steps, max(1, args.warmup))
-        reference = {"ms_per_step": ref_ms, "speedup": ref_ms / ms,
+        ref_calls = time_calls(ref_step, args.steps, max(1, args.warmup))
+        ref_ms = ref_calls["median_ms"]
+        reference = {"ms_per_step": ref_ms, "p95_ms": ref_calls["p95_ms"], "speedup": ref_ms / ms,
+                     "back_to_back_ms_per_step": time_steps(ref_step, args.steps, 0),
                      "what": "reference eager path on the same GPU: per-layer rotate chain + cats, clone_cache, "
                              "bool mask, index_copy_, HF sdpa_attention_forward with repeat_kv",
                      "sdpa": sdpa_backend_used(ref_step)}
@@ -1223,18 +1332,23 @@ def run_workload(args, workload: Workload, device) -> dict:
                            "method": "each call bracketed by torch.cuda.synchronize(), both paths once per round in "
                                      "a shuffled order"}
     scoring = scoring_measurement(model, new_ids, device) if headline else None
-    del old
     if args.no_cpu_baseline:
         cpu = None
     elif headline:
-        cpu = cpu_baseline(workload, args.cpu_layers)
+        cpu = cpu_baseline(workload, model, old, old_ids, new_ids, args.cpu_layers)
     else:
         cpu = cpu_kernel_baseline(workload)
+    del old
     suffix = workload.suffix
     rotate = kernels["kvr_rope_delta_rotate"]
     line = {
         "metric": METRIC if headline else f"refresh-stage latency (ms) per repair, {workload.name}",
         "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "p95_ms": per_call["p95_ms"], "back_to_back_ms_per_step": back_to_back,
+        "timing": "value = ms_per_step = median of the steps' per-call samples, each call bracketed by "
+                  "torch.cuda.synchronize() (benchmark_refresh.py:106-126); back_to_back_ms_per_step = the same "
+                  "steps run back to back between two synchronisations",
+        "per_call_samples_ms": per_call["samples_ms"],
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (random-init model of the workload's shape, K/V ~ N(0,1), random ids)",
         "config": {"workload": workload.description, "layers": workload.layers, "kv_heads": workload.hkv,
@@ -1270,7 +1384,8 @@ def main(argv=None) -> int:
                         help="rounds of per-call timing, this build and the reference stage in shuffled order "
                              "(0 skips); reported beside the bracketed value, which it does not change")
     parser.add_argument("--interleaved-warmups", type=int, default=10)
-    parser.add_argument("--cpu-layers", type=int, default=4, help="layers in the bounded CPU-baseline sample")
+    parser.add_argument("--cpu-layers", type=int, default=0,
+                        help="layers in the CPU-baseline sample (0: all layers of the workload)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-reference", action="store_true", help="skip the same-GPU reference stage and checks")
     parser.add_argument("--no-fp32-control", action="store_true", help="parity checks without the fp32 control")
