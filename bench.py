@@ -486,18 +486,29 @@ def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
     return torch.ldexp(torch.ones_like(x, dtype=torch.float32), exponent - 8)
 
 
-def _north_star(a: torch.Tensor, b: torch.Tensor) -> dict:
+def _north_star(a: torch.Tensor, b: torch.Tensor, rotated: bool = False) -> dict:
     """max-abs, RMSE, smallest per-row cosine (rows = last-dim vectors) of ``a``
     against ``b``, the count of elements beyond 2e-2 and whether each of those
-    is within two bf16 ulps of ``b``. A projection rounded once in fp32 by two
-    summation orders can differ by one ulp of the projected value; RoPE adds two
-    rounded products of such values, so a rotated key can differ by two ulps of
-    its own binade (0.031 at |x| in [2, 4), where 2e-2 is 1.3 ulps)."""
+    is within two bf16 ulps of its scale: |b| itself, or for ``rotated`` rows
+    (RoPE'd keys) the norm r of the element's rotate-half pair in ``b``.
+
+    Why: a projection rounded once from fp32 by two summation orders can differ
+    by one ulp of the projected value, and the normalised input it reads by one
+    or two more; RoPE then adds two rounded products k cos and k2 sin, each at
+    most r in magnitude (rotation keeps the pair norm), so a rotated key can sit
+    two ulps of r away even where it is itself small (cancellation). At r in
+    [2, 4) two ulps are 0.031, where 2e-2 is 1.3 ulps."""
     stats = row_errors(a, b)
-    d = (a.float() - b.float()).abs()
+    bf = b.float()
+    d = (a.float() - bf).abs()
     beyond = d > NORTH_STAR_MAX_ABS
+    scale = bf.abs()
+    if rotated:
+        half = bf.shape[-1] // 2
+        r = torch.sqrt(bf[..., :half].square() + bf[..., half:].square())
+        scale = torch.cat((r, r), dim=-1)
     stats["beyond_2e-2"] = int(beyond.sum().item())
-    stats["beyond_2e-2_within_2ulp"] = bool((d[beyond] <= 2 * _bf16_ulp(b)[beyond]).all().item())
+    stats["beyond_2e-2_within_2ulp"] = bool((d[beyond] <= 2 * _bf16_ulp(scale)[beyond]).all().item())
     return stats
 
 
@@ -589,7 +600,7 @@ def teacher_forced_parity(model, new_ids, intervals, record, reference_output) -
     for i in range(n_layers):
         ours, theirs = output.layers[i], reference_output.layers[i]
         entry = {"layer": i,
-                 "k": _north_star(ours.keys.index_select(2, index), theirs.keys.index_select(2, index)),
+                 "k": _north_star(ours.keys.index_select(2, index), theirs.keys.index_select(2, index), True),
                  "v": _north_star(ours.values.index_select(2, index), theirs.values.index_select(2, index)),
                  "attention": _north_star(attended[i].reshape(-1, dim), record["attention"][i].reshape(-1, dim))}
         for p, t in (("k", ours.keys), ("v", ours.values), ("attention", attended[i])):
