@@ -124,20 +124,36 @@ __device__ inline void norm_row(u32x4& lo, u32x4& hi, const u32x4& w_lo, const u
 
 // Vector path: unit dim strides, 16-byte aligned rows. TPR threads share a
 // row; thread c owns the 16-byte chunk c of the first half and chunk c of the
-// second half (its rotate_half partner).
-template <typename T>
+// second half (its rotate_half partner). PARTIALS: q/k/v come from split-K
+// partial sums; NORM: per-head RMSNorm weights are given. Each combination is
+// its own instantiation, so the plain path keeps its register count (and
+// occupancy) free of the partial sums' and the norm's live values. Outputs are
+// written with nontemporal stores (streamed, not kept in L2: -20% at c5).
+template <typename T, bool PARTIALS, bool NORM>
 __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tpr_log2) {
     using E = elem<T>;
     using bits = typename E::bits;
     constexpr int EPV = 16 / E::size;
     const int tpr = 1 << tpr_log2;
-    const int64_t g = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> tpr_log2;
+    // the launch keeps rows * TPR below 2^31, so the row decode runs in 32 bits
+    const uint32_t g = (blockIdx.x * kThreads + threadIdx.x) >> tpr_log2;
     const int c = threadIdx.x & (tpr - 1);
-    const int64_t rows = (static_cast<int64_t>(a.n_q_heads) + 2 * a.n_kv_heads) * a.n_sel;
-    if (g >= rows) return;
+    const uint32_t nq = static_cast<uint32_t>(a.n_q_heads) * static_cast<uint32_t>(a.n_sel);
+    const uint32_t nkv = static_cast<uint32_t>(a.n_kv_heads) * static_cast<uint32_t>(a.n_sel);
+    if (g >= nq + 2 * nkv) return;
     int part;
     int64_t h, r;
-    decode_row(a, g, part, h, r);
+    if (g < nq) {
+        part = 0;
+        r = g / static_cast<uint32_t>(a.n_q_heads);
+        h = g - static_cast<uint32_t>(r) * static_cast<uint32_t>(a.n_q_heads);
+    } else {
+        const uint32_t k = g - nq;
+        part = k < nkv ? 1 : 2;
+        const uint32_t kk = part == 2 ? k - nkv : k;
+        r = kk / static_cast<uint32_t>(a.n_kv_heads);
+        h = kk - static_cast<uint32_t>(r) * static_cast<uint32_t>(a.n_kv_heads);
+    }
     const int half = a.head_dim >> 1;
     const int64_t lo_off = static_cast<int64_t>(c) * EPV;
     const int64_t hi_off = lo_off + half;
@@ -146,12 +162,10 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
     // fp32 partials, the cos/sin chunks) so the thread waits once; the
     // position is checked only before the store.
     const int64_t pos = part == 0 ? 0 : a.positions[r];
-    const char* src = nullptr;
-    if (!a.src.base)
-        src = part == 0 ? a.q + (h * a.qs[0] + r * a.qs[1]) * E::size
-                        : a.fresh[part - 1] + (h * a.fs[part - 1][0] + r * a.fs[part - 1][1]) * E::size;
     u32x4 lo, hi, c_lo, c_hi, s_lo, s_hi;
-    if (src) {
+    if constexpr (!PARTIALS) {
+        const char* src = part == 0 ? a.q + (h * a.qs[0] + r * a.qs[1]) * E::size
+                                    : a.fresh[part - 1] + (h * a.fs[part - 1][0] + r * a.fs[part - 1][1]) * E::size;
         lo = *reinterpret_cast<const u32x4*>(src + lo_off * E::size);
         hi = *reinterpret_cast<const u32x4*>(src + hi_off * E::size);
     }
@@ -163,8 +177,8 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
         s_lo = *reinterpret_cast<const u32x4*>(srow + lo_off * E::size);
         s_hi = *reinterpret_cast<const u32x4*>(srow + hi_off * E::size);
     }
-    if constexpr (EPV == 8) {
-        if (a.src.base) {  // the projection's output, rounded as its reduce kernel rounds it
+    if constexpr (PARTIALS && EPV == 8) {
+        {  // the projection's output, rounded as its reduce kernel rounds it
             const int64_t col = a.part_col[part] + h * a.head_dim;
             float sl8[8], sh8[8];
             partial_sum8(a.src, r, col + lo_off, sl8);
@@ -180,7 +194,7 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
     }
     // per-head RMSNorm of a q or k row (uniform over the row's TPR lanes, so
     // the butterfly below runs on whole lane groups)
-    if (part < 2 && a.norm_w[part]) {
+    if (NORM && part < 2) {
         const char* wrow = a.norm_w[part];
         const u32x4 w_lo = *reinterpret_cast<const u32x4*>(wrow + lo_off * E::size);
         const u32x4 w_hi = *reinterpret_cast<const u32x4*>(wrow + hi_off * E::size);
@@ -195,8 +209,8 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
         dst = a.out[kv] + (h * a.os[kv][0] + pos * a.os[kv][1]) * E::size;
     }
     if (part == 2) {  // values: bit copy
-        *reinterpret_cast<u32x4*>(dst + lo_off * E::size) = lo;
-        *reinterpret_cast<u32x4*>(dst + hi_off * E::size) = hi;
+        __builtin_nontemporal_store(lo, reinterpret_cast<u32x4*>(dst + lo_off * E::size));
+        __builtin_nontemporal_store(hi, reinterpret_cast<u32x4*>(dst + hi_off * E::size));
         return;
     }
     bits xl[EPV], xh[EPV], cl[EPV], ch[EPV], sl[EPV], sh[EPV], ol[EPV], oh[EPV];
@@ -217,8 +231,8 @@ __global__ void __launch_bounds__(kThreads) fresh_vec_kernel(FreshArgs a, int tp
     u32x4 out_lo, out_hi;
     __builtin_memcpy(&out_lo, ol, 16);
     __builtin_memcpy(&out_hi, oh, 16);
-    *reinterpret_cast<u32x4*>(dst + lo_off * E::size) = out_lo;
-    *reinterpret_cast<u32x4*>(dst + hi_off * E::size) = out_hi;
+    __builtin_nontemporal_store(out_lo, reinterpret_cast<u32x4*>(dst + lo_off * E::size));
+    __builtin_nontemporal_store(out_hi, reinterpret_cast<u32x4*>(dst + hi_off * E::size));
 }
 
 // Scalar path: one thread per (row, pair index i < head_dim/2), any strides.
@@ -301,9 +315,17 @@ int launch(const FreshArgs& a, bool vec, int tpr_log2, hipStream_t s) {
     // fp16 rows always take the scalar kernel: the vector kernel's fp16
     // instantiation does not compile with packed fp32 instructions disabled.
     if constexpr (!std::is_same<T, f16_t>::value) {
-        if (vec) {
-            const int64_t threads = rows << tpr_log2;
-            fresh_vec_kernel<T><<<static_cast<unsigned>(ceil_div(threads, kThreads)), kThreads, 0, s>>>(a, tpr_log2);
+        if (vec && (rows << tpr_log2) < (int64_t(1) << 31)) {
+            const unsigned blocks = static_cast<unsigned>(ceil_div(rows << tpr_log2, kThreads));
+            const bool partials = a.src.base != nullptr, norm = a.norm_w[0] != nullptr;
+            if (partials && norm)
+                fresh_vec_kernel<T, true, true><<<blocks, kThreads, 0, s>>>(a, tpr_log2);
+            else if (partials)
+                fresh_vec_kernel<T, true, false><<<blocks, kThreads, 0, s>>>(a, tpr_log2);
+            else if (norm)
+                fresh_vec_kernel<T, false, true><<<blocks, kThreads, 0, s>>>(a, tpr_log2);
+            else
+                fresh_vec_kernel<T, false, false><<<blocks, kThreads, 0, s>>>(a, tpr_log2);
             return launch_status();
         }
     }

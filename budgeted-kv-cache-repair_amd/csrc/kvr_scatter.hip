@@ -25,24 +25,27 @@ struct ScatterArgs {
 };
 
 // Vector path: one thread moves one 16-byte chunk. Flat index order is
-// (kv, head, row, chunk) so neighbouring lanes touch neighbouring bytes.
+// (kv, head, row, chunk) so neighbouring lanes touch neighbouring bytes. The
+// launch keeps the thread count below 2^31, so the index decode runs in 32
+// bits; the cache rows are written with nontemporal stores (streamed).
 __global__ void __launch_bounds__(kThreads) scatter_vec_kernel(ScatterArgs a, int esize, int chunks_log2) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const int64_t chunks = int64_t(1) << chunks_log2;
-    const int64_t per_kv = static_cast<int64_t>(a.n_heads) * a.n_sel * chunks;
+    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t n_sel = static_cast<uint32_t>(a.n_sel);
+    const uint32_t per_kv = (static_cast<uint32_t>(a.n_heads) * n_sel) << chunks_log2;
     if (idx >= 2 * per_kv) return;
     const int kv = idx >= per_kv ? 1 : 0;
-    const int64_t rem = idx - kv * per_kv;
-    const int64_t c = rem & (chunks - 1);
-    const int64_t hr = rem >> chunks_log2;
-    const int64_t r = hr % a.n_sel;
-    const int64_t h = hr / a.n_sel;
+    const uint32_t rem = idx - (kv ? per_kv : 0);
+    const int64_t c = rem & ((1u << chunks_log2) - 1);
+    const uint32_t hr = rem >> chunks_log2;
+    const uint32_t h32 = hr / n_sel;
+    const int64_t r = hr - h32 * n_sel;
+    const int64_t h = h32;
     const int64_t pos = a.positions[r];
     if (pos < 0 || pos >= a.n_keys) return;
     const int64_t src_off = (h * a.fresh_stride[kv][0] + r * a.fresh_stride[kv][1]) * esize + c * 16;
     const int64_t dst_off = (h * a.out_stride[kv][0] + pos * a.out_stride[kv][1]) * esize + c * 16;
     const u32x4 v = *reinterpret_cast<const u32x4*>(a.fresh[kv] + src_off);
-    *reinterpret_cast<u32x4*>(a.out[kv] + dst_off) = v;
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(a.out[kv] + dst_off));
 }
 
 // Scalar path: one thread per element, arbitrary positive strides.
@@ -116,6 +119,7 @@ extern "C" int kvr_indexed_scatter_kv(void* out_k, void* out_v, const void* fres
     vec = vec && aligned16(out_k) && aligned16(out_v) && aligned16(fresh_k) && aligned16(fresh_v);
 
     hipStream_t s = as_stream(stream);
+    vec = vec && 2 * static_cast<int64_t>(n_heads) * n_sel * (int64_t(1) << chunks_log2) < (int64_t(1) << 31);
     if (vec) {
         const int64_t total = 2 * static_cast<int64_t>(n_heads) * n_sel * (int64_t(1) << chunks_log2);
         scatter_vec_kernel<<<static_cast<unsigned>(ceil_div(total, kThreads)), kThreads, 0, s>>>(a, esize,
