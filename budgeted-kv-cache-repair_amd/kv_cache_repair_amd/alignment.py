@@ -6,6 +6,8 @@ starts). Same definitions as the reference (src/kv_cache_repair/alignment.py:6-3
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 
@@ -39,6 +41,28 @@ def token_alignment(old_ids: list[int], new_ids: list[int]) -> dict[str, int]:
         "mandatory_changed_tokens": len(new_ids) - prefix - suffix,
         "position_shift": new_start - old_start,
     }
+
+
+_ALIGNMENT_KEYS = ("prefix", "suffix", "old_suffix_start", "new_suffix_start", "mandatory_changed_tokens",
+                   "position_shift")
+
+
+def token_alignment_host(old_ids: np.ndarray, new_ids: np.ndarray, vocab: int | None = None) -> dict[str, int]:
+    """token_alignment of two 1-D int64 host arrays in one libkvrepair host call
+    (kvr_token_alignment, same definitions), which also requires every id to lie
+    in [0, vocab) (nonnegative when ``vocab`` is None): ValueError otherwise."""
+    from . import _native
+
+    old_ids = np.ascontiguousarray(old_ids, dtype=np.int64).reshape(-1)
+    new_ids = np.ascontiguousarray(new_ids, dtype=np.int64).reshape(-1)
+    out = (ctypes.c_int64 * 6)()
+    i64p = ctypes.POINTER(ctypes.c_int64)
+    status = _native.lib().kvr_token_alignment(old_ids.ctypes.data_as(i64p), old_ids.size,
+                                               new_ids.ctypes.data_as(i64p), new_ids.size,
+                                               0 if vocab is None else int(vocab), out)
+    if status != 0:
+        raise ValueError("token ids must lie in [0, vocab_size) of the model's embedding table")
+    return dict(zip(_ALIGNMENT_KEYS, out))
 
 
 def token_alignment_arrays(old_ids: np.ndarray, new_ids: np.ndarray) -> dict[str, int]:

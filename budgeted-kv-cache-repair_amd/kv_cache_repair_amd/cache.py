@@ -11,13 +11,15 @@ objects whose layers hold ``[1, kv_heads, tokens, head_dim]`` tensors.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any
 
+import numpy as np
 import torch
 from transformers.cache_utils import DynamicCache, DynamicLayer
 
 from . import _native
-from .alignment import token_alignment, token_alignment_arrays
+from .alignment import token_alignment, token_alignment_host
 from .kernels.executor import layer_kv
 
 
@@ -204,6 +206,17 @@ def run_tokens_from_prefix(model: Any, prefix_cache: Any, input_ids: torch.Tenso
                 return_dict=True).past_key_values
 
 
+def _host_id_rows(old_input_ids: torch.Tensor, new_input_ids: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """Both id rows as int64 host arrays: CPU tensors are read in place (no copy,
+    no device synchronisation, as the API layer holds its tokenizer ids); device
+    ids come over in one device-to-host copy of both rows."""
+    old_row, new_row = old_input_ids[0].reshape(-1), new_input_ids[0].reshape(-1)
+    if old_row.device.type == "cpu" and new_row.device.type == "cpu":
+        return (np.asarray(old_row.numpy(), dtype=np.int64), np.asarray(new_row.numpy(), dtype=np.int64))
+    ids = torch.cat((old_row, new_row.to(device=old_row.device, dtype=old_row.dtype))).cpu().numpy()
+    return ids[:old_row.numel()].astype(np.int64, copy=False), ids[old_row.numel():].astype(np.int64, copy=False)
+
+
 @torch.no_grad()
 def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, new_input_ids: torch.Tensor,
                      halo_tokens: int) -> tuple[DynamicCache, dict[str, int]]:
@@ -212,47 +225,47 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     Same result and metadata as the reference (cache.py:103-144). When no token
     needs recomputation the whole shifted cache (prefix copy, rotated K tail,
     copied V tail, every layer) is written by ONE kvr_shift_cache_build launch
-    into freshly allocated, independently owned tensors; the old cache is
-    never mutated. The alignment is computed on the host: id tensors already on
-    the CPU (as the API layer holds them) are read without a device
-    synchronisation; device ids are copied to the host once.
+    into one freshly allocated slab of independently owned per-layer tensors;
+    the old cache is never mutated. The alignment (and the check that every id
+    indexes the model's embedding table) is one host call on the id rows; the
+    launch takes the per-layer output addresses computed from the slab, and the
+    per-layer tensor views are made after it, while the GPU runs.
     """
-    n_old = int(old_input_ids.shape[1])
     n_new = int(new_input_ids.shape[1])
-    ids = torch.cat((old_input_ids[0].reshape(-1),
-                     new_input_ids[0].reshape(-1).to(device=old_input_ids.device, dtype=old_input_ids.dtype)))
-    # Everything that does not depend on the id values (cache checks, the
-    # output allocation, the launch arguments) is done before the one
-    # device-to-host copy of both id rows, which waits for the stream.
     old = [layer_kv(old_cache, i) for i in range(len(old_cache.layers))]
     _check_uniform(old, "build_halo_cache")
     generator = getattr(model, "generator", model)
     k0 = old[0][0]
-    inv_freq, scaling, rotary_dim = _rotary(generator, k0.device)
-    # one allocation for every layer's K and V; each layer gets contiguous [1, Hkv, N, D] views
-    slab = torch.empty((len(old), 2, 1, k0.shape[1], n_new, k0.shape[3]), dtype=k0.dtype, device=k0.device)
-    views = slab.view(2 * len(old), 1, k0.shape[1], n_new, k0.shape[3]).unbind(0)
-    new = list(zip(views[0::2], views[1::2]))
-    new_k, new_v = list(views[0::2]), list(views[1::2])
-    shift_tail = _shift_launcher([k for k, _ in old], [v for _, v in old], new_k, new_v, inv_freq=inv_freq,
-                                 scaling=scaling, rotary_dim=rotary_dim) if n_new else None
-    ids = ids.cpu().numpy()
-    vocab = _vocab_size(generator)
-    if ids.size and (int(ids.min()) < 0 or (vocab is not None and int(ids.max()) >= vocab)):
-        # the refresh and any boundary recomputation gather embedding rows by
-        # these ids on the GPU: refuse them here, before any launch
-        raise ValueError("token ids must lie in [0, vocab_size) of the model's embedding table")
-    align = token_alignment_arrays(ids[:n_old], ids[n_old:])
+    old_np, new_np = _host_id_rows(old_input_ids, new_input_ids)
+    # the refresh and any boundary recomputation gather embedding rows by these
+    # ids on the GPU: out-of-range ids are refused here, before any launch
+    align = token_alignment_host(old_np, new_np, _vocab_size(generator))
     halo = min(max(int(halo_tokens), 0), align["suffix"])
     recompute_end = align["new_suffix_start"] + halo
     old_tail_start = align["old_suffix_start"] + halo
     tail_rows = align["suffix"] - halo
+    inv_freq, scaling, rotary_dim = _rotary(generator, k0.device)
+    layers, heads, dim = len(old), int(k0.shape[1]), int(k0.shape[3])
+    # one allocation for every layer's K and V; layer l's K is block 2 l, its V block 2 l + 1
+    slab = torch.empty((layers, 2, 1, heads, n_new, dim), dtype=k0.dtype, device=k0.device)
     if recompute_end == align["prefix"]:
         # No recomputed rows: prefix copy + shifted tail in one launch.
         if n_new:
-            shift_tail(prefix_rows=align["prefix"], old_tail_start=old_tail_start, new_tail_start=recompute_end,
-                       tail_rows=tail_rows, shift=align["position_shift"])
+            block = heads * n_new * dim * slab.element_size()
+            base = slab.data_ptr()
+            new_k = (ctypes.c_void_p * layers)(*range(base, base + 2 * layers * block, 2 * block))
+            new_v = (ctypes.c_void_p * layers)(*range(base + block, base + 2 * layers * block, 2 * block))
+            status = _native.lib().kvr_shift_cache_build(
+                _native.ptr_array(k for k, _ in old), _native.ptr_array(v for _, v in old), new_k, new_v, layers,
+                heads, dim, int(rotary_dim), _native.i64_array(_native.strides3(k0)),
+                _native.i64_array((n_new * dim, dim, 1)), align["prefix"], old_tail_start, recompute_end, tail_rows,
+                align["position_shift"], inv_freq.data_ptr(), float(scaling), _native.DTYPE_CODES[k0.dtype],
+                _native.stream_handle(k0.device))
+            _native.check(status, "kvr_shift_cache_build")
+        views = slab.view(2 * layers, 1, heads, n_new, dim).unbind(0)
     else:
+        views = slab.view(2 * layers, 1, heads, n_new, dim).unbind(0)
+        new_k, new_v = list(views[0::2]), list(views[1::2])
         prefix_cache = clone_cache(old_cache, align["prefix"])
         recomputed = run_tokens_from_prefix(generator, prefix_cache,
                                             new_input_ids[:, align["prefix"]:recompute_end].to(k0.device),
@@ -263,10 +276,11 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
                     prefix_rows=recompute_end, old_tail_start=0, new_tail_start=recompute_end, tail_rows=0, shift=0,
                     inv_freq=None, scaling=1.0, rotary_dim=rotary_dim)
         if tail_rows:
-            shift_tail(prefix_rows=0, old_tail_start=old_tail_start, new_tail_start=recompute_end,
-                       tail_rows=tail_rows, shift=align["position_shift"])
-    return cache_from_tensors(new), {**align, "halo_tokens": halo,
-                                     "recomputed_tokens": align["mandatory_changed_tokens"] + halo}
+            _shift_rows([k for k, _ in old], [v for _, v in old], new_k, new_v, prefix_rows=0,
+                        old_tail_start=old_tail_start, new_tail_start=recompute_end, tail_rows=tail_rows,
+                        shift=align["position_shift"], inv_freq=inv_freq, scaling=scaling, rotary_dim=rotary_dim)
+    return cache_from_tensors(zip(views[0::2], views[1::2])), {
+        **align, "halo_tokens": halo, "recomputed_tokens": align["mandatory_changed_tokens"] + halo}
 
 
 def merge_intervals(intervals: list[tuple[int, int]]) -> list[tuple[int, int]]:

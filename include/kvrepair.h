@@ -69,6 +69,19 @@ int kvr_abi_version(void);
 const char* kvr_status_string(int status);
 
 /*
+ * Host-only token alignment of a context edit (no device access): the
+ * reference `token_alignment(old_ids, new_ids)` with `shared_prefix_len` /
+ * `shared_suffix_len` (src/kv_cache_repair/alignment.py:6-31). Writes
+ * out = {prefix, suffix, old_suffix_start, new_suffix_start,
+ * mandatory_changed_tokens, position_shift}. With vocab > 0 every id must lie
+ * in [0, vocab) (else KVR_E_INVALID_ARGUMENT; vocab <= 0: ids only nonnegative),
+ * the check the shift-cache build makes before any launch that gathers
+ * embedding rows by these ids.
+ */
+int kvr_token_alignment(const int64_t* old_ids, int64_t n_old, const int64_t* new_ids, int64_t n_new,
+                        int64_t vocab, int64_t out[6]);
+
+/*
  * RoPE delta re-rotation of retained-suffix keys for every layer in ONE launch.
  *
  * Replaces the per-layer eager chain of the reference

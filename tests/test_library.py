@@ -29,7 +29,7 @@ def test_header_declares_the_entry_points():
         "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
         "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance", "kvr_packed_causal_attention_noalloc",
-        "kvr_attention_scratch_limit"])
+        "kvr_attention_scratch_limit", "kvr_token_alignment"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():

@@ -357,10 +357,12 @@ def test_package_alignment_matches_golden_vectors_and_oracle(old, new, expect):
     golden tuples (tests/test_cache.py:43-68) and the C oracle on random edits."""
     import numpy as np
 
-    from kv_cache_repair_amd.alignment import token_alignment, token_alignment_arrays
+    from kv_cache_repair_amd.alignment import token_alignment, token_alignment_arrays, token_alignment_host
 
     assert tuple(token_alignment(old, new).values()) == expect
     assert tuple(token_alignment_arrays(np.array(old, dtype=np.int64), np.array(new, dtype=np.int64)).values()) == \
+        expect
+    assert tuple(token_alignment_host(np.array(old, dtype=np.int64), np.array(new, dtype=np.int64), 10).values()) == \
         expect
     rng = random.Random(len(old) * 7 + len(new))
     for _ in range(300):
@@ -371,6 +373,25 @@ def test_package_alignment_matches_golden_vectors_and_oracle(old, new, expect):
         want = orc.token_alignment(base, edited)
         assert token_alignment(base, edited) == want
         assert token_alignment_arrays(np.array(base, dtype=np.int64), np.array(edited, dtype=np.int64)) == want
+        assert token_alignment_host(np.array(base, dtype=np.int64), np.array(edited, dtype=np.int64), 4) == want
+
+
+def test_host_alignment_refuses_ids_outside_the_vocabulary():
+    """kvr_token_alignment (the shift-cache build's host call) checks every id of
+    both rows against [0, vocab): the build gathers embedding rows by them."""
+    import numpy as np
+
+    from kv_cache_repair_amd.alignment import token_alignment_host
+
+    old = np.array([1, 2, 3, 4], dtype=np.int64)
+    assert token_alignment_host(old, np.array([1, 3, 4], dtype=np.int64), 5)["position_shift"] == -1
+    assert token_alignment_host(old, old, None)["prefix"] == 4  # no vocabulary: ids only nonnegative
+    for bad_old, bad_new, vocab in (([1, 2, 5], [1, 2], 5), ([1, 2], [1, 9, 2], 5), ([1, -1], [1], 5),
+                                    ([1], [-3], None)):
+        with pytest.raises(ValueError, match="vocab"):
+            token_alignment_host(np.array(bad_old, dtype=np.int64), np.array(bad_new, dtype=np.int64), vocab)
+    # int32 rows are widened; empty rows are valid
+    assert token_alignment_host(np.array([7, 8], dtype=np.int32), np.array([], dtype=np.int32), 9)["suffix"] == 0
 
 
 def test_positions_to_intervals_kat_and_brute_force():
