@@ -68,6 +68,16 @@ def _validate_intervals(intervals: Sequence[tuple[int, int]], logical_length: in
     result = []
     previous_end = -1
     for interval in intervals:
+        # fast path: a (start, end) tuple of plain ints (what every caller builds)
+        if type(interval) is tuple and len(interval) == 2 and type(interval[0]) is int and type(interval[1]) is int:
+            start, end = interval
+            if not 0 <= start < end <= logical_length:
+                raise ValueError("interval bounds must satisfy 0 <= start < end <= token length")
+            if start <= previous_end:
+                raise ValueError("intervals must be sorted, disjoint, and maximal (no adjacent ranges)")
+            result.append(interval)
+            previous_end = end
+            continue
         if not isinstance(interval, (tuple, list)) or len(interval) != 2:
             raise ValueError("each interval must contain exactly a start and end")
         if any(isinstance(value, bool) or not isinstance(value, Integral) for value in interval):

@@ -73,10 +73,13 @@ class IndexedPlan:
             raw = tuple(self.positions)
         except TypeError as error:
             raise ValueError("positions must be a sequence of host integers") from error
-        if any(isinstance(p, bool) or not isinstance(p, Integral) for p in raw):
-            raise ValueError("positions must contain host integers")
-        positions = tuple(int(p) for p in raw)
-        if any(p < 0 or p >= length for p in positions):
+        if all(type(p) is int for p in raw):  # plain ints (the common case): no ABC checks
+            positions = raw
+        else:
+            if any(isinstance(p, bool) or not isinstance(p, Integral) for p in raw):
+                raise ValueError("positions must contain host integers")
+            positions = tuple(int(p) for p in raw)
+        if positions and (min(positions) < 0 or max(positions) >= length):
             raise ValueError("positions must lie within logical_length")
         if any(b <= a for a, b in zip(positions, positions[1:])):
             raise ValueError("positions must be strictly increasing and unique")
@@ -92,8 +95,12 @@ class IndexedPlan:
     def selected_count(self) -> int:
         return len(self.positions)
 
-    def to(self, device: torch.device | str | int) -> "DeviceIndexedPlan":
-        """Upload O(B) metadata on the caller's current stream for this device."""
+    def to(self, device: torch.device | str | int, *, attention: tuple | None = None) -> "DeviceIndexedPlan":
+        """Upload O(B) metadata on the caller's current stream for this device.
+
+        ``attention`` = (n_q_heads, n_kv_heads, head_dim, dtype, rounded) also
+        builds that attention work schedule (DeviceIndexedPlan.attention_schedule)
+        and uploads it in the same copy."""
         device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         if device.type != "cuda":
             raise ValueError("device plan requires a CUDA (ROCm) device")
@@ -102,17 +109,52 @@ class IndexedPlan:
         # int64 positions and bounds; version counters stay live even under
         # inference mode so every launch can reject in-place mutation with a
         # host-side check instead of a device read.
-        # One staged upload for the three arrays; the device tensors are
-        # contiguous views of it (sharing one version counter, so a write
-        # through any of them unseals the plan).
+        # One staged upload for the three arrays (and the schedule); the device
+        # tensors are contiguous views of it (sharing one version counter, so a
+        # write through any of them unseals the plan).
         n, tiles = len(self.positions), len(self.full_prefix_tiles)
+        values = torch.tensor(self.positions + self.full_prefix_tiles + self.total_tiles, dtype=torch.int64)
+        schedule = None
+        if attention is not None:
+            n_q_heads, n_kv_heads, head_dim, dtype, rounded = attention
+            key = _schedule_key(n_q_heads, n_kv_heads, head_dim, dtype, 0, rounded)
+            schedule = (key, _host_schedule(self, key))
         with torch.cuda.device(device), torch.inference_mode(False):
-            packed = _upload(torch.tensor(self.positions + self.full_prefix_tiles + self.total_tiles,
-                                          dtype=torch.int64), device)
+            if schedule is None:
+                packed = _upload(values, device)
+            else:
+                head = 8 * values.numel()
+                staging = torch.empty(head + 4 * len(schedule[1]), dtype=torch.uint8, pin_memory=True)
+                staging[:head].view(torch.int64).copy_(values)
+                staging[head:].view(torch.int32).copy_(torch.frombuffer(schedule[1], dtype=torch.int32))
+                both = staging.to(device, non_blocking=True)
+                packed, sched_dev = both[:head].view(torch.int64), both[head:].view(torch.int32)
             positions, full, total = packed[:n], packed[n:n + tiles], packed[n + tiles:]
         tensors = (positions, full, total)
         seal = (id(self), tuple(id(t) for t in tensors), tuple(t._version for t in tensors))
-        return DeviceIndexedPlan(self, positions, full, total, seal)
+        plan = DeviceIndexedPlan(self, positions, full, total, seal)
+        if schedule is not None:
+            plan._schedules[schedule[0]] = (schedule[1], sched_dev, sched_dev._version)
+        return plan
+
+
+def _schedule_key(n_q_heads, n_kv_heads, head_dim, dtype, chunk_keys, rounded) -> tuple:
+    return (int(n_q_heads), int(n_kv_heads), int(head_dim), dtype, int(chunk_keys), bool(rounded))
+
+
+def _host_schedule(host_plan: "IndexedPlan", key: tuple):
+    """kvr_attention_schedule_ex of ``host_plan`` for ``key`` (a _schedule_key): the
+    int32 host array."""
+    n_q_heads, n_kv_heads, head_dim, dtype, chunk_keys, rounded = key
+    lib = _native.lib()
+    pos = _native.i64_array(host_plan.positions)
+    args = (pos, host_plan.selected_count, host_plan.logical_length, n_q_heads, n_kv_heads, head_dim,
+            _native.DTYPE_CODES[dtype], chunk_keys, _native.ATTN_ROUNDED_PROBABILITIES if rounded else 0)
+    need = lib.kvr_attention_schedule_ex(*args, None, 0)
+    _native.check(int(need), "kvr_attention_schedule_ex")
+    host = (ctypes.c_int32 * int(need))()
+    _native.check(int(lib.kvr_attention_schedule_ex(*args, host, int(need))), "kvr_attention_schedule_ex")
+    return host
 
 
 def _upload(host: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -159,22 +201,14 @@ class DeviceIndexedPlan:
         the input dtype before the PV product (the SDPA precision the packed
         executor replaces); the default keeps them as a hi + lo pair.
         """
-        key = (int(n_q_heads), int(n_kv_heads), int(head_dim), dtype, int(chunk_keys), bool(rounded))
+        key = _schedule_key(n_q_heads, n_kv_heads, head_dim, dtype, chunk_keys, rounded)
         cached = self._schedules.get(key)
         if cached is not None:
             host, dev, version = cached
             if dev._version != version:
                 raise ValueError("device plan attention schedule was mutated")
             return host, dev
-        lib = _native.lib()
-        pos = _native.i64_array(self.host_plan.positions)
-        args = (pos, self.selected_count, self.logical_length, int(n_q_heads), int(n_kv_heads), int(head_dim),
-                _native.DTYPE_CODES[dtype], int(chunk_keys),
-                _native.ATTN_ROUNDED_PROBABILITIES if rounded else 0)
-        need = lib.kvr_attention_schedule_ex(*args, None, 0)
-        _native.check(int(need), "kvr_attention_schedule_ex")
-        host = (ctypes.c_int32 * int(need))()
-        _native.check(int(lib.kvr_attention_schedule_ex(*args, host, int(need))), "kvr_attention_schedule_ex")
+        host = _host_schedule(self.host_plan, key)
         with torch.cuda.device(self.device), torch.inference_mode(False):
             dev = _upload(torch.frombuffer(host, dtype=torch.int32), self.device)
         self._schedules[key] = (host, dev, dev._version)

@@ -24,11 +24,12 @@ import types
 import weakref
 from functools import partial
 from itertools import chain, repeat
-from operator import attrgetter, is_not, itemgetter, methodcaller
+from operator import is_not, itemgetter, methodcaller
 from dataclasses import dataclass, field
 from threading import Lock
 from typing import Any, Sequence
 
+import numpy as np
 import torch
 import transformers
 from transformers.cache_utils import Cache, DynamicLayer
@@ -533,27 +534,23 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
     return view
 
 
-_MODULES = itemgetter("_modules")
 _PARAMETERS = itemgetter("_parameters")
 _TRAINING = itemgetter("training")
 _FORWARD_HOOKS = itemgetter("_forward_hooks")
 _FORWARD_PRE_HOOKS = itemgetter("_forward_pre_hooks")
 _HF_HOOK = methodcaller("get", "_hf_hook")
-_DICT_OF = attrgetter("__dict__")
 _NOT_NONE = partial(is_not, None)
 
 
 def _subtree_dicts(root, skip) -> list:
     """The __dict__ of every module under ``root`` (itself included), level by
     level through the `_modules` dicts, leaving out the subtree of ``skip``.
-    (Iterated with map/chain: the qualification walks every module per refresh.)"""
+    (One list comprehension per level: the qualification walks every module
+    per refresh.)"""
     found, level = [], [root.__dict__]
     while level:
         found += level
-        children = filter(_NOT_NONE, chain.from_iterable(map(dict.values, map(_MODULES, level))))
-        if skip is not None:
-            children = filter(partial(is_not, skip), children)
-        level = list(map(_DICT_OF, children))
+        level = [m.__dict__ for d in level for m in d["_modules"].values() if m is not None and m is not skip]
     return found
 
 
@@ -582,7 +579,9 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     training = any(map(_TRAINING, inner))
     overridden = True in map(dict.__contains__, inner, repeat("forward"))
     everything = inner + outer
-    hooked = True in map(is_not, map(_HF_HOOK, everything), repeat(None))
+    # an accelerate dispatch hook lives in the module's __dict__ as `_hf_hook`
+    hooked = True in map(dict.__contains__, everything, repeat("_hf_hook")) and \
+        True in map(is_not, map(_HF_HOOK, everything), repeat(None))
     # Forward hooks on the decoder's modules (or global ones) run only where the
     # modules' own forwards run: the refresh then takes the module path.
     from torch.nn.modules import module as _module
@@ -695,11 +694,15 @@ class _PackedLayer(DynamicLayer):
         self.updated = True
 
 
+def _rounded_probabilities(dtype: torch.dtype) -> bool:
+    """The reference executor's SDPA rounds probabilities to the 16-bit input
+    dtype before PV (packed_cache.py:60-67); this path keeps that precision."""
+    return dtype in (torch.bfloat16, torch.float16)
+
+
 def _launcher(device_plan: DeviceIndexedPlan, config, key: torch.Tensor) -> _Launcher:
     q_heads, kv_heads, dim = int(config.num_attention_heads), int(key.shape[1]), int(key.shape[3])
-    # the reference executor's SDPA rounds probabilities to the 16-bit input
-    # dtype before PV (packed_cache.py:60-67); this path keeps that precision
-    rounded = key.dtype in (torch.bfloat16, torch.float16)
+    rounded = _rounded_probabilities(key.dtype)
     host, dev = device_plan.attention_schedule(q_heads, kv_heads, dim, key.dtype, rounded=rounded)
     ws_bytes = int(_native.lib().kvr_attention_workspace_bytes(host, len(host), q_heads, dim))
     _native.check(ws_bytes, "kvr_attention_workspace_bytes")
@@ -797,6 +800,15 @@ def _native_layers_for(native_layers, base, plans, fused_epilogue: bool, fused_l
     return bool(native_layers)
 
 
+# int64 word offsets of the cache fields in kvr_layer_desc (a multiple of 8 bytes long)
+_DESC_K = _native.LayerDesc.cache_k.offset // 8
+_DESC_V = _native.LayerDesc.cache_v.offset // 8
+_DESC_STRIDES = _native.LayerDesc.cache_strides.offset // 8
+if ctypes.sizeof(_native.LayerDesc) % 8 or (_native.LayerDesc.cache_k.offset | _native.LayerDesc.cache_v.offset
+                                             | _native.LayerDesc.cache_strides.offset) % 8:
+    raise RuntimeError("kvr_layer_desc layout is not 8-byte aligned")
+
+
 def _native_layer_descs(plans, output, layer_count):
     """Per-refresh array of the layers' descriptors with this cache's pointers;
     each layer but the last computes the next layer's input norm in its down
@@ -814,11 +826,12 @@ def _native_layer_descs(plans, output, layer_count):
         if isinstance(plans, _PlanList):
             plans.descs_template = template
     descs = (_native.LayerDesc * layer_count).from_buffer_copy(template)
-    for desc, layer in zip(descs, output.layers):
-        keys, values = layer.keys, layer.values
-        desc.cache_k, desc.cache_v = keys.data_ptr(), values.data_ptr()
-        ks, vs = keys.stride(), values.stride()
-        desc.cache_strides[:] = (ks[1], ks[2], ks[3], vs[1], vs[2], vs[3])
+    # the per-layer cache fields through one int64 view of the descriptor array
+    words = np.frombuffer(descs, dtype=np.int64).reshape(layer_count, -1)
+    layers = output.layers
+    words[:, _DESC_K] = [layer.keys.data_ptr() for layer in layers]
+    words[:, _DESC_V] = [layer.values.data_ptr() for layer in layers]
+    words[:, _DESC_STRIDES:_DESC_STRIDES + 6] = [layer.keys.stride()[1:] + layer.values.stride()[1:] for layer in layers]
     return descs
 
 
@@ -899,9 +912,12 @@ def _refresh_into(shim, output, edited_ids_t, host_plan: IndexedPlan, layer_coun
                              "native_layers must not be requested")
         fused_layers = fused_projections = native_layers = False
     base = shim._base_transformer(shim.generator)
-    device_plan = host_plan.to(edited_ids_t.device)
-    positions = device_plan.positions
     key0 = layer_kv(output, 0)[0]
+    # the plan and the attention schedule _launcher asks for, in one upload
+    device_plan = host_plan.to(edited_ids_t.device, attention=(
+        int(base.config.num_attention_heads), int(key0.shape[1]), int(key0.shape[3]), key0.dtype,
+        _rounded_probabilities(key0.dtype)))
+    positions = device_plan.positions
     launcher = _launcher(device_plan, base.config, key0)
     plans = _projection_plans_for(base, fused_projections, key0.dtype, device_plan.selected_count, fingerprint)
     fused_layers = _fused_layers_for(fused_layers, key0.dtype)
