@@ -1299,6 +1299,71 @@ def profile_kernels(args, workload: Workload, device) -> dict:
     return {"profiled": names, "launches_each": args.profile_launches, "workload": workload.name}
 
 
+def host_timeline(args, workload: Workload, device) -> dict:
+    """When, within one synchronised stage call, the host issues the stage's
+    three launches that bracket its host work: the shift-cache build, the
+    refresh's first kernel (kvr_refresh_inputs) and the enqueue of every layer
+    (kvr_decoder_forward, entry and return), plus the call's return and its
+    completion (after torch.cuda.synchronize()). Medians over ``args.steps``
+    calls after ``args.warmup``, microseconds from the call's entry. The GPU
+    idles until the first launch and between the build's end and the refresh's
+    first kernel whenever the host work between them outlasts the build."""
+    from kv_cache_repair_amd import _native
+    from kv_cache_repair_amd.cache import OperatorShim
+
+    lib = _native.lib()
+    model = make_model(device, workload)
+    shim = OperatorShim(model)
+    old, old_ids, new_ids = make_request(device, workload)
+    intervals = workload.intervals()
+    host_ids = (old_ids.cpu(), new_ids.cpu())
+    marks = {}
+    originals = {}
+
+    def stamped(name):
+        fn = originals[name] = getattr(lib, name)
+
+        def call(*a):
+            marks[name + " entry"] = time.perf_counter()
+            status = fn(*a)
+            marks[name + " return"] = time.perf_counter()
+            return status
+        return call
+
+    names = ("kvr_shift_cache_build", "kvr_refresh_inputs", "kvr_decoder_forward")
+    for name in names:
+        setattr(lib, name, stamped(name))
+    samples = []
+    try:
+        with no_gc():
+            for i in range(args.warmup + args.steps):
+                marks.clear()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                out = hip_stage(shim, old, old_ids, new_ids, intervals, host_ids=host_ids)
+                t1 = time.perf_counter()
+                torch.cuda.synchronize()
+                t2 = time.perf_counter()
+                del out
+                if i >= args.warmup:
+                    samples.append({**{k: (v - t0) * 1e6 for k, v in marks.items()},
+                                    "stage call returns": (t1 - t0) * 1e6, "stage complete (synchronised)": (t2 - t0) * 1e6})
+    finally:
+        for name, fn in originals.items():
+            setattr(lib, name, fn)
+    keys = sorted(samples[0], key=lambda k: statistics.median(s[k] for s in samples))
+    # the launchers hold raw pointers into `keep`'s tensors (the build's output
+    # cache among them): keep them alive until the timing is done
+    launchers, keep = kernel_launchers(model, workload, old, old_ids, new_ids, device)
+    build_us = graph_device_us(launchers["kvr_shift_cache_build"][0])
+    del launchers, keep
+    torch.cuda.synchronize()
+    return {"metric": "host timeline of one synchronised stage call (us from entry, medians)",
+            "workload": workload.description, "calls": args.steps, "warmup": args.warmup,
+            "timeline_us": {k: round(statistics.median(s[k] for s in samples), 1) for k in keys},
+            "kernel_device_us": {"kvr_shift_cache_build": build_us}}
+
+
 def run_workload(args, workload: Workload, device) -> dict:
     from kv_cache_repair_amd import _native
     from kv_cache_repair_amd.cache import OperatorShim
@@ -1407,6 +1472,8 @@ def main(argv=None) -> int:
                         help="comma-separated libkvrepair calls (or 'all') to launch --profile-launches times each "
                              "with the workload's shapes, for rocprofv3 counter passes; no stage timing")
     parser.add_argument("--profile-launches", type=int, default=5)
+    parser.add_argument("--host-timeline", action="store_true",
+                        help="print when one synchronised stage call issues its key launches (no stage timing)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build runs on a single GPU (--gpus {args.gpus} requested). "
@@ -1428,7 +1495,9 @@ def main(argv=None) -> int:
                 print(json.dumps(grid_case(model, length, count, 64, args.grid_warmups, args.grid_repeats, 71)),
                       flush=True)
         return 0
-    if args.profile_kernels:
+    if args.host_timeline:
+        line = host_timeline(args, WORKLOADS[args.workload], device)
+    elif args.profile_kernels:
         line = profile_kernels(args, WORKLOADS[args.workload], device)
     else:
         line = run_workload(args, WORKLOADS[args.workload], device)
