@@ -833,8 +833,9 @@ def kernel_launchers(model, workload: Workload, old, old_ids, new_ids, device):
         x = torch.randn(b, w.hidden, device=device, generator=gen, dtype=torch.bfloat16)
         xi = torch.randn(b, w.mlp, device=device, generator=gen, dtype=torch.bfloat16)
         xo = torch.randn(b, w.hq * w.dim, device=device, generator=gen, dtype=torch.bfloat16)
-        gemms = [(mod.weight, xin) for mod, xin in ((a.q_proj, x), (a.k_proj, x), (a.v_proj, x), (a.o_proj, xo),
-                                                    (m.gate_proj, x), (m.up_proj, x), (m.down_proj, xi))]
+        gemms = [(mod.weight.detach(), xin) for mod, xin in ((a.q_proj, x), (a.k_proj, x), (a.v_proj, x),
+                                                             (a.o_proj, xo), (m.gate_proj, x), (m.up_proj, x),
+                                                             (m.down_proj, xi))]
         outs = [torch.empty(b, wt.shape[0], device=device, dtype=torch.bfloat16) for wt, _ in gemms]
 
         def launch_gemms():
