@@ -1959,10 +1959,18 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Ordering of the calls that use one device's array: the completion event of
+// the last call enqueued outside graph capture, and its stream. A call on
+// another stream first waits for that event on the device, so two such calls
+// never overlap (no host blocking, no rejection of correctly ordered callers).
+hipEvent_t g_scratch_done[kMaxDevices] = {};
+hipStream_t g_scratch_last[kMaxDevices] = {};
+bool g_scratch_used[kMaxDevices] = {};
 
 // Device address of `scratch` on the device of `stream` (which must be the
-// current device); nullptr when the lookup fails.
-void* scratch_address(void* stream) {
+// current device), and that device; nullptr when the lookup fails. The first
+// call on a device also creates its ordering event (no device allocation).
+void* scratch_address(void* stream, int* device) {
     int current = -1;
     if (hipGetDevice(&current) != hipSuccess || current < 0 || current >= kMaxDevices) return nullptr;
     if (stream) {
@@ -1973,10 +1981,51 @@ void* scratch_address(void* stream) {
     if (!g_scratch_ptr[current]) {
         void* ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        if (!g_scratch_done[current] &&
+            hipEventCreateWithFlags(&g_scratch_done[current], hipEventDisableTiming) != hipSuccess) {
+            g_scratch_done[current] = nullptr;
+            return nullptr;
+        }
         g_scratch_ptr[current] = ptr;
     }
+    *device = current;
     return g_scratch_ptr[current];
 }
+
+// Serialises the calls on one device's scratch array for the duration of an
+// enqueue: outside graph capture, a call on a stream other than the previous
+// call's waits on the device for the previous call's completion event, and
+// records its own when its launches are enqueued. Under capture (where a
+// wait on an event recorded outside the graph is not allowed) neither
+// happens: replays of captured calls must be ordered by the caller.
+class ScratchOrder {
+  public:
+    ScratchOrder() = default;
+    int begin(int device, hipStream_t s) {
+        lock_ = std::unique_lock<std::mutex>(g_scratch_mutex);
+        hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return KVR_OK;
+        if (g_scratch_used[device] && g_scratch_last[device] != s &&
+            hipStreamWaitEvent(s, g_scratch_done[device], 0) != hipSuccess)
+            return KVR_E_DEVICE;
+        device_ = device;
+        stream_ = s;
+        return KVR_OK;
+    }
+    // after the launches (whatever their status): the array is in use until `stream_` gets here
+    int end() {
+        if (device_ < 0) return KVR_OK;
+        if (hipEventRecord(g_scratch_done[device_], stream_) != hipSuccess) return KVR_E_DEVICE;
+        g_scratch_last[device_] = stream_;
+        g_scratch_used[device_] = true;
+        return KVR_OK;
+    }
+
+  private:
+    std::unique_lock<std::mutex> lock_;
+    int device_ = -1;
+    hipStream_t stream_ = nullptr;
+};
 
 }  // namespace
 }  // namespace kvr
@@ -2235,10 +2284,11 @@ int attention_call(const void* q, const void* k, const void* v, void* out, const
     if (hs[H_PROB] != 0 && hs[H_PROB] != 1) return KVR_E_BAD_SCHEDULE;
     const int64_t ws_need = kvr_attention_workspace_bytes(hs, schedule_len, n_q_heads, head_dim);
     if (ws_need < 0) return KVR_E_BAD_SCHEDULE;
+    int scratch_device = -1;
     if (scratch_limit > 0) {
         if (ws_need > scratch_limit) return KVR_E_SCRATCH_LIMIT;
         if (ws_need > 0) {
-            workspace = scratch_address(stream);
+            workspace = scratch_address(stream, &scratch_device);
             if (!workspace) return KVR_E_DEVICE;
             workspace_bytes = scratch_limit;
         }
@@ -2298,6 +2348,13 @@ int attention_call(const void* q, const void* k, const void* v, void* out, const
 
     hipStream_t s = as_stream(stream);
     const dim3 grid(static_cast<unsigned>(n_kv_heads * a.n_head_groups), static_cast<unsigned>(a.n_work));
+    const int dmax = use_mfma ? 0 : generic_dmax(head_dim);
+    if (!use_mfma && dmax == 0) return KVR_E_UNSUPPORTED_SHAPE;
+    ScratchOrder order;
+    if (scratch_device >= 0) {
+        const int ost = order.begin(scratch_device, s);
+        if (ost != KVR_OK) return ost;
+    }
     int st;
     if (use_mfma) {
         if (dtype == KVR_DTYPE_BF16)
@@ -2305,20 +2362,21 @@ int attention_call(const void* q, const void* k, const void* v, void* out, const
         else
             st = head_dim == 128 ? launch_mfma<f16_t, 128>(a, a.qt, grid, s) : launch_mfma<f16_t, 64>(a, a.qt, grid, s);
     } else {
-        const int dmax = generic_dmax(head_dim);
-        if (dmax == 0) return KVR_E_UNSUPPORTED_SHAPE;
         switch (dtype) {
             case KVR_DTYPE_F32: st = launch_generic<f32_t>(a, dmax, grid, s); break;
             case KVR_DTYPE_F16: st = launch_generic<f16_t>(a, dmax, grid, s); break;
             default: st = launch_generic<bf16_t>(a, dmax, grid, s); break;
         }
     }
-    if (st != KVR_OK || hs[H_NMULTI] == 0) return st;
-    switch (dtype) {
-        case KVR_DTYPE_F32: return launch_merge<f32_t>(a, hs[H_MAXCHUNKS], s);
-        case KVR_DTYPE_F16: return launch_merge<f16_t>(a, hs[H_MAXCHUNKS], s);
-        default: return launch_merge<bf16_t>(a, hs[H_MAXCHUNKS], s);
+    if (st == KVR_OK && hs[H_NMULTI] != 0) {
+        switch (dtype) {
+            case KVR_DTYPE_F32: st = launch_merge<f32_t>(a, hs[H_MAXCHUNKS], s); break;
+            case KVR_DTYPE_F16: st = launch_merge<f16_t>(a, hs[H_MAXCHUNKS], s); break;
+            default: st = launch_merge<bf16_t>(a, hs[H_MAXCHUNKS], s); break;
+        }
     }
+    const int ost = order.end();
+    return st != KVR_OK ? st : ost;
 }
 
 }  // namespace

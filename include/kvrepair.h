@@ -466,11 +466,17 @@ int kvr_packed_causal_attention(const void* q, const void* k, const void* v, voi
  * on every device where its code object loads, until the process ends. A
  * schedule whose kvr_attention_workspace_bytes exceeds that limit is refused
  * with KVR_E_SCRATCH_LIMIT before anything is launched; use the workspace
- * entry point for it. The call allocates and frees nothing. `stream` must
- * belong to the current device. All calls on one device share the array
- * (its previous contents are never read: every partial a launch reads is
- * written by the same launch), so calls that overlap on one device --
- * concurrent streams or threads -- race and must be serialised by the caller.
+ * entry point for it. The call allocates and frees nothing (the first call
+ * on a device looks up the array's address and creates one event for the
+ * ordering below). `stream` must belong to the current device. All calls on
+ * one device share the array (its previous contents are never read: every
+ * partial a launch reads is written by the same launch). Calls made outside
+ * graph capture are ordered on the device: a call on a stream other than the
+ * previous call's first waits (hipStreamWaitEvent, no host blocking) for the
+ * previous call to finish, so concurrent streams or threads cannot overlap on
+ * the array. Calls captured into a graph are not tracked: replays of captured
+ * calls, and eager calls running beside such a replay, must be ordered by the
+ * caller (replay on one stream).
  */
 int kvr_packed_causal_attention_noalloc(const void* q, const void* k, const void* v, void* out,
                                         const int64_t* positions, int64_t n_sel, int32_t n_q_heads,
