@@ -691,6 +691,14 @@ def graph_device_us(launch, per_graph: int = 20, replays: int = 5) -> float:
     return us
 
 
+def launch_floor_us(device) -> float:
+    """Per-launch device time of a one-element fill kernel timed like every
+    libkvrepair call (graph of back-to-back launches): the floor under which
+    no launch's average duration falls, whatever its bytes."""
+    t = torch.zeros(1, device=device)
+    return graph_device_us(lambda: t.zero_())
+
+
 def _checked(fn, *args, after=()):
     """A launch of ``fn(*args, stream, *after)`` on the stream current at call
     time (a graph capture swaps it), raising on a nonzero status."""
@@ -1388,6 +1396,7 @@ def run_workload(args, workload: Workload, device) -> dict:
     back_to_back = time_steps(step, args.steps, 0)
     kernels = measure_kernels(model, workload, old, old_ids, new_ids, device)
     roofline, north = rooflines(kernels, workload.name)
+    floor_us = launch_floor_us(device)
 
     reference = None
     interleaved = None
@@ -1441,6 +1450,9 @@ def run_workload(args, workload: Workload, device) -> dict:
                          "call with the stage's shapes (device time only); kvr_linear_multi = one layer's four "
                          "projections as the native forward launches them (q/k/v, o, down leave split-K partials "
                          "to their consumers: kvr_linear_multi_partials), per projection",
+        "launch_floor_us": floor_us,
+        "launch_floor": "the same graph timing of a one-element fill kernel: the per-launch time no launch "
+                        "goes below (small launches, such as the scatter and the epilogue at <= 64 rows, sit near it)",
         "reference_same_gpu": reference, "interleaved": interleaved, "checks": checks, "selection_scoring": scoring,
         "cpu_baseline": cpu, "device": torch.cuda.get_device_name(device),
     }
