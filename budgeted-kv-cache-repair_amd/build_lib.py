@@ -1,4 +1,5 @@
-"""Build libkvrepair.so (gfx950 HIP kernels + C ABI) in-tree with hipcc.
+"""Build libkvrepair.so (gfx950 HIP kernels + C ABI) in-tree with hipcc, and the
+host-side CPython extension _kvr_walk (the executor's module-tree walk) with gcc.
 
 The library links the HIP runtime by SONAME (libamdhip64.so.7). It must be
 loaded after ``import torch`` so that the dynamic linker binds it to the
@@ -10,6 +11,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PACKAGE_ROOT = Path(__file__).resolve().parent
@@ -17,6 +19,8 @@ REPO_ROOT = PACKAGE_ROOT.parent
 CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / "libkvrepair.so"
+WALK_SOURCE = CSRC / "kvr_module_walk.c"
+WALK_OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / ("_kvr_walk" + sysconfig.get_config_var("EXT_SUFFIX"))
 SOURCES = ("kvr_common.hip", "kvr_rotate.hip", "kvr_scatter.hip", "kvr_fresh.hip", "kvr_layer.hip", "kvr_gemm.hip", "kvr_attention.hip", "kvr_decoder.hip", "kvr_writeback.hip", "kvr_inputs.hip", "kvr_scoring.hip")
 ARCH = "gfx950"
 
@@ -51,8 +55,25 @@ def _defines() -> list[str]:
     return [f"-DKVR_ATTN_SCRATCH_MB={int(mb)}"]
 
 
+def build_walk(verbose: bool = False) -> Path:
+    """Compile the _kvr_walk CPython extension (host C, this interpreter's
+    headers) next to the package's modules; returns its path."""
+    tmp = WALK_OUTPUT.with_name(WALK_OUTPUT.name + ".tmp")
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-shared", "-fPIC", "-Wall", "-Werror",
+           f"-I{sysconfig.get_paths()['include']}", str(WALK_SOURCE), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    result = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if result.returncode != 0:
+        raise RuntimeError("gcc failed for _kvr_walk:\n" + result.stdout)
+    os.replace(tmp, WALK_OUTPUT)
+    return WALK_OUTPUT
+
+
 def build(verbose: bool = False, jobs: int = 4) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
+    """Compile every HIP source and link the shared library, then the _kvr_walk
+    extension; returns the library's path."""
+    build_walk(verbose)
     build_dir = PACKAGE_ROOT / "_build"
     defines = _defines()
     build_dir.mkdir(exist_ok=True)

@@ -60,8 +60,10 @@ class RefreshDesc(ctypes.Structure):
 def _declare(lib: ctypes.CDLL) -> None:
     lib.kvr_abi_version.argtypes = []
     lib.kvr_abi_version.restype = ctypes.c_int
-    lib.kvr_token_alignment.argtypes = [_i64p, ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.c_int64, _i64p]
+    lib.kvr_token_alignment.argtypes = [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int64, _i64p]
     lib.kvr_token_alignment.restype = ctypes.c_int
+    lib.kvr_upload_async.argtypes = [_vp, _vpp, _i64p, ctypes.c_int32, _vp]
+    lib.kvr_upload_async.restype = ctypes.c_int
     lib.kvr_status_string.argtypes = [ctypes.c_int]
     lib.kvr_status_string.restype = ctypes.c_char_p
     lib.kvr_rope_delta_rotate.argtypes = [_vpp, _vpp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,

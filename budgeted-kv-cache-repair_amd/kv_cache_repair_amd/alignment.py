@@ -56,10 +56,9 @@ def token_alignment_host(old_ids: np.ndarray, new_ids: np.ndarray, vocab: int | 
     old_ids = np.ascontiguousarray(old_ids, dtype=np.int64).reshape(-1)
     new_ids = np.ascontiguousarray(new_ids, dtype=np.int64).reshape(-1)
     out = (ctypes.c_int64 * 6)()
-    i64p = ctypes.POINTER(ctypes.c_int64)
-    status = _native.lib().kvr_token_alignment(old_ids.ctypes.data_as(i64p), old_ids.size,
-                                               new_ids.ctypes.data_as(i64p), new_ids.size,
-                                               0 if vocab is None else int(vocab), out)
+    # the arrays stay referenced here for the duration of the call
+    status = _native.lib().kvr_token_alignment(old_ids.ctypes.data, old_ids.size, new_ids.ctypes.data,
+                                               new_ids.size, 0 if vocab is None else int(vocab), out)
     if status != 0:
         raise ValueError("token ids must lie in [0, vocab_size) of the model's embedding table")
     return dict(zip(_ALIGNMENT_KEYS, out))

@@ -210,9 +210,10 @@ def _host_id_rows(old_input_ids: torch.Tensor, new_input_ids: torch.Tensor) -> t
     """Both id rows as int64 host arrays: CPU tensors are read in place (no copy,
     no device synchronisation, as the API layer holds its tokenizer ids); device
     ids come over in one device-to-host copy of both rows."""
+    if old_input_ids.device.type == "cpu" and new_input_ids.device.type == "cpu":
+        return (np.asarray(old_input_ids.numpy()[0], dtype=np.int64).reshape(-1),
+                np.asarray(new_input_ids.numpy()[0], dtype=np.int64).reshape(-1))
     old_row, new_row = old_input_ids[0].reshape(-1), new_input_ids[0].reshape(-1)
-    if old_row.device.type == "cpu" and new_row.device.type == "cpu":
-        return (np.asarray(old_row.numpy(), dtype=np.int64), np.asarray(new_row.numpy(), dtype=np.int64))
     ids = torch.cat((old_row, new_row.to(device=old_row.device, dtype=old_row.dtype))).cpu().numpy()
     return ids[:old_row.numel()].astype(np.int64, copy=False), ids[old_row.numel():].astype(np.int64, copy=False)
 

@@ -109,27 +109,25 @@ class IndexedPlan:
         # int64 positions and bounds; version counters stay live even under
         # inference mode so every launch can reject in-place mutation with a
         # host-side check instead of a device read.
-        # One staged upload for the three arrays (and the schedule); the device
-        # tensors are contiguous views of it (sharing one version counter, so a
-        # write through any of them unseals the plan).
+        # One upload for the three arrays (and the schedule) through the
+        # library's pinned staging (kvr_upload_async); the device tensors are
+        # contiguous views of it (sharing one version counter, so a write
+        # through any of them unseals the plan).
         n, tiles = len(self.positions), len(self.full_prefix_tiles)
-        values = torch.tensor(self.positions + self.full_prefix_tiles + self.total_tiles, dtype=torch.int64)
+        values = (ctypes.c_int64 * (n + 2 * tiles))(*self.positions, *self.full_prefix_tiles, *self.total_tiles)
+        parts = [values]
         schedule = None
         if attention is not None:
             n_q_heads, n_kv_heads, head_dim, dtype, rounded = attention
             key = _schedule_key(n_q_heads, n_kv_heads, head_dim, dtype, 0, rounded)
-            schedule = (key, _host_schedule(self, key))
-        with torch.cuda.device(device), torch.inference_mode(False):
-            if schedule is None:
-                packed = _upload(values, device)
-            else:
-                head = 8 * values.numel()
-                staging = torch.empty(head + 4 * len(schedule[1]), dtype=torch.uint8, pin_memory=True)
-                staging[:head].view(torch.int64).copy_(values)
-                staging[head:].view(torch.int32).copy_(torch.frombuffer(schedule[1], dtype=torch.int32))
-                both = staging.to(device, non_blocking=True)
-                packed, sched_dev = both[:head].view(torch.int64), both[head:].view(torch.int32)
+            schedule = (key, _host_schedule(self, key, values))
+            parts.append(schedule[1])
+        with torch.inference_mode(False):
+            both = _upload(parts, device)
+            head = ctypes.sizeof(values)
+            packed = both[:head].view(torch.int64)
             positions, full, total = packed[:n], packed[n:n + tiles], packed[n + tiles:]
+            sched_dev = both[head:].view(torch.int32) if schedule is not None else None
         tensors = (positions, full, total)
         seal = (id(self), tuple(id(t) for t in tensors), tuple(t._version for t in tensors))
         plan = DeviceIndexedPlan(self, positions, full, total, seal)
@@ -142,12 +140,13 @@ def _schedule_key(n_q_heads, n_kv_heads, head_dim, dtype, chunk_keys, rounded) -
     return (int(n_q_heads), int(n_kv_heads), int(head_dim), dtype, int(chunk_keys), bool(rounded))
 
 
-def _host_schedule(host_plan: "IndexedPlan", key: tuple):
+def _host_schedule(host_plan: "IndexedPlan", key: tuple, positions=None):
     """kvr_attention_schedule_ex of ``host_plan`` for ``key`` (a _schedule_key): the
-    int32 host array."""
+    int32 host array. ``positions``: the plan's positions as a ctypes int64
+    array (its first selected_count entries), when the caller has one."""
     n_q_heads, n_kv_heads, head_dim, dtype, chunk_keys, rounded = key
     lib = _native.lib()
-    pos = _native.i64_array(host_plan.positions)
+    pos = _native.i64_array(host_plan.positions) if positions is None else positions
     args = (pos, host_plan.selected_count, host_plan.logical_length, n_q_heads, n_kv_heads, head_dim,
             _native.DTYPE_CODES[dtype], chunk_keys, _native.ATTN_ROUNDED_PROBABILITIES if rounded else 0)
     need = lib.kvr_attention_schedule_ex(*args, None, 0)
@@ -157,12 +156,18 @@ def _host_schedule(host_plan: "IndexedPlan", key: tuple):
     return host
 
 
-def _upload(host: torch.Tensor, device: torch.device) -> torch.Tensor:
-    """Copy a small host tensor to ``device`` on the current stream without
-    blocking the host: staged through pinned memory (whose block the caching
-    host allocator keeps until the copy has run), so the refresh's kernels can
-    be enqueued while earlier work is still running."""
-    return host.pin_memory().to(device, non_blocking=True)
+def _upload(parts, device: torch.device) -> torch.Tensor:
+    """A uint8 tensor on ``device`` holding the host buffers ``parts`` (ctypes
+    arrays) back to back: one kvr_upload_async copy on the device's current
+    stream from the library's pinned staging, so the host does not wait and the
+    refresh's kernels can be enqueued while earlier work is still running."""
+    sizes = [ctypes.sizeof(part) for part in parts]
+    out = torch.empty(sum(sizes), dtype=torch.uint8, device=device)
+    count = len(parts)
+    status = _native.lib().kvr_upload_async(out.data_ptr(), (ctypes.c_void_p * count)(*map(ctypes.addressof, parts)),
+                                            (ctypes.c_int64 * count)(*sizes), count, _native.stream_handle(device))
+    _native.check(status, "kvr_upload_async")
+    return out
 
 
 @dataclass(frozen=True)
@@ -209,8 +214,8 @@ class DeviceIndexedPlan:
                 raise ValueError("device plan attention schedule was mutated")
             return host, dev
         host = _host_schedule(self.host_plan, key)
-        with torch.cuda.device(self.device), torch.inference_mode(False):
-            dev = _upload(torch.frombuffer(host, dtype=torch.int32), self.device)
+        with torch.inference_mode(False):
+            dev = _upload([host], self.device).view(torch.int32)
         self._schedules[key] = (host, dev, dev._version)
         return host, dev
 

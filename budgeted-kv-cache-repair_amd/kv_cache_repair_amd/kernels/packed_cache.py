@@ -22,9 +22,6 @@ import copy
 import ctypes
 import types
 import weakref
-from functools import partial
-from itertools import chain, repeat
-from operator import is_not, itemgetter, methodcaller
 from dataclasses import dataclass, field
 from threading import Lock
 from typing import Any, Sequence
@@ -534,24 +531,16 @@ def _make_native_view(base, fused_epilogue: bool = True, fused_layers: bool = Tr
     return view
 
 
-_PARAMETERS = itemgetter("_parameters")
-_TRAINING = itemgetter("training")
-_FORWARD_HOOKS = itemgetter("_forward_hooks")
-_FORWARD_PRE_HOOKS = itemgetter("_forward_pre_hooks")
-_HF_HOOK = methodcaller("get", "_hf_hook")
-_NOT_NONE = partial(is_not, None)
-
-
-def _subtree_dicts(root, skip) -> list:
-    """The __dict__ of every module under ``root`` (itself included), level by
-    level through the `_modules` dicts, leaving out the subtree of ``skip``.
-    (One list comprehension per level: the qualification walks every module
-    per refresh.)"""
-    found, level = [], [root.__dict__]
-    while level:
-        found += level
-        level = [m.__dict__ for d in level for m in d["_modules"].values() if m is not None and m is not skip]
-    return found
+def _module_walk():
+    """The _kvr_walk extension (built in-tree with libkvrepair.so): one C pass
+    over the module tree for the qualification below. No Python fallback: a
+    missing build raises here."""
+    try:
+        from .. import _kvr_walk
+    except ImportError as error:
+        raise ImportError("kv_cache_repair_amd._kvr_walk is not built: run build_lib.py (or "
+                          "__graft_entry__.build())") from error
+    return _kvr_walk
 
 
 def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend):
@@ -568,35 +557,27 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     if (type(model), type(base)) not in {(LlamaForCausalLM, LlamaModel), (Qwen3ForCausalLM, Qwen3Model)}:
         raise ValueError("packed executor requires exact native dense Llama or Qwen3 classes")
     device = edited_ids.device
-    # Module-tree conditions, gathered from the modules' __dict__s in two flat
-    # walks through the `_modules` dicts: the decoder (`base`) subtree, whose
-    # modules must all be in eval mode with no per-instance forward, and the
-    # rest of the model; no module anywhere may carry a dispatch hook or a
-    # parameter off the request device (compared by index: get_device() is -1
-    # off the GPUs, and the request device is a GPU when it matters below).
+    # Module-tree conditions, gathered from the modules' __dict__s in one C pass
+    # (_kvr_walk.qualify_walk) through the `_modules` dicts: over the decoder
+    # (`base`) subtree, whose modules must all be in eval mode with no
+    # per-instance forward and whose forward hooks send the refresh down the
+    # module path, and over the rest of the model; no module anywhere may carry
+    # a dispatch hook (accelerate's lives in the module's __dict__ as `_hf_hook`)
+    # or a parameter off the request device (compared by index: get_device() is
+    # -1 off the GPUs, and the request device is a GPU when it matters below).
     index = device.index if device.type == "cuda" else -2
-    inner, outer = _subtree_dicts(base, None), _subtree_dicts(model, base)
-    training = any(map(_TRAINING, inner))
-    overridden = True in map(dict.__contains__, inner, repeat("forward"))
-    everything = inner + outer
-    # an accelerate dispatch hook lives in the module's __dict__ as `_hf_hook`
-    hooked = True in map(dict.__contains__, everything, repeat("_hf_hook")) and \
-        True in map(is_not, map(_HF_HOOK, everything), repeat(None))
-    # Forward hooks on the decoder's modules (or global ones) run only where the
-    # modules' own forwards run: the refresh then takes the module path.
+    training, overridden, hooked, forward_hooked, params, dict_ids, param_ids, ptrs = \
+        _module_walk().qualify_walk(model, base, torch.Tensor.data_ptr)
     from torch.nn.modules import module as _module
 
-    forward_hooked = (any(map(_FORWARD_HOOKS, inner)) or any(map(_FORWARD_PRE_HOOKS, inner))
-                      or bool(_module._global_forward_hooks) or bool(_module._global_forward_pre_hooks))
+    forward_hooked = (forward_hooked or bool(_module._global_forward_hooks)
+                      or bool(_module._global_forward_pre_hooks))
     # Fingerprint of the tree: every module (its __dict__'s identity) and every
     # parameter slot (the tensor's identity and storage address; an empty slot
     # counts). A tree with the fingerprint that last qualified on this GPU has
     # the same parameter tensors at the same addresses, so their device check
     # holds as it did; the layer plans are reused under the same condition.
-    params = list(chain.from_iterable(map(dict.values, map(_PARAMETERS, everything))))
-    # (empty slots hold None, whose identity the second tuple already records)
-    ptrs = tuple(map(torch.Tensor.data_ptr, filter(_NOT_NONE, params)))
-    fingerprint = (tuple(map(id, everything)), tuple(map(id, params)), ptrs)
+    fingerprint = (dict_ids, param_ids, ptrs)
     with _PLAN_LOCK:
         previous = _QUALIFIED.get(base)
     if previous is not None and previous[1] == index and previous[0] == fingerprint:

@@ -15,7 +15,9 @@
  *   - `dtype` is one of KVR_DTYPE_*; every tensor of a call shares it.
  *   - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream);
  *     NULL means the legacy default stream. Calls only enqueue work on that
- *     stream: no allocation, no free, no host<->device copy, no synchronisation.
+ *     stream: no allocation, no free, no host<->device copy, no synchronisation
+ *     (the one exception is kvr_upload_async, whose job is a host-to-device
+ *     copy from the library's own pinned staging).
  *   - Return value 0 is success; a negative value is a KVR_E_* status whose
  *     text kvr_status_string() gives. Arguments are checked before any launch:
  *     a failed check enqueues nothing.
@@ -67,6 +69,26 @@ int kvr_abi_version(void);
 
 /* Static, NUL-terminated description of a status code. */
 const char* kvr_status_string(int status);
+
+/*
+ * Asynchronous host-to-device upload of small metadata (a plan's positions and
+ * tile bounds, an attention schedule): the `count` host ranges (srcs[i],
+ * sizes[i] bytes) are packed back to back into a pinned staging buffer that
+ * the library owns, and one copy of the concatenation to `dst` (device memory)
+ * is enqueued on `stream`; the call returns without waiting for the device,
+ * and the host ranges may be reused as soon as it returns. Each device of a
+ * stream has a ring of 8 staging buffers; a buffer is reused only after its
+ * previous copy has completed (its event is waited for then). Buffers are
+ * pinned with hipHostMalloc on first use and grown when an upload does not fit
+ * (at most 256 MiB per upload, else KVR_E_INVALID_ARGUMENT); they are held
+ * until the process ends. Refused under stream capture (KVR_E_INVALID_ARGUMENT:
+ * a captured copy would read the buffer again at every replay). Thread-safe.
+ * No counterpart in the reference, whose plan upload is three
+ * torch.tensor(..., device=...) calls (src/kv_cache_repair/kernels/
+ * indexed_attention.py:104-107); this one call replaces the chain of host-side
+ * tensor operations (pinned staging, packing, copy) of the refresh's set-up.
+ */
+int kvr_upload_async(void* dst, const void* const* srcs, const int64_t* sizes, int32_t count, void* stream);
 
 /*
  * Host-only token alignment of a context edit (no device access): the

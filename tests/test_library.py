@@ -29,7 +29,7 @@ def test_header_declares_the_entry_points():
         "kvr_decoder_scratch_bytes",
         "kvr_decoder_gemm_workspace_bytes", "kvr_decoder_layer", "kvr_decoder_forward", "kvr_decoder_desc_sizes",
         "kvr_copy_kv_interval", "kvr_refresh_inputs", "kvr_query_relevance", "kvr_packed_causal_attention_noalloc",
-        "kvr_attention_scratch_limit", "kvr_token_alignment"])
+        "kvr_attention_scratch_limit", "kvr_token_alignment", "kvr_upload_async"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -78,6 +78,14 @@ def test_entry_points_validate_before_any_launch():
     assert lib.kvr_rms_norm(None, None, None, None, None, 4, 4096, rs, 1e-5, 2, None) == -5
     assert lib.kvr_rms_norm(None, None, None, None, None, 0, 4096, rs, 1e-5, 2, None) == 0
     assert lib.kvr_silu_mul(None, None, None, 8, 5, None) == -2
+    # uploads: argument checks come before any device query; nothing to copy is a no-op
+    srcs, sizes = (ctypes.c_void_p * 2)(None, None), _native.i64_array([8, 8])
+    assert lib.kvr_upload_async(None, srcs, sizes, 2, None) == -5
+    assert lib.kvr_upload_async(1, srcs, sizes, -1, None) == -1
+    assert lib.kvr_upload_async(1, srcs, _native.i64_array([-8, 8]), 2, None) == -1
+    assert lib.kvr_upload_async(1, srcs, sizes, 2, None) == -5  # null source range
+    assert lib.kvr_upload_async(1, srcs, _native.i64_array([0, 0]), 2, None) == 0
+    assert lib.kvr_upload_async(1, None, None, 0, None) == 0
     assert lib.kvr_silu_mul(None, None, None, -1, 2, None) == -1
     assert lib.kvr_silu_mul(None, None, None, 8, 2, None) == -5
     assert lib.kvr_linear_splits(65, 4096, 4096) == -3 and lib.kvr_linear_splits(64, 4096, 4095) == -3

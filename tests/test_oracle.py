@@ -394,6 +394,41 @@ def test_host_alignment_refuses_ids_outside_the_vocabulary():
     assert token_alignment_host(np.array([7, 8], dtype=np.int32), np.array([], dtype=np.int32), 9)["suffix"] == 0
 
 
+def test_host_alignment_on_long_rows_matches_the_oracle_and_the_range_rule():
+    """Rows long enough for the C scan's 64-id block compares (prefix, suffix and
+    the edited middle at every offset relative to the blocks), random deletions,
+    insertions and substitutions, against the C oracle's alignment; an id outside
+    [0, vocab) planted anywhere in either row is refused."""
+    import numpy as np
+
+    from kv_cache_repair_amd.alignment import token_alignment_host
+
+    rng = random.Random(23)
+    for trial in range(600):
+        base = [rng.randrange(6) for _ in range(rng.randrange(0, 400))]
+        edited = list(base)
+        for _ in range(rng.randrange(0, 3)):
+            at = rng.randrange(len(edited) + 1)
+            kind = rng.randrange(3)
+            if kind == 0:
+                del edited[at:at + rng.randrange(1, 90)]
+            elif kind == 1:
+                edited[at:at] = [rng.randrange(6) for _ in range(rng.randrange(1, 90))]
+            elif edited:
+                edited[rng.randrange(len(edited))] = rng.randrange(6)
+        if trial % 3 == 0:
+            row = base if (trial % 2 and base) or not edited else edited
+            if row:
+                row[rng.randrange(len(row))] = rng.choice([6, 7, -1, -(1 << 40)])
+        bad = any(x < 0 or x >= 6 for x in base + edited)
+        if bad:
+            with pytest.raises(ValueError, match="vocab"):
+                token_alignment_host(np.array(base, dtype=np.int64), np.array(edited, dtype=np.int64), 6)
+        else:
+            assert token_alignment_host(np.array(base, dtype=np.int64), np.array(edited, dtype=np.int64), 6) == \
+                orc.token_alignment(base, edited)
+
+
 def test_positions_to_intervals_kat_and_brute_force():
     # reference tests/test_cache.py:161-162
     assert orc.positions_to_intervals([5, 2, 3, 2, 8, 6]) == [(2, 4), (5, 7), (8, 9)]
