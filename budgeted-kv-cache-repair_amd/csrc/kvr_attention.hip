@@ -936,8 +936,11 @@ struct PairWave {
 
     // Scores past a row's position become -inf (the causal mask; only sub-tiles
     // that reach past the tile's first position need it).
-    __device__ inline void apply_mask(f32x4 (&st)[2], int32_t key0, int lj) {
-        const int32_t lim = pos - key0 - 4 * lj;  // key 16 kt + 4 lj + i is visible iff 16 kt + i <= lim
+    __device__ inline void apply_mask(f32x4 (&st)[2], int32_t key0, int lj) { apply_mask_at(st, key0, lj, pos); }
+
+    // The same with the row's last visible key given (at most its position).
+    __device__ static inline void apply_mask_at(f32x4 (&st)[2], int32_t key0, int lj, int32_t last) {
+        const int32_t lim = last - key0 - 4 * lj;  // key 16 kt + 4 lj + i is visible iff 16 kt + i <= lim
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -1076,7 +1079,6 @@ struct PairWave {
                                    float scale_log2) {
         f32x4 s0[2], s1[2];
         float x0[2][4], x1[2][4];
-        u32x4 h0, l0, h1, l1;
         qk(0, kf, s0);
         qk(1, kf, s1);
         __builtin_amdgcn_sched_barrier(0);
@@ -1086,11 +1088,207 @@ struct PairWave {
         }
         rescale_if(0, row_max(s0, scale_log2, x0));
         rescale_if(1, row_max(s1, scale_log2, x1));
+        finish_subtile(vf, x0, x1, scale_log2);
+    }
+
+    // P and PV of both heads from masked, rescaled scores x0 / x1.
+    __device__ inline void finish_subtile(const v8 (&vf)[DT], float (&x0)[2][4], float (&x1)[2][4],
+                                          float scale_log2) {
+        u32x4 h0, l0, h1, l1;
         probs(0, x0, scale_log2, h0, l0);
         __builtin_amdgcn_sched_barrier(0);
         pv0_probs1(vf, h0, l0, x1, scale_log2, h1, l1);
         __builtin_amdgcn_sched_barrier(0);
         pv(1, vf, h1, l1);
+    }
+
+    // ---- Software-pipelined stage (one key class: the wave walks every
+    // sub-tile of the stage). Sub-tile j's work is split so that the MFMAs of
+    // one part issue beside the vector-ALU work of another:
+    //   A: P of sub-tile j (both heads)       with the QK MFMAs of sub-tile j + 1
+    //   B: PV of sub-tile j (and row sums)    with the row maxima of sub-tile j + 1
+    //   C: the lazy rescale for sub-tile j + 1 (rare)
+    // Every operation, operand and per-accumulator order is that of step():
+    // the results are bit-identical, only independent instructions move.
+
+    // scaled row maximum of one head's scores (the value row_max returns)
+    __device__ static inline float scaled_max(const f32x4 (&st)[2], float scale_log2) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[kt][i]);
+        return mx * scale_log2;
+    }
+
+    // V^T fragment of d tile dt (one tile of read_v).
+    __device__ inline v8 read_v_tile(const char* Vs, int dt) {
+        const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vs + voff[dt]));
+        const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vs + voff[dt] + 16 * D * 2));
+        return __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+
+    // K fragment f of the sub-tile at Ks: k-step f / 2, key tile f % 2 (read_k's kf[f / 2][f % 2]).
+    __device__ inline v8 read_k_frag(const char* Ks, int f) {
+        return __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(Ks + koff[f >> 1] + 16 * (f & 1) * D * 2));
+    }
+
+    // A: probabilities of both heads from scores c0 / c1 (maxima applied), each
+    // computed before one QK MFMA of the next sub-tile (K tiles at Ks1) into
+    // n0 / n1. The MFMAs go by K fragment, both heads in turn; fragments are
+    // read three ahead, each freed after its second MFMA.
+    __device__ inline void probs_qk(const f32x4 (&c0)[2], const f32x4 (&c1)[2], const char* Ks1, f32x4 (&n0)[2],
+                                    f32x4 (&n1)[2], float scale_log2, u32x4& h0, u32x4& l0, u32x4& h1, u32x4& l1) {
+        static_assert(DS == 4, "head_dim 128");
+        constexpr int kAhead = 3;
+        const float m0 = (m_run[0] == -INFINITY) ? 0.f : m_run[0];
+        const float m1 = (m_run[1] == -INFINITY) ? 0.f : m_run[1];
+        float p[16];
+        uint32_t hv[8], lv[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        v8 kf[2 * DS];
+#pragma unroll
+        for (int f = 0; f < kAhead; ++f) kf[f] = read_k_frag(Ks1, f);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) n0[kt] = n1[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            // probability i: head i / 8, key 16 kt + 4 lj + e with (kt, e) = divmod(i % 8, 4)
+            const int e = i & 7;
+            const float s = i < 8 ? c0[e >> 2][e & 3] : c1[e >> 2][e & 3];
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s, scale_log2, -(i < 8 ? m0 : m1)));
+            if (i & 1) {
+                pack(p[i - 1], p[i], hv[i >> 1], lv[i >> 1]);
+                // pinned here: otherwise the compiler sinks the probabilities
+                // to their first use in part B, past every QK MFMA
+                asm volatile("" : "+v"(hv[i >> 1]), "+v"(lv[i >> 1]));
+            }
+            // QK MFMA i: K fragment i / 2 (k-step i / 4, key tile (i / 2) % 2), head i % 2
+            // (per accumulator the k-steps go in qk()'s order)
+            const int f = i >> 1, ds = i >> 2, kt = f & 1;
+            if (i & 1) {
+                n1[kt] = M::mma(kf[f], qf[1][ds], n1[kt]);
+                if (f + kAhead < 2 * DS) kf[f + kAhead] = read_k_frag(Ks1, f + kAhead);
+            } else {
+                n0[kt] = M::mma(kf[f], qf[0][ds], n0[kt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        h0 = u32x4{hv[0], hv[1], hv[2], hv[3]};
+        l0 = u32x4{lv[0], lv[1], lv[2], lv[3]};
+        h1 = u32x4{hv[4], hv[5], hv[6], hv[7]};
+        l1 = u32x4{lv[4], lv[5], lv[6], lv[7]};
+    }
+
+    // B: PV of both heads by d tile (V^T fragments read three tiles ahead from
+    // Vs, each freed after its two heads' MFMAs), then the row sums; the next
+    // sub-tile's scaled row maxima (n0 / n1, masked beforehand where needed)
+    // are computed between the MFMAs.
+    __device__ inline void pv_max(const char* Vs, const u32x4& h0, const u32x4& l0, const u32x4& h1,
+                                  const u32x4& l1, const f32x4 (&n0)[2], const f32x4 (&n1)[2], float scale_log2,
+                                  float (&mx)[2]) {
+        constexpr int kAhead = 3;
+        const v8 b[2][2] = {{__builtin_bit_cast(v8, h0), __builtin_bit_cast(v8, l0)},
+                            {__builtin_bit_cast(v8, h1), __builtin_bit_cast(v8, l1)}};
+        v8 vf[DT];
+#pragma unroll
+        for (int dt = 0; dt < kAhead; ++dt) vf[dt] = read_v_tile(Vs, dt);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            if (dt + kAhead < DT) vf[dt + kAhead] = read_v_tile(Vs, dt + kAhead);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                o[t][dt] = M::mma(vf[dt], b[t][0], o[t][dt]);
+                if (HILO) o[t][dt] = M::mma(vf[dt], b[t][1], o[t][dt]);
+            }
+            if (dt == 1) {
+                mx[0] = scaled_max(n0, scale_log2);
+                asm volatile("" : "+v"(mx[0]));  // pinned between the MFMAs
+            }
+            if (dt == 3) {
+                mx[1] = scaled_max(n1, scale_log2);
+                asm volatile("" : "+v"(mx[1]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            lsum[t] = M::mma(ones, b[t][0], lsum[t]);
+            if (HILO) lsum[t] = M::mma(ones, b[t][1], lsum[t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Mask (where a key can lie past a row's last visible key) and lazy rescale
+    // of the scores of the sub-tile starting at key0, outside the pipelined parts.
+    __device__ inline void mask_rescale(f32x4 (&s0)[2], f32x4 (&s1)[2], bool mask, int32_t key0, int lj,
+                                        int32_t last, float scale_log2) {
+        if (mask) {
+            apply_mask_at(s0, key0, lj, last);
+            apply_mask_at(s1, key0, lj, last);
+        }
+        rescale_if(0, scaled_max(s0, scale_log2));
+        rescale_if(1, scaled_max(s1, scale_log2));
+    }
+
+    // Sub-tile J of a stage (scores of J in c0 / c1, next scores into n0 / n1).
+    template <int J>
+    __device__ inline void pipelined_subtile(const char* Ks, const char* Vs, int32_t key0, int32_t mask_from,
+                                             int32_t last, int lj, float scale_log2, f32x4 (&c0)[2],
+                                             f32x4 (&c1)[2], f32x4 (&n0)[2], f32x4 (&n1)[2]) {
+        if (J + 1 < kPairSubs) {
+            const int32_t key1 = key0 + kPairSub * (J + 1);
+            u32x4 h0, l0, h1, l1;
+            probs_qk(c0, c1, Ks + kPairSub * (J + 1) * D * 2, n0, n1, scale_log2, h0, l0, h1, l1);
+            if (key1 + kPairSub > mask_from) {
+                apply_mask_at(n0, key1, lj, last);
+                apply_mask_at(n1, key1, lj, last);
+            }
+            float mx[2];
+            pv_max(Vs + kPairSub * J * D * 2, h0, l0, h1, l1, n0, n1, scale_log2, mx);
+            rescale_if(0, mx[0]);
+            rescale_if(1, mx[1]);
+        } else {
+            v8 vf[DT];
+            read_v(Vs + kPairSub * J * D * 2, vf);
+            __builtin_amdgcn_sched_barrier(0);
+            float x0[2][4], x1[2][4];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x0[kt][i] = c0[kt][i];
+                    x1[kt][i] = c1[kt][i];
+                }
+            finish_subtile(vf, x0, x1, scale_log2);
+        }
+    }
+
+    // All kPairSubs sub-tiles of a staged step, straight-line code (the
+    // accumulators stay in their registers): Ks / Vs its K and V tiles, key0
+    // the first sub-tile's first key. `last` is this lane's last visible key
+    // (its row's position, and before the chunk's end); keys below mask_from
+    // are visible to every row of the tile. Sub-tiles past the chunk's end or
+    // the tile's causal limit are masked whole: their probabilities are 0 and
+    // they add exact zeros (V rows past the chunk's end are zeroed in LDS).
+    __device__ inline void stage_pipelined(const char* Ks, const char* Vs, int32_t key0, int32_t mask_from,
+                                           int32_t last, int lj, float scale_log2) {
+        static_assert(kPairSubs == 4, "four sub-tiles per stage");
+        f32x4 sa0[2], sa1[2], sb0[2], sb1[2];
+        {
+            v8 kf[DS][2];
+            read_k(Ks, kf);
+            __builtin_amdgcn_sched_barrier(0);
+            qk(0, kf, sa0);
+            qk(1, kf, sa1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        mask_rescale(sa0, sa1, key0 + kPairSub > mask_from, key0, lj, last, scale_log2);
+        pipelined_subtile<0>(Ks, Vs, key0, mask_from, last, lj, scale_log2, sa0, sa1, sb0, sb1);
+        pipelined_subtile<1>(Ks, Vs, key0, mask_from, last, lj, scale_log2, sb0, sb1, sa0, sa1);
+        pipelined_subtile<2>(Ks, Vs, key0, mask_from, last, lj, scale_log2, sa0, sa1, sb0, sb1);
+        pipelined_subtile<3>(Ks, Vs, key0, mask_from, last, lj, scale_log2, sb0, sb1, sa0, sa1);
     }
 };
 
@@ -1182,8 +1380,11 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
 #pragma unroll
             for (int ds = 0; ds < W::DS; ++ds) asm volatile("" : "+v"(raw[t][ds]));
         const bool live_row = row < a.n_sel;
-        kmax = row0 < a.n_sel ? kmax_raw + 1 : 0;
-        nomask_end = (row0 + kRowTile <= a.n_sel) ? first_raw + 1 : 0;
+        // the tile's limits are the same in every lane (each lane loaded the
+        // same two positions): held in scalar registers, the loop's sub-tile
+        // counts and mask tests are scalar branches
+        kmax = __builtin_amdgcn_readfirstlane(row0 < a.n_sel ? kmax_raw + 1 : 0);
+        nomask_end = __builtin_amdgcn_readfirstlane((row0 + kRowTile <= a.n_sel) ? first_raw + 1 : 0);
         w.pos = live_row ? pos_raw : -1;
         w.init(lq, lj);
 #pragma unroll
@@ -1210,13 +1411,22 @@ __global__ void __launch_bounds__(kPairThreads) attn_pair_kernel(AttnArgs a) {
         if (i + 1 < n_it) load(i + 1, smem + ((i + 1) & 1) * C::stage_bytes);
         const char* Ks = stage;
         const char* Vs = stage + C::tensor_bytes;
+        if constexpr (X == 1 && D == 128) {
+            // every sub-tile of the step, software-pipelined, when any of them
+            // lies inside the chunk and starts below the tile's causal limit
+            const int32_t key0 = key_begin + kPairStepKeys * i;
+            if (key0 < kmax)
+                w.stage_pipelined(Ks, Vs, key0, min(nomask_end, key_end), min(w.pos, key_end - 1), lj,
+                                  a.scale_log2);
+        } else {
 #pragma unroll 1
-        for (int j = kq; j < kPairSubs; j += X) {
-            const int s = kPairSubs * i + j;
-            const int32_t key0 = key_begin + kPairSub * s;
-            if (s < n_sub && key0 < kmax)
-                w.step(Ks + kPairSub * j * D * 2, Vs + kPairSub * j * D * 2, key0 + kPairSub > nomask_end, key0, lj,
-                       a.scale_log2);
+            for (int j = kq; j < kPairSubs; j += X) {
+                const int s = kPairSubs * i + j;
+                const int32_t key0 = key_begin + kPairSub * s;
+                if (s < n_sub && key0 < kmax)
+                    w.step(Ks + kPairSub * j * D * 2, Vs + kPairSub * j * D * 2, key0 + kPairSub > nomask_end, key0,
+                           lj, a.scale_log2);
+            }
         }
     }
     pair_finish<T, D, RT, HILO>(a, w, smem, hp, rt, kq, lane, lq, lj, work, n_chunks, head0, row0, kmax, key_begin);
