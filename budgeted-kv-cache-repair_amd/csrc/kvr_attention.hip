@@ -875,6 +875,10 @@ struct PairWave {
     f32x4 o[2][DT];
     f32x4 lsum[2];    // row sums of P as a 17th output tile: row 0 of O^T += ones . P^T
     float m_run[2];
+    // kept with m_run, so the per-sub-tile work does not recompute them: the
+    // exponent offset -(m_run, or 0 while m_run = -inf) and the lazy-rescale
+    // threshold m_run + kLazyLog2
+    float m_neg[2], m_thr[2];
     int32_t pos;      // this lane's row position; -1 past the selected rows
     v8 ones;          // A operand of the row-sum tile: row 0 all ones, rows 1..15 zero
     // Per-lane byte offsets of this lane's fragment reads within a staged tile,
@@ -897,6 +901,8 @@ struct PairWave {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             m_run[t] = -INFINITY;
+            m_neg[t] = -0.f;
+            m_thr[t] = -INFINITY + kLazyLog2;
             lsum[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -964,13 +970,15 @@ struct PairWave {
     // exceeds it by more than kLazyLog2 (so p <= 2^8 and the fp32 accumulators
     // cannot overflow); O and the row sums are rescaled then (rare).
     __device__ inline void rescale_if(int t, float mx) {
-        if (__any(mx > m_run[t] + kLazyLog2)) {
+        if (__any(mx > m_thr[t])) {
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = (mx > m_run[t] + kLazyLog2) ? mx : m_run[t];
+            const float m_new = (mx > m_thr[t]) ? mx : m_run[t];
             // 1 if unmoved, 0 from -inf; a row with no visible key keeps m = -inf
             const float alpha = __builtin_amdgcn_exp2f(m_run[t] - (m_new == -INFINITY ? 0.f : m_new));
             m_run[t] = m_new;
+            m_neg[t] = -(m_new == -INFINITY ? 0.f : m_new);
+            m_thr[t] = m_new + kLazyLog2;
             lsum[t] *= alpha;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[t][dt] *= alpha;
@@ -988,11 +996,10 @@ struct PairWave {
     // P = exp2(scale x - m) of head t as the B operand(s) of the PV MFMA:
     // element 4h + i of lane (lq, lj) is key 16h + 4 lj + i.
     __device__ inline void probs(int t, float (&x)[2][4], float scale_log2, u32x4& phi, u32x4& plo) {
-        const float m_use = (m_run[t] == -INFINITY) ? 0.f : m_run[t];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], scale_log2, -m_use));
+            for (int i = 0; i < 4; ++i) x[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], scale_log2, m_neg[t]));
         uint32_t hv[4], lv[4] = {0u, 0u, 0u, 0u};
         pack(x[0][0], x[0][1], hv[0], lv[0]);
         pack(x[0][2], x[0][3], hv[1], lv[1]);
@@ -1031,7 +1038,6 @@ struct PairWave {
     __device__ inline void pv0_probs1(const v8 (&vf)[DT], const u32x4& h0, const u32x4& l0, float (&x1)[2][4],
                                       float scale_log2, u32x4& h1, u32x4& l1) {
         const v8 bh = __builtin_bit_cast(v8, h0), bl = __builtin_bit_cast(v8, l0);
-        const float m_use = (m_run[1] == -INFINITY) ? 0.f : m_run[1];
         float p[8];
         uint32_t hv[4], lv[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -1039,7 +1045,7 @@ struct PairWave {
             o[0][dt] = M::mma(vf[dt], bh, o[0][dt]);
             if (HILO) o[0][dt] = M::mma(vf[dt], bl, o[0][dt]);
             if (dt < 8) {
-                p[dt] = __builtin_amdgcn_exp2f(__builtin_fmaf(x1[dt >> 2][dt & 3], scale_log2, -m_use));
+                p[dt] = __builtin_amdgcn_exp2f(__builtin_fmaf(x1[dt >> 2][dt & 3], scale_log2, m_neg[1]));
                 if (dt & 1) pack(p[dt - 1], p[dt], hv[dt >> 1], lv[dt >> 1]);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -1047,7 +1053,7 @@ struct PairWave {
         if (DT < 8) {  // head_dim 64: the remaining probabilities
 #pragma unroll
             for (int e = DT; e < 8; ++e) {
-                p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x1[e >> 2][e & 3], scale_log2, -m_use));
+                p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x1[e >> 2][e & 3], scale_log2, m_neg[1]));
                 if (e & 1) pack(p[e - 1], p[e], hv[e >> 1], lv[e >> 1]);
             }
         }
@@ -1141,8 +1147,6 @@ struct PairWave {
                                     f32x4 (&n1)[2], float scale_log2, u32x4& h0, u32x4& l0, u32x4& h1, u32x4& l1) {
         static_assert(DS == 4, "head_dim 128");
         constexpr int kAhead = 3;
-        const float m0 = (m_run[0] == -INFINITY) ? 0.f : m_run[0];
-        const float m1 = (m_run[1] == -INFINITY) ? 0.f : m_run[1];
         float p[16];
         uint32_t hv[8], lv[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
         v8 kf[2 * DS];
@@ -1156,12 +1160,16 @@ struct PairWave {
             // probability i: head i / 8, key 16 kt + 4 lj + e with (kt, e) = divmod(i % 8, 4)
             const int e = i & 7;
             const float s = i < 8 ? c0[e >> 2][e & 3] : c1[e >> 2][e & 3];
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s, scale_log2, -(i < 8 ? m0 : m1)));
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s, scale_log2, m_neg[i >> 3]));
             if (i & 1) {
                 pack(p[i - 1], p[i], hv[i >> 1], lv[i >> 1]);
                 // pinned here: otherwise the compiler sinks the probabilities
-                // to their first use in part B, past every QK MFMA
-                asm volatile("" : "+v"(hv[i >> 1]), "+v"(lv[i >> 1]));
+                // to their first use in part B, past every QK MFMA (the lo
+                // halves only where they exist: a pinned constant 0 costs a move)
+                if (HILO)
+                    asm volatile("" : "+v"(hv[i >> 1]), "+v"(lv[i >> 1]));
+                else
+                    asm volatile("" : "+v"(hv[i >> 1]));
             }
             // QK MFMA i: K fragment i / 2 (k-step i / 4, key tile (i / 2) % 2), head i % 2
             // (per accumulator the k-steps go in qk()'s order)
