@@ -1,5 +1,7 @@
 """Build libkvrepair.so (gfx950 HIP kernels + C ABI) in-tree with hipcc, and the
-host-side CPython extension _kvr_walk (the executor's module-tree walk) with gcc.
+host-side CPython extensions _kvr_walk (the executor's module-tree walk, C) with
+gcc and _kvr_layout (a cache's per-layer K/V layout and addresses, C++ on torch's
+tensor headers) with g++.
 
 The library links the HIP runtime by SONAME (libamdhip64.so.7). It must be
 loaded after ``import torch`` so that the dynamic linker binds it to the
@@ -21,6 +23,8 @@ INCLUDE = REPO_ROOT / "include"
 OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / "libkvrepair.so"
 WALK_SOURCE = CSRC / "kvr_module_walk.c"
 WALK_OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / ("_kvr_walk" + sysconfig.get_config_var("EXT_SUFFIX"))
+LAYOUT_SOURCE = CSRC / "kvr_tensor_layout.cpp"
+LAYOUT_OUTPUT = PACKAGE_ROOT / "kv_cache_repair_amd" / ("_kvr_layout" + sysconfig.get_config_var("EXT_SUFFIX"))
 SOURCES = ("kvr_common.hip", "kvr_rotate.hip", "kvr_scatter.hip", "kvr_fresh.hip", "kvr_layer.hip", "kvr_gemm.hip", "kvr_attention.hip", "kvr_decoder.hip", "kvr_writeback.hip", "kvr_inputs.hip", "kvr_scoring.hip")
 ARCH = "gfx950"
 
@@ -70,10 +74,38 @@ def build_walk(verbose: bool = False) -> Path:
     return WALK_OUTPUT
 
 
+def build_layout(verbose: bool = False) -> subprocess.Popen:
+    """Start compiling the _kvr_layout extension (C++ against the installed
+    torch's headers and libraries, its C++ ABI); returns the running compiler,
+    whose output replaces LAYOUT_OUTPUT once finish_layout() sees it succeed."""
+    import torch
+
+    root = Path(torch.__file__).resolve().parent
+    lib = root / "lib"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-shared", "-fPIC", "-std=c++17", "-Wall", "-Werror",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           f"-I{root / 'include'}", f"-I{root / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+           f"-I{sysconfig.get_paths()['include']}", str(LAYOUT_SOURCE),
+           "-o", str(LAYOUT_OUTPUT.with_name(LAYOUT_OUTPUT.name + ".tmp")),
+           f"-L{lib}", "-lc10", "-ltorch_cpu", "-ltorch_python", f"-Wl,-rpath,{lib}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def finish_layout(proc: subprocess.Popen) -> Path:
+    out, _ = proc.communicate()
+    if proc.returncode != 0:
+        raise RuntimeError("g++ failed for _kvr_layout:\n" + out)
+    os.replace(LAYOUT_OUTPUT.with_name(LAYOUT_OUTPUT.name + ".tmp"), LAYOUT_OUTPUT)
+    return LAYOUT_OUTPUT
+
+
 def build(verbose: bool = False, jobs: int = 4) -> Path:
-    """Compile every HIP source and link the shared library, then the _kvr_walk
-    extension; returns the library's path."""
+    """Compile the host extensions and every HIP source and link the shared
+    library; returns the library's path."""
     build_walk(verbose)
+    layout = build_layout(verbose)  # compiles while the HIP sources do
     build_dir = PACKAGE_ROOT / "_build"
     defines = _defines()
     build_dir.mkdir(exist_ok=True)
@@ -105,6 +137,7 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
     if result.returncode != 0:
         raise RuntimeError("hipcc link failed:\n" + result.stdout)
     os.replace(tmp, OUTPUT)
+    finish_layout(layout)
     return OUTPUT
 
 

@@ -20,7 +20,7 @@ from transformers.cache_utils import DynamicCache, DynamicLayer
 
 from . import _native
 from .alignment import token_alignment, token_alignment_host
-from .kernels.executor import layer_kv
+from .kernels.executor import layer_kv, tensor_layout
 
 
 class OperatorShim:
@@ -206,6 +206,23 @@ def run_tokens_from_prefix(model: Any, prefix_cache: Any, input_ids: torch.Tenso
                 return_dict=True).past_key_values
 
 
+def _layer_addresses(cache: Any, what: str):
+    """(first K tensor, K address array, V address array) of every cache layer,
+    after _check_uniform's checks. The layout and addresses of all layers are
+    read in one _kvr_layout pass; a cache that is not one uniform GPU layout
+    takes _check_uniform's per-tensor path (same errors)."""
+    k_bytes, v_bytes, first, uniform = tensor_layout().kv_layers(cache.layers)
+    if not (uniform and first.ndim == 4 and first.shape[0] == 1 and first.get_device() >= 0
+            and all(s > 0 for s in first.stride())):
+        pairs = [layer_kv(cache, i) for i in range(len(cache.layers))]
+        _check_uniform(pairs, what)
+        return pairs[0][0], _native.ptr_array(k for k, _ in pairs), _native.ptr_array(v for _, v in pairs)
+    _require_device(first, what)
+    count = len(k_bytes) // 8
+    return (first, (ctypes.c_void_p * count).from_buffer_copy(k_bytes),
+            (ctypes.c_void_p * count).from_buffer_copy(v_bytes))
+
+
 def _host_id_rows(old_input_ids: torch.Tensor, new_input_ids: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
     """Both id rows as int64 host arrays: CPU tensors are read in place (no copy,
     no device synchronisation, as the API layer holds its tokenizer ids); device
@@ -233,10 +250,8 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     per-layer tensor views are made after it, while the GPU runs.
     """
     n_new = int(new_input_ids.shape[1])
-    old = [layer_kv(old_cache, i) for i in range(len(old_cache.layers))]
-    _check_uniform(old, "build_halo_cache")
+    k0, old_k, old_v = _layer_addresses(old_cache, "build_halo_cache")
     generator = getattr(model, "generator", model)
-    k0 = old[0][0]
     old_np, new_np = _host_id_rows(old_input_ids, new_input_ids)
     # the refresh and any boundary recomputation gather embedding rows by these
     # ids on the GPU: out-of-range ids are refused here, before any launch
@@ -246,7 +261,7 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
     old_tail_start = align["old_suffix_start"] + halo
     tail_rows = align["suffix"] - halo
     inv_freq, scaling, rotary_dim = _rotary(generator, k0.device)
-    layers, heads, dim = len(old), int(k0.shape[1]), int(k0.shape[3])
+    layers, heads, dim = len(old_k), int(k0.shape[1]), int(k0.shape[3])
     # one allocation for every layer's K and V; layer l's K is block 2 l, its V block 2 l + 1
     slab = torch.empty((layers, 2, 1, heads, n_new, dim), dtype=k0.dtype, device=k0.device)
     if recompute_end == align["prefix"]:
@@ -257,7 +272,7 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
             new_k = (ctypes.c_void_p * layers)(*range(base, base + 2 * layers * block, 2 * block))
             new_v = (ctypes.c_void_p * layers)(*range(base + block, base + 2 * layers * block, 2 * block))
             status = _native.lib().kvr_shift_cache_build(
-                _native.ptr_array(k for k, _ in old), _native.ptr_array(v for _, v in old), new_k, new_v, layers,
+                old_k, old_v, new_k, new_v, layers,
                 heads, dim, int(rotary_dim), _native.i64_array(_native.strides3(k0)),
                 _native.i64_array((n_new * dim, dim, 1)), align["prefix"], old_tail_start, recompute_end, tail_rows,
                 align["position_shift"], inv_freq.data_ptr(), float(scaling), _native.DTYPE_CODES[k0.dtype],
@@ -271,7 +286,8 @@ def build_halo_cache(model: Any, old_cache: Any, old_input_ids: torch.Tensor, ne
         recomputed = run_tokens_from_prefix(generator, prefix_cache,
                                             new_input_ids[:, align["prefix"]:recompute_end].to(k0.device),
                                             recompute_end)
-        rec = [layer_kv(recomputed, i) for i in range(len(old))]
+        old = [layer_kv(old_cache, i) for i in range(layers)]
+        rec = [layer_kv(recomputed, i) for i in range(layers)]
         _check_uniform(rec, "build_halo_cache")
         _shift_rows([k for k, _ in rec], [v for _, v in rec], new_k, new_v,
                     prefix_rows=recompute_end, old_tail_start=0, new_tail_start=recompute_end, tail_rows=0, shift=0,

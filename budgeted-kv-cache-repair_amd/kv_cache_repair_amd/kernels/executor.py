@@ -19,6 +19,29 @@ def layer_kv(cache: Any, index: int):
     return layer.keys, layer.values
 
 
+def tensor_layout():
+    """The _kvr_layout extension (built in-tree with libkvrepair.so): every
+    cache layer's K/V layout and addresses in one pass over torch's tensor
+    metadata. No Python fallback: a missing build raises here."""
+    try:
+        from .. import _kvr_layout
+    except ImportError as error:
+        raise ImportError("kv_cache_repair_amd._kvr_layout is not built: run build_lib.py (or "
+                          "__graft_entry__.build())") from error
+    return _kvr_layout
+
+
+def uniform_layers(layers):
+    """(K address bytes, V address bytes, first K) when every layer's K and V are
+    tensors of one layout (shape, strides, dtype, device), else None; a layer
+    without .keys / .values gives None too."""
+    try:
+        k_raw, v_raw, first, uniform = tensor_layout().kv_layers(layers)
+    except AttributeError:
+        return None
+    return (k_raw, v_raw, first) if uniform else None
+
+
 def _validate_cache(cache: Any, logical_length: int) -> int:
     layers = getattr(cache, "layers", None)
     if layers is None:
@@ -26,8 +49,15 @@ def _validate_cache(cache: Any, logical_length: int) -> int:
     layer_count = len(layers)
     if layer_count == 0:
         raise ValueError("base_cache must contain at least one K/V layer")
-    # Fast path: every layer's K and V share one shape, dtype and GPU that
-    # satisfy the per-layer checks below; otherwise those checks name the layer.
+    # Fast paths: every layer's K and V share one layout (read in one pass), or
+    # one shape, dtype and GPU, that satisfies the per-layer checks below;
+    # otherwise those checks name the layer.
+    same = uniform_layers(layers)
+    if same is not None:
+        first = same[2]
+        if (first.ndim == 4 and first.get_device() >= 0 and first.shape[0] == 1 and first.shape[2] == logical_length
+                and first.shape[1] > 0 and first.shape[3] > 0 and first.is_floating_point()):
+            return layer_count
     try:
         tensors = [t for entry in layers for t in (entry.keys, entry.values)]
     except AttributeError:

@@ -33,7 +33,7 @@ from transformers.cache_utils import Cache, DynamicLayer
 
 from .. import _native
 from . import projection as _projection
-from .executor import _validate_cache, _validate_intervals, layer_kv
+from .executor import _validate_cache, _validate_intervals, layer_kv, uniform_layers
 from .indexed_attention import IndexedPlan, DeviceIndexedPlan, _require_gfx950
 
 _ATTENTION_NAME = "kvr_hip_packed_absolute_attention_v1"
@@ -612,7 +612,9 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
         raise ValueError("packed HIP executor requires one ROCm GPU device")
     if off_device:
         raise ValueError("packed executor requires all model parameters on the request device")
-    if True in [t.get_device() != index for i in range(len(base_cache.layers)) for t in layer_kv(base_cache, i)]:
+    same = uniform_layers(base_cache.layers)  # one layout: one device for every layer
+    if (same is None or same[2].get_device() != index) and True in [
+            t.get_device() != index for i in range(len(base_cache.layers)) for t in layer_kv(base_cache, i)]:
         raise ValueError("packed executor requires all cache layers on the request device")
     _require_gfx950(device)
     with _PLAN_LOCK:
@@ -810,6 +812,13 @@ def _native_layer_descs(plans, output, layer_count):
     # the per-layer cache fields through one int64 view of the descriptor array
     words = np.frombuffer(descs, dtype=np.int64).reshape(layer_count, -1)
     layers = output.layers
+    same = uniform_layers(layers)
+    if same is not None and len(same[0]) == 8 * layer_count:  # one layout: addresses from one pass, shared strides
+        k_raw, v_raw, first = same
+        words[:, _DESC_K] = np.frombuffer(k_raw, dtype=np.int64)
+        words[:, _DESC_V] = np.frombuffer(v_raw, dtype=np.int64)
+        words[:, _DESC_STRIDES:_DESC_STRIDES + 6] = first.stride()[1:] * 2
+        return descs
     words[:, _DESC_K] = [layer.keys.data_ptr() for layer in layers]
     words[:, _DESC_V] = [layer.values.data_ptr() for layer in layers]
     words[:, _DESC_STRIDES:_DESC_STRIDES + 6] = [layer.keys.stride()[1:] + layer.values.stride()[1:] for layer in layers]

@@ -640,3 +640,36 @@ def test_native_layer_call_is_bit_identical_to_dispatched_fused_layers(gpu_devic
         pc.packed_interval_repair(shim, base, edited, intervals, native_layers=True, fused_projections=False)
     with pytest.raises(ValueError, match="native_layers"):  # more rows than one projection launch serves
         pc.packed_interval_repair(shim, base, edited, [(0, 65)], native_layers=True)
+
+
+def test_cache_layer_off_the_request_device_is_refused(gpu_device):
+    """One layer's K and V on the host: the one-pass layout read sees two devices
+    and the per-layer device check names the problem before any launch."""
+    from kv_cache_repair_amd.kernels.packed_cache import packed_interval_repair
+
+    model = make_model(gpu_device, layers=3)
+    shim, ids, base = make_request(model)
+    base.layers[1].keys, base.layers[1].values = base.layers[1].keys.cpu(), base.layers[1].values.cpu()
+    with pytest.raises(ValueError, match="cache layers on the request device"):
+        packed_interval_repair(shim, base, ids + 13, [(3, 5), (8, 10)])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_owned_refresh_with_one_layer_at_other_strides_matches_uniform_layout(gpu_device, dtype):
+    """A cache whose layers do not share one layout takes the per-tensor reads
+    (validation, device check, per-layer descriptors): same bits as the same
+    values in one uniform layout."""
+    from kv_cache_repair_amd.kernels.packed_cache import packed_refresh_owned_
+
+    model = make_model(gpu_device, layers=3, dtype=dtype)
+    shim, ids, base = make_request(model)
+    uniform, mixed = ref.clone_cache(base), ref.clone_cache(base)
+    layer = mixed.layers[1]
+    layer.keys = layer.keys.transpose(1, 2).contiguous().transpose(1, 2)  # token-major storage, same values
+    layer.values = layer.values.transpose(1, 2).contiguous().transpose(1, 2)
+    assert layer.keys.stride() != uniform.layers[1].keys.stride()
+    intervals = [(0, 1), (3, 5), (8, 10)]
+    packed_refresh_owned_(shim, uniform, ids + 13, intervals)
+    packed_refresh_owned_(shim, mixed, ids + 13, intervals)
+    for a, b in zip(uniform.layers, mixed.layers):
+        assert bits_equal(a.keys, b.keys) and bits_equal(a.values, b.values)
