@@ -33,7 +33,7 @@ from transformers.cache_utils import Cache, DynamicLayer
 
 from .. import _native
 from . import projection as _projection
-from .executor import _validate_cache, _validate_intervals, layer_kv, uniform_layers
+from .executor import _validate_cache, _validate_intervals, layer_kv, tensor_layout, uniform_layers
 from .indexed_attention import IndexedPlan, DeviceIndexedPlan, _require_gfx950
 
 _ATTENTION_NAME = "kvr_hip_packed_absolute_attention_v1"
@@ -567,7 +567,7 @@ def _qualify(shim, edited_ids, base_cache, attention_backend, writeback_backend)
     # -1 off the GPUs, and the request device is a GPU when it matters below).
     index = device.index if device.type == "cuda" else -2
     training, overridden, hooked, forward_hooked, params, dict_ids, param_ids, ptrs = \
-        _module_walk().qualify_walk(model, base, torch.Tensor.data_ptr)
+        _module_walk().qualify_walk(model, base, tensor_layout().data_ptr)
     from torch.nn.modules import module as _module
 
     forward_hooked = (forward_hooked or bool(_module._global_forward_hooks)

@@ -141,3 +141,18 @@ def test_walk_raises_like_the_dict_lookups_it_replaces():
         python_walk(model, model.model)
     with pytest.raises(KeyError):
         c_walk(model, model.model)
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen3"])
+def test_walk_with_the_layout_extensions_address_reader_matches(family):
+    """The qualification passes the layout extension's data_ptr builtin as the
+    walk's address reader: same walk result as with torch.Tensor.data_ptr."""
+    from kv_cache_repair_amd.kernels.executor import tensor_layout
+
+    model = tiny(family)
+    base = model.model
+    model.lm_head.weight = base.embed_tokens.weight  # one tensor in two slots
+    with_method = pc._module_walk().qualify_walk(model, base, torch.Tensor.data_ptr)
+    with_builtin = pc._module_walk().qualify_walk(model, base, tensor_layout().data_ptr)
+    assert with_builtin[:4] == with_method[:4] and with_builtin[5:] == with_method[5:]
+    assert all(a is b for a, b in zip(with_builtin[4], with_method[4]))

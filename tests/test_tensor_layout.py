@@ -141,3 +141,18 @@ def test_validate_cache_fast_path_accepts_and_refuses_as_the_per_layer_checks(mo
     pairs[2] = (pairs[2][0], pairs[2][1].float())
     with pytest.raises(ValueError, match="geometry, dtype, and device must agree"):
         _validate_cache(cache_of(pairs), 7)
+
+
+def test_data_ptr_builtin_equals_the_tensor_method():
+    """The module walk's address reader (a builtin of the layout extension)
+    gives what torch.Tensor.data_ptr gives, for every kind of tensor a model
+    holds, and refuses anything else."""
+    data_ptr = tensor_layout().data_ptr
+    base = torch.randn(6, 8)
+    cases = [base, base[2:], base.t(), base[:, 3], torch.empty(0), torch.nn.Parameter(torch.zeros(3)),
+             torch.zeros(2, 2, dtype=torch.bfloat16), torch.empty(4, device="meta")]
+    for t in cases:
+        assert data_ptr(t) == torch.Tensor.data_ptr(t)
+    for bad in (None, 3, [base]):
+        with pytest.raises(TypeError, match="expected a tensor"):
+            data_ptr(bad)
