@@ -117,7 +117,8 @@ PyObject* data_ptr(PyObject*, PyObject* obj) {
         return nullptr;
     }
     try {
-        return PyLong_FromVoidPtr(THPVariable_Unpack(obj).data_ptr());
+        // the read-only address: never materialises a copy-on-write storage
+        return PyLong_FromVoidPtr(const_cast<void*>(THPVariable_Unpack(obj).const_data_ptr()));
     } catch (const std::exception& error) {
         PyErr_SetString(PyExc_RuntimeError, error.what());
         return nullptr;
