@@ -49,7 +49,7 @@ def hipcc() -> str:
 
 def _defines() -> list[str]:
     """-D options from the environment: KVR_ATTN_SCRATCH_MB sizes the static
-    device array of kvr_packed_causal_attention_noalloc (MiB, default 64),
+    device array of kvr_packed_causal_attention_noalloc (MiB, default 128),
     which every GPU the library's code object loads on holds."""
     mb = os.environ.get("KVR_ATTN_SCRATCH_MB")
     if mb is None:

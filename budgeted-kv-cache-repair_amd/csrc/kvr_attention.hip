@@ -2165,10 +2165,10 @@ int64_t schedule_span(const std::vector<GroupKeys>& keys, std::vector<Chunk>& ch
 // device address comes from hipGetSymbolAddress, looked up once per device
 // (with that device current) and kept per device.
 // ---------------------------------------------------------------------------
-// Size in MiB, set at build time with -DKVR_ATTN_SCRATCH_MB=<n> (default 64:
-// every c1-c5 schedule fits; the largest, c4, needs 49 MB).
+// Size in MiB, set at build time with -DKVR_ATTN_SCRATCH_MB=<n> (default 128:
+// every c1-c5 schedule fits; the largest, c4, needs 68 MB).
 #ifndef KVR_ATTN_SCRATCH_MB
-#define KVR_ATTN_SCRATCH_MB 64
+#define KVR_ATTN_SCRATCH_MB 128
 #endif
 static_assert(KVR_ATTN_SCRATCH_MB >= 1 && KVR_ATTN_SCRATCH_MB <= 4096, "KVR_ATTN_SCRATCH_MB out of range");
 constexpr int64_t kScratchBytes = int64_t(KVR_ATTN_SCRATCH_MB) << 20;
@@ -2339,6 +2339,10 @@ extern "C" int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n
         const int64_t max_cost = *std::max_element(group_cost.begin(), group_cost.end());
         // (The head-pair kernel also runs one block per CU in 64-row groups.)
         const bool one_block_per_cu = group_rows == kTileGroupRows || (mfma && qt == 4 && KVR_ATTN_PAIR);
+        // The head-pair kernel walks a chunk in steps of two sub-tiles from its
+        // first key: a boundary after an odd number of sub-tiles would leave a
+        // half-empty step, so inner boundaries close on whole steps.
+        const bool pair_steps = mfma && qt == 4 && KVR_ATTN_PAIR && kPairStepKeys == 2 * kSub;
         // Chunks for a share of `share` blocks per head.
         auto build = [&](int64_t share) {
             auto chunks_of = [&](int64_t g, int64_t cap) {
@@ -2349,22 +2353,32 @@ extern "C" int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n
                 return nc > kMaxChunksPerGroup ? int64_t(kMaxChunksPerGroup) : nc;
             };
             // Per-chunk cost cap: the even share of the total. The tile kernel
-            // (one block per CU) raises it until the groups' rounded-up chunk
-            // counts fit the share too (no extra, partial round of blocks), or
-            // every group is one chunk; the wide kernel runs two blocks per CU.
+            // (one block per CU) raises it to the smallest cap whose rounded-up
+            // chunk counts fit the share too (no extra, partial round of
+            // blocks), or to the largest group cost (every group one chunk); the
+            // count only falls as the cap grows, so a bisection finds it. The
+            // wide kernel runs two blocks per CU.
             int64_t cap = (total + share - 1) / share;
-            while (one_block_per_cu) {
+            auto fits = [&](int64_t c) {
                 int64_t sum = 0;
-                for (int64_t g = 0; g < n_groups; ++g) sum += chunks_of(g, cap);
-                if (sum <= share || cap >= max_cost) break;
-                cap += (cap + 15) / 16;
+                for (int64_t g = 0; g < n_groups; ++g) sum += chunks_of(g, c);
+                return sum <= share;
+            };
+            if (one_block_per_cu && cap < max_cost && !fits(cap)) {
+                int64_t lo = cap, hi = max_cost;  // lo does not fit; hi fits or is the largest group cost
+                while (hi - lo > 1) {
+                    const int64_t mid = lo + (hi - lo) / 2;
+                    (fits(mid) ? hi : lo) = mid;
+                }
+                cap = hi;
             }
             std::vector<Chunk> out;
             for (int64_t g = 0; g < n_groups; ++g) {
                 const int64_t n_sub = (keys[g].kmax + kSub - 1) / kSub;
                 const int64_t nc = chunks_of(g, cap);
                 // Boundary i closes the chunk once the running cost reaches i/nc of
-                // the group's cost, leaving at least one sub-tile per later chunk.
+                // the group's cost (and the chunk is whole steps long, for the
+                // head-pair kernel), leaving at least one sub-tile per later chunk.
                 int64_t s = 0, acc = 0;
                 for (int64_t i = 0; i < nc; ++i) {
                     const int64_t begin = s;
@@ -2375,7 +2389,7 @@ extern "C" int64_t kvr_attention_schedule_ex(const int64_t* positions, int64_t n
                         do {
                             acc += subtile_cost(keys[g], s);
                             ++s;
-                        } while (acc < goal && n_sub - s > nc - 1 - i);
+                        } while ((acc < goal || (pair_steps && ((s - begin) & 1))) && n_sub - s > nc - 1 - i);
                     }
                     const int64_t end = s * kSub < keys[g].kmax ? s * kSub : keys[g].kmax;
                     out.push_back({static_cast<int32_t>(g), static_cast<int32_t>(i),

@@ -483,7 +483,7 @@ int kvr_packed_causal_attention(const void* q, const void* k, const void* v, voi
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same arguments, kernels and results as
  * kvr_packed_causal_attention, without `workspace`: the split-K partials go to
- * a static device array of kvr_attention_scratch_limit() bytes (64 MiB unless
+ * a static device array of kvr_attention_scratch_limit() bytes (128 MiB unless
  * the library is built with -DKVR_ATTN_SCRATCH_MB=<n>) that the library holds
  * on every device where its code object loads, until the process ends. A
  * schedule whose kvr_attention_workspace_bytes exceeds that limit is refused

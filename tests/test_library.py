@@ -216,10 +216,12 @@ def test_default_chunking_keeps_one_block_per_cu_for_the_c3_support():
     assert s[16] == 16 and n_groups == 4  # 64 rows: four 16-row groups for the tile kernel
     assert 24 * 8 <= n_work * 8 <= 256
     # chunks are cost balanced: one row tile per group, so every chunk carries about
-    # the same number of keys (whole 64-key sub-tiles, the group's last one shorter)
+    # the same number of keys; the head-pair kernel steps 128 keys from a chunk's
+    # start, so every chunk but a group's last is whole steps long (the last ends
+    # at the group's causal limit)
     work = [tuple(s[18 + 2 * n_groups + 4 * w:22 + 2 * n_groups + 4 * w]) for w in range(n_work)]
     lengths = [e - b for g, c, b, e in work if c + 1 < s[19 + 2 * g]]  # all but each group's last chunk
-    assert max(lengths) - min(lengths) <= 64
+    assert max(lengths) - min(lengths) <= 128 and all(n % 128 == 0 for n in lengths)
     # a group that fits one block's share is never split
     s = schedule(list(range(15104)), 16128, 32, 8, 128)
     assert s[16] == 64 and s[12] == 0 and s[5] == s[3]
@@ -253,8 +255,17 @@ def test_64_row_schedules_dispatch_longest_groups_first_and_may_take_more_rounds
             assert g not in seen and c == 0
             seen.append(g)
     assert sorted(seen) == list(range(n_groups))
-    longest = [max(e - b for g2, _, b, e in work if g2 == g) for g in seen]
-    assert longest[0] == max(longest)
+    # first the group whose costliest chunk costs most: a 64-key sub-tile costs its
+    # staging (3) plus one per 16-row tile of the group still attending to it
+    positions = c4_positions()
+
+    def cost(g, b, e):
+        limits = [positions[min(64 * g + 16 * t + 15, len(positions) - 1)] + 1
+                  for t in range(4) if 64 * g + 16 * t < len(positions)]
+        return sum(3 + sum(k > 64 * sub for k in limits) for sub in range(b // 64, (e + 63) // 64))
+
+    costliest = [max(cost(g, b, e) for g2, _, b, e in work if g2 == g) for g in seen]
+    assert costliest[0] == max(costliest)
 
 
 def test_generic_schedules_keep_64_row_groups():
@@ -309,7 +320,7 @@ def test_noalloc_attention_refuses_oversized_schedules_before_any_launch():
 
     lib = _native.lib()
     limit = int(lib.kvr_attention_scratch_limit())
-    assert limit == 64 << 20
+    assert limit == 128 << 20
     positions = list(range(8192, 8192 + 4096))
     s = schedule(positions, 12288, 32, 8, 128, chunk=64)
     buf = (ctypes.c_int32 * len(s))(*s)
